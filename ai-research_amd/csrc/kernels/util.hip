@@ -1,0 +1,111 @@
+// util.hip -- device-side synthetic-data generator and the bit-exact block
+// quantizer (src/quant.zig:20-90) for gfx950.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../common/quant_block.h"
+#include "../common/synth.h"
+
+// 8 consecutive elements per thread: one 32-byte (f32: 2 x 16 B) store run.
+extern "C" __global__ __launch_bounds__(256) void gh_synth_normal_f32_k(
+    float* dst, uint64_t n, uint64_t key, double mean, double stddev, uint64_t offset) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * 8;
+  for (uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; i < n; i += stride) {
+    if (i + 8 <= n) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = gh_normal_f32(key, offset + i + j, mean, stddev);
+      float4* p = reinterpret_cast<float4*>(dst + i);
+      if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+        p[0] = make_float4(v[0], v[1], v[2], v[3]);
+        p[1] = make_float4(v[4], v[5], v[6], v[7]);
+      } else {
+        for (int j = 0; j < 8; j++) dst[i + j] = v[j];
+      }
+    } else {
+      for (uint64_t j = i; j < n; j++) dst[j] = gh_normal_f32(key, offset + j, mean, stddev);
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void gh_synth_normal_bf16_k(
+    uint16_t* dst, uint64_t n, uint64_t key, double mean, double stddev, uint64_t offset) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x * 8;
+  for (uint64_t i = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; i < n; i += stride) {
+    if (i + 8 <= n && (reinterpret_cast<uintptr_t>(dst + i) & 15) == 0) {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        uint32_t lo = gh_bf16_rne(gh_normal_f32(key, offset + i + 2 * j, mean, stddev));
+        uint32_t hi = gh_bf16_rne(gh_normal_f32(key, offset + i + 2 * j + 1, mean, stddev));
+        w[j] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(dst + i) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      const uint64_t e = i + 8 < n ? i + 8 : n;
+      for (uint64_t j = i; j < e; j++)
+        dst[j] = gh_bf16_rne(gh_normal_f32(key, offset + j, mean, stddev));
+    }
+  }
+}
+
+// One thread per 32-element block.  src: bf16 [rows][cols], dst: blocks with
+// row stride ceil(cols/32) blocks (quant.zig:164-171); cols % 32 == 0.
+extern "C" __global__ __launch_bounds__(256) void gh_quantize_q4_k(
+    uint32_t* dst, const uint16_t* src, uint64_t rows, uint32_t cols) {
+  const uint32_t nb = cols >> 5;
+  const uint64_t total = rows * nb;
+  for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < total;
+       b += (uint64_t)gridDim.x * blockDim.x) {
+    uint16_t v[32];
+    const uint4* p = reinterpret_cast<const uint4*>(src + b * 32);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint4 t = p[j];
+      const uint32_t ww[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        v[8 * j + 2 * k] = (uint16_t)(ww[k] & 0xFFFFu);
+        v[8 * j + 2 * k + 1] = (uint16_t)(ww[k] >> 16);
+      }
+    }
+    uint32_t out[5];
+    gh_quantize_block_q4(v, out);
+    uint32_t* d = dst + b * 5;
+#pragma unroll
+    for (int j = 0; j < 5; j++) d[j] = out[j];
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void gh_quantize_q8_k(
+    uint32_t* dst, const uint16_t* src, uint64_t rows, uint32_t cols) {
+  const uint32_t nb = cols >> 5;
+  const uint64_t total = rows * nb;
+  for (uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; b < total;
+       b += (uint64_t)gridDim.x * blockDim.x) {
+    uint16_t v[32];
+    const uint4* p = reinterpret_cast<const uint4*>(src + b * 32);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint4 t = p[j];
+      const uint32_t ww[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        v[8 * j + 2 * k] = (uint16_t)(ww[k] & 0xFFFFu);
+        v[8 * j + 2 * k + 1] = (uint16_t)(ww[k] >> 16);
+      }
+    }
+    uint32_t out[9];
+    gh_quantize_block_q8(v, out);
+    uint32_t* d = dst + b * 9;
+#pragma unroll
+    for (int j = 0; j < 9; j++) d[j] = out[j];
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void gh_fill_u32_k(uint32_t* dst, uint32_t value,
+                                                                uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    dst[i] = value;
+}

@@ -1,0 +1,262 @@
+"""ctypes binding of libgemma_hip.so (include/gemma_hip.h).
+
+This mirrors the reference's GPU interface for Python callers (tests, bench):
+  Context      <- GpuContext / GpuEngine (src/gpu/context.zig, src/gpu/kernels.zig)
+  Buffer       <- GpuBuffer (src/gpu/buffer.zig)
+  Model        <- GpuModelContext + gpuDispatchForwardToken
+                  (src/gpu/model_gpu.zig, src/gpu/model_dispatch.zig)
+Every call goes through the C ABI; a non-zero status raises GhError with the
+library's message.  There is no fallback: without the built library or a
+gfx950 device the calls fail.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgemma_hip.so")
+
+QUANT_NONE, QUANT_Q8, QUANT_Q4 = 0, 1, 2
+
+_vp = C.c_void_p
+_sz = C.c_size_t
+_u32 = C.c_uint32
+_u64 = C.c_uint64
+_f32 = C.c_float
+_f64 = C.c_double
+_i = C.c_int
+
+# name -> (restype, argtypes); the single table of the ABI's signatures.
+_SIGS = {
+    "gh_device_count": (_i, []),
+    "gh_context_init": (_i, [C.c_char_p, C.POINTER(_vp)]),
+    "gh_context_deinit": (None, [_vp]),
+    "gh_context_device_name": (C.c_char_p, [_vp]),
+    "gh_last_error": (C.c_char_p, []),
+    "gh_sync": (_i, [_vp]),
+    "gh_buffer_alloc": (_i, [_vp, _sz, C.POINTER(_vp)]),
+    "gh_buffer_free": (_i, [_vp, _vp]),
+    "gh_buffer_write": (_i, [_vp, _vp, _vp, _sz]),
+    "gh_buffer_read": (_i, [_vp, _vp, _vp, _sz]),
+    "gh_buffer_copy": (_i, [_vp, _vp, _vp, _sz]),
+    "gh_buffer_fill_u32": (_i, [_vp, _vp, _u32, _sz]),
+    "gh_event_create": (_i, [_vp, C.POINTER(_vp)]),
+    "gh_event_record": (_i, [_vp, _vp]),
+    "gh_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f32)]),
+    "gh_event_destroy": (_i, [_vp]),
+    "gh_graph_begin": (_i, [_vp]),
+    "gh_graph_end": (_i, [_vp, C.POINTER(_vp)]),
+    "gh_graph_launch": (_i, [_vp, _vp]),
+    "gh_graph_destroy": (_i, [_vp]),
+    "gh_quantized_row_words": (_sz, [_sz, _i]),
+    "gh_quantized_size_bytes": (_sz, [_sz, _sz, _i]),
+    "gh_quantize_matrix": (_i, [_vp, _vp, _sz, _sz, _i, _i]),
+    "gh_quantize_matrix_dev": (_i, [_vp, _vp, _vp, _sz, _sz, _i]),
+    "gh_synth_normal_f32": (_i, [_vp, _sz, _u64, _u64, _f64, _f64, _u64]),
+    "gh_synth_normal_bf16": (_i, [_vp, _sz, _u64, _u64, _f64, _f64, _u64]),
+    "gh_synth_normal_f32_dev": (_i, [_vp, _vp, _sz, _u64, _u64, _f64, _f64, _u64]),
+    "gh_synth_normal_bf16_dev": (_i, [_vp, _vp, _sz, _u64, _u64, _f64, _f64, _u64]),
+    "gh_synth_uniform_u32": (_i, [_vp, _sz, _u64, _u64, _u32]),
+    "gh_gemv_q4": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
+    "gh_gemv_q8": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
+    "gh_gate_up_geglu_q4": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32]),
+}
+
+_lib = None
+
+
+class GhError(RuntimeError):
+    pass
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GhError("libgemma_hip.so is not built (run ai-research_amd/build.py)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def _check(st, what=""):
+    if st != 0:
+        msg = lib().gh_last_error().decode(errors="replace")
+        raise GhError("%s failed (status %d): %s" % (what, st, msg))
+
+
+def device_count():
+    return lib().gh_device_count()
+
+
+def _ptr(a):
+    return a.ctypes.data_as(_vp)
+
+
+# ---- host-side routines (no device needed) ---------------------------------
+def quantize_matrix(w_bf16, mode, nthreads=0):
+    """quantizeMatrix (src/quant.zig:92-162) on the host."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    rows, cols = w.shape
+    out = np.zeros((rows, lib().gh_quantized_row_words(cols, mode)), np.uint32)
+    _check(lib().gh_quantize_matrix(_ptr(out), _ptr(w), rows, cols, mode, nthreads),
+           "gh_quantize_matrix")
+    return out
+
+
+def synth_normal(n, seed, stream, mean=0.0, std=1.0, bf16=False, offset=0):
+    out = np.empty(n, np.uint16 if bf16 else np.float32)
+    fn = lib().gh_synth_normal_bf16 if bf16 else lib().gh_synth_normal_f32
+    _check(fn(_ptr(out), n, seed, stream, mean, std, offset), "gh_synth_normal")
+    return out
+
+
+def synth_uniform_u32(n, seed, stream, bound):
+    out = np.empty(n, np.uint32)
+    _check(lib().gh_synth_uniform_u32(_ptr(out), n, seed, stream, bound), "gh_synth_uniform_u32")
+    return out
+
+
+class Buffer:
+    """A device allocation (GpuBuffer, src/gpu/buffer.zig:13-53)."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = _vp()
+        _check(lib().gh_buffer_alloc(ctx.h, self.nbytes, C.byref(p)), "gh_buffer_alloc")
+        self.ptr = p.value
+
+    def write(self, arr, offset=0):
+        a = np.ascontiguousarray(arr)
+        assert offset + a.nbytes <= self.nbytes
+        _check(lib().gh_buffer_write(self.ctx.h, self.ptr + offset, _ptr(a), a.nbytes),
+               "gh_buffer_write")
+        return self
+
+    def read(self, dtype, count=None, offset=0):
+        dtype = np.dtype(dtype)
+        n = (self.nbytes - offset) // dtype.itemsize if count is None else int(count)
+        out = np.empty(n, dtype)
+        _check(lib().gh_buffer_read(self.ctx.h, _ptr(out), self.ptr + offset, out.nbytes),
+               "gh_buffer_read")
+        return out
+
+    def free(self):
+        if self.ptr:
+            _check(lib().gh_buffer_free(self.ctx.h, self.ptr), "gh_buffer_free")
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.ctx.h:
+                lib().gh_buffer_free(self.ctx.h, self.ptr)
+        except Exception:
+            pass
+
+
+class Context:
+    """GpuContext + GpuEngine: one gfx950 device, one in-order stream."""
+
+    def __init__(self, code_object_dir=None):
+        h = _vp()
+        d = code_object_dir.encode() if code_object_dir else None
+        _check(lib().gh_context_init(d, C.byref(h)), "gh_context_init")
+        self.h = h.value
+
+    @property
+    def device_name(self):
+        return lib().gh_context_device_name(self.h).decode()
+
+    def close(self):
+        if self.h:
+            lib().gh_context_deinit(self.h)
+            self.h = None
+
+    def sync(self):
+        _check(lib().gh_sync(self.h), "gh_sync")
+
+    # ---- memory
+    def alloc(self, nbytes):
+        return Buffer(self, nbytes)
+
+    def upload(self, arr):
+        a = np.ascontiguousarray(arr)
+        return Buffer(self, max(a.nbytes, 4)).write(a)
+
+    def copy(self, dst, src, nbytes, dst_off=0, src_off=0):
+        _check(lib().gh_buffer_copy(self.h, _addr(dst) + dst_off, _addr(src) + src_off, nbytes),
+               "gh_buffer_copy")
+
+    def fill_u32(self, buf, value, count):
+        _check(lib().gh_buffer_fill_u32(self.h, _addr(buf), value, count), "gh_buffer_fill_u32")
+
+    # ---- events
+    def event(self):
+        e = _vp()
+        _check(lib().gh_event_create(self.h, C.byref(e)), "gh_event_create")
+        return e.value
+
+    def record(self, ev):
+        _check(lib().gh_event_record(self.h, ev), "gh_event_record")
+
+    @staticmethod
+    def elapsed_ms(a, b):
+        ms = _f32()
+        _check(lib().gh_event_elapsed_ms(a, b, C.byref(ms)), "gh_event_elapsed_ms")
+        return ms.value
+
+    @staticmethod
+    def destroy_event(ev):
+        lib().gh_event_destroy(ev)
+
+    # ---- pre-recorded work (hipGraph capture of the context stream)
+    def graph_begin(self):
+        _check(lib().gh_graph_begin(self.h), "gh_graph_begin")
+
+    def graph_end(self):
+        g = _vp()
+        _check(lib().gh_graph_end(self.h, C.byref(g)), "gh_graph_end")
+        return g.value
+
+    def graph_launch(self, g):
+        _check(lib().gh_graph_launch(self.h, g), "gh_graph_launch")
+
+    @staticmethod
+    def graph_destroy(g):
+        lib().gh_graph_destroy(g)
+
+    # ---- quantization / synthetic data on the device
+    def quantize_dev(self, dst, src_bf16, rows, cols, mode):
+        _check(lib().gh_quantize_matrix_dev(self.h, _addr(dst), _addr(src_bf16), rows, cols, mode),
+               "gh_quantize_matrix_dev")
+
+    def synth_normal_dev(self, dst, n, seed, stream, mean=0.0, std=1.0, bf16=False, offset=0):
+        fn = lib().gh_synth_normal_bf16_dev if bf16 else lib().gh_synth_normal_f32_dev
+        _check(fn(self.h, _addr(dst), n, seed, stream, mean, std, offset), "gh_synth_normal_dev")
+
+    # ---- engine kernels (GpuEngine.record*)
+    def gemv_q4(self, W, X, Y, M, K):
+        _check(lib().gh_gemv_q4(self.h, _addr(W), _addr(X), _addr(Y), M, K), "gh_gemv_q4")
+
+    def gemv_q8(self, W, X, Y, M, K):
+        _check(lib().gh_gemv_q8(self.h, _addr(W), _addr(X), _addr(Y), M, K), "gh_gemv_q8")
+
+    def gate_up_geglu_q4(self, Wg, Wu, X, Y, M, K):
+        _check(lib().gh_gate_up_geglu_q4(self.h, _addr(Wg), _addr(Wu), _addr(X), _addr(Y), M, K),
+               "gh_gate_up_geglu_q4")
+
+
+def _addr(b):
+    if isinstance(b, Buffer):
+        return b.ptr
+    return int(b)

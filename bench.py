@@ -1,0 +1,226 @@
+"""Benchmark of the Q4_0 decode hot path on one MI355X.
+
+Headline workload (one "step"): the fused gate+up GeGLU MLP in Q4_0 at batch
+1 -- hidden 3840, intermediate 15360: act = gelu_tanh(Wg x) * (Wu x), then
+out = Wd act, fp32 accumulation, weights random N(0, 0.02) -> bf16 -> Q4_0.
+Weights are rotated over several distinct copies so every step streams its
+110.6 MB from HBM rather than from the 256 MB Infinity Cache.
+
+Printed as one JSON line: value = MLP HBM GB/s (algorithmic bytes / wall time
+of the K timed steps), plus the dominant kernel's roofline, the CPU baseline
+(the oracle's restatement of the reference CPU path, timed on this host) and
+secondary figures (single Q4_0 GEMV 8192 x 2048).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ai-research_amd"))
+
+import numpy as np  # noqa: E402
+
+import gemma_hip as gh  # noqa: E402
+
+METRIC = "Q4_0 GEMV/fused-MLP HBM GB/s (% peak); 12B-shape Q4_0 decode tokens/s"
+HBM_PEAK_GBS = 8000.0
+H, I = 3840, 15360
+Q4_ROW = lambda k: (k // 32) * 20  # noqa: E731  bytes per Q4_0 row (quant.zig:164-175)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_q4(ctx, rows, cols, seed, stream, staging):
+    """Random N(0, 0.02) weights drawn, rounded to bf16 and quantized on the device."""
+    ctx.synth_normal_dev(staging, rows * cols, seed, stream, 0.0, 0.02, bf16=True)
+    out = ctx.alloc(rows * Q4_ROW(cols))
+    ctx.quantize_dev(out, staging, rows, cols, gh.QUANT_Q4)
+    return out
+
+
+def bench_mlp(ctx, steps, warmup):
+    ncopy = 6  # 6 x 110.6 MB = 664 MB > 2.5 x the 256 MB Infinity Cache
+    staging = ctx.alloc(I * H * 2)
+    copies = []
+    for c in range(ncopy):
+        copies.append((make_q4(ctx, I, H, 0, 100 + 3 * c, staging),
+                       make_q4(ctx, I, H, 0, 101 + 3 * c, staging),
+                       make_q4(ctx, H, I, 0, 102 + 3 * c, staging)))
+    staging.free()
+    # x = RMSNorm(x_raw) * (1 + N(0, 0.1)), eps 1e-6 (input prep, not timed)
+    xr = gh.synth_normal(H, 0, 1, 0.0, 1.0).astype(np.float64)
+    w = gh.synth_normal(H, 0, 2, 1.0, 0.1).astype(np.float64)
+    x = (xr / np.sqrt(np.mean(xr * xr) + 1e-6) * w).astype(np.float32)
+    X, ACT, OUT = ctx.upload(x), ctx.alloc(I * 4), ctx.alloc(H * 4)
+
+    def step(i, evs=None):
+        wg, wu, wd = copies[i % ncopy]
+        if evs is not None:
+            ctx.record(evs[0])
+        ctx.gate_up_geglu_q4(wg, wu, X, ACT, I, H)
+        if evs is not None:
+            ctx.record(evs[1])
+        ctx.gemv_q4(wd, ACT, OUT, H, I)
+        if evs is not None:
+            ctx.record(evs[2])
+
+    for i in range(warmup):
+        step(i)
+    ctx.sync()
+    # timed region: the K steps launched back to back on the context stream,
+    # an event on each side of every kernel (same stream) for the roofline.
+    evs = [[ctx.event() for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, evs[i])
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    gu_ms = [ctx.elapsed_ms(e[0], e[1]) for e in evs]
+    dn_ms = [ctx.elapsed_ms(e[1], e[2]) for e in evs]
+    gpu_ms = ctx.elapsed_ms(evs[0][0], evs[-1][2])
+    for e in evs:
+        for v in e:
+            ctx.destroy_event(v)
+    # the same K steps recorded once and replayed as one graph (how the decode
+    # step runs); reported beside the direct launches
+    ctx.graph_begin()
+    for i in range(steps):
+        step(i)
+    g = ctx.graph_end()
+    ctx.graph_launch(g)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    ctx.graph_launch(g)
+    ctx.record(e1)
+    graph_ms = ctx.elapsed_ms(e0, e1)
+    ctx.graph_destroy(g)
+    out = OUT.read(np.float32, H)
+    assert np.all(np.isfinite(out))
+    host_w = [b.read(np.uint32) for b in copies[0]]
+    return wall, float(np.mean(gu_ms)), float(np.mean(dn_ms)), gpu_ms, graph_ms, x, host_w
+
+
+def bench_gemv(ctx, reps=256):
+    """Single Q4_0 GEMV, 8192 x 2048, rotated over 64 weight copies (671 MB)."""
+    M, K, ncopy = 8192, 2048, 64
+    staging = ctx.alloc(M * K * 2)
+    ws = [make_q4(ctx, M, K, 0, 500 + c, staging) for c in range(ncopy)]
+    staging.free()
+    X = ctx.upload(gh.synth_normal(K, 0, 3, 0.0, 1.0))
+    Y = ctx.alloc(M * 4)
+    for i in range(ncopy):
+        ctx.gemv_q4(ws[i], X, Y, M, K)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.graph_begin()
+    for i in range(reps):
+        ctx.gemv_q4(ws[i % ncopy], X, Y, M, K)
+    g = ctx.graph_end()
+    ctx.graph_launch(g)
+    ctx.sync()
+    ctx.record(e0)
+    ctx.graph_launch(g)
+    ctx.record(e1)
+    ms = ctx.elapsed_ms(e0, e1) / reps
+    ctx.graph_destroy(g)
+    nbytes = M * Q4_ROW(K) + K * 4 + M * 4
+    return nbytes / (ms * 1e-3) / 1e9, ms * 1e3
+
+
+def cpu_baseline(x, host_w, budget_s=10.0):
+    """The oracle's restatement of the reference CPU path (src/test_q4_exec.zig
+    dequant loop inside gatedMlp's 16-job row split, src/kernels.zig:100-129)
+    timed on this host over whole MLP steps."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    nt = max(1, min(16, os.cpu_count() or 1))
+    wg, wu, wd = (w.reshape(r, -1) for w, r in zip(host_w, (I, I, H)))
+    orc.gated_mlp_q4(x, wg, wu, wd, nt)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        orc.gated_mlp_q4(x, wg, wu, wd, nt)
+        n += 1
+    dt = time.perf_counter() - t0
+    return n, dt, nt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: the decode backend has no multi-GPU path "
+              "(--gpus %d requested)" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    ctx = gh.Context()
+    log("device:", ctx.device_name)
+    wall, gu_ms, dn_ms, gpu_ms, graph_ms, x, host_w = bench_mlp(ctx, args.steps, args.warmup)
+    gu_bytes = 2 * I * Q4_ROW(H) + H * 4 + I * 4
+    dn_bytes = H * Q4_ROW(I) + I * 4 + H * 4
+    step_bytes = gu_bytes + dn_bytes
+    value = step_bytes * args.steps / wall / 1e9
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    gemv_gbs, gemv_us = bench_gemv(ctx)
+    log("mlp %.1f GB/s, gate_up %.2f us, down %.2f us, gemv8192x2048 %.2f us"
+        % (value, gu_ms * 1e3, dn_ms * 1e3, gemv_us))
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("gh_gateup_q4", None)
+
+    cpu = None
+    if not args.no_cpu:
+        n, dt, nt = cpu_baseline(x, host_w)
+        cpu = {"value": round(step_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": nt,
+               "kind": "port",
+               "sample": "%d full MLP steps (3840/15360 Q4_0, copy 0 of the weights) in %.1f s "
+                         "with the oracle's 16-way row split" % (n, dt)}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "fused gate+up GeGLU + down projection, Q4_0, batch 1",
+                   "hidden": H, "intermediate": I, "weight_copies_rotated": 6,
+                   "bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "gh_gateup_q4",
+                     "avg_launch_us": round(gu_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "extra": {"mlp_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
+                  "mlp_gbs_event_timed": round(step_bytes * args.steps / (gpu_ms * 1e-3) / 1e9, 1),
+                  "mlp_gbs_graph_replay": round(step_bytes * args.steps / (graph_ms * 1e-3) / 1e9, 1),
+                  "down_proj_us": round(dn_ms * 1e3, 3),
+                  "down_proj_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
+                  "gemv_q4_8192x2048_gbs": round(gemv_gbs, 1),
+                  "gemv_q4_8192x2048_us": round(gemv_us, 3)},
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+/*
+ * gemma_hip.h -- C ABI of the MI355X (gfx950) decode backend.
+ *
+ * This is the drop-in boundary for the Vulkan backend of Sullux/ai-research
+ * (src/gpu.zig, the src/gpu/ directory and the WGSL shaders under shaders/).
+ * A Zig host binds it with
+ * @cImport; every entry point names the reference interface it replaces.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  "dev" pointers are device (HBM)
+ *    addresses, from gh_buffer_alloc or any HIP allocator on the same device.
+ *  - Every call returns gh_status; GH_OK is 0.  Nothing is swallowed (the
+ *    reference returns token 0 on a failed submit, model_dispatch.zig:145).
+ *    gh_last_error() gives the message of the calling thread's last failure.
+ *  - Kernel entry points (gh_gemv_*, ...) are enqueued on the context's single
+ *    in-order stream and return at once, like recording into the reference's
+ *    command buffer; gh_sync waits, like submitPreRecorded (kernels.zig:147).
+ *  - Weight layouts are the reference's, unchanged (src/quant.zig):
+ *      Q4_0 row = ceil(K/32) blocks x 5 u32  {f32 d, 4 words of 8 nibbles}
+ *      Q8_0 row = ceil(K/32) blocks x 9 u32  {f32 d, 8 words of 4 int8}
+ *    KV caches are [slot][kv_heads*head_dim] f32 per layer, slots numbered as
+ *    src/ring_buffer.zig numbers them ([anchors | window | recall]).
+ */
+#ifndef GEMMA_HIP_H
+#define GEMMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum gh_status {
+  GH_OK = 0,
+  GH_ERR_NO_DEVICE = 1,      /* NoVulkanDevices / NoComputeDeviceFound (context.zig:24-68) */
+  GH_ERR_CODE_OBJECT = 2,    /* a gfx950 code object failed to load */
+  GH_ERR_ALLOC = 3,          /* device or host allocation failed (buffer.zig:20-44) */
+  GH_ERR_INVALID = 4,        /* bad argument (null pointer, zero size, ...) */
+  GH_ERR_UNSUPPORTED = 5,    /* shape outside what the kernels handle */
+  GH_ERR_HIP = 6             /* a HIP runtime call failed (launch, copy, sync) */
+} gh_status;
+
+/* QuantMode (src/quant.zig:3-13). */
+typedef enum gh_quant_mode { GH_QUANT_NONE = 0, GH_QUANT_Q8 = 1, GH_QUANT_Q4 = 2 } gh_quant_mode;
+
+typedef struct gh_context gh_context;
+
+/* ---- context: GpuContext (src/gpu/context.zig:13-104) -------------------- */
+/* Number of visible HIP devices (0 when none); never fails. */
+int gh_device_count(void);
+/* GpuContext.init (context.zig:17): picks device 0, loads the gfx950 code
+ * objects from code_object_dir (NULL = the directory holding this library). */
+gh_status gh_context_init(const char *code_object_dir, gh_context **out);
+/* GpuContext.deinit (context.zig:104). */
+void gh_context_deinit(gh_context *ctx);
+/* GpuContext.device_name (context.zig:15). */
+const char *gh_context_device_name(const gh_context *ctx);
+const char *gh_last_error(void);
+/* Waits for all work enqueued on the context (submitPreRecorded's fence wait,
+ * src/gpu/kernels.zig:147-157). */
+gh_status gh_sync(gh_context *ctx);
+
+/* ---- buffers: GpuBuffer (src/gpu/buffer.zig:13-53) ------------------------ */
+/* GpuBuffer.init: 256-byte aligned device memory. */
+gh_status gh_buffer_alloc(gh_context *ctx, size_t bytes, void **dev);
+/* GpuBuffer.deinit. */
+gh_status gh_buffer_free(gh_context *ctx, void *dev);
+/* The reference writes through a mapped pointer (asSlice); here copies are
+ * explicit and synchronous with the context stream. */
+gh_status gh_buffer_write(gh_context *ctx, void *dev_dst, const void *host_src, size_t bytes);
+gh_status gh_buffer_read(gh_context *ctx, void *host_dst, const void *dev_src, size_t bytes);
+gh_status gh_buffer_copy(gh_context *ctx, void *dev_dst, const void *dev_src, size_t bytes);
+gh_status gh_buffer_fill_u32(gh_context *ctx, void *dev, uint32_t value, size_t count);
+
+/* ---- timing on the context stream (no reference counterpart: the reference
+ * times with host clocks, src/model/bench.zig:14-21) ------------------------ */
+gh_status gh_event_create(gh_context *ctx, void **ev);
+gh_status gh_event_record(gh_context *ctx, void *ev);
+gh_status gh_event_elapsed_ms(void *ev_start, void *ev_end, float *ms);
+gh_status gh_event_destroy(void *ev);
+
+/* ---- pre-recorded work: recordForwardGraph + submitPreRecorded
+ * (src/gpu/model_dispatch.zig:103-129, src/gpu/kernels.zig:147-157).  Work
+ * enqueued on the context between begin and end is captured into a HIP graph
+ * instead of running; gh_graph_launch replays it on the context stream. ---- */
+gh_status gh_graph_begin(gh_context *ctx);
+gh_status gh_graph_end(gh_context *ctx, void **graph);
+gh_status gh_graph_launch(gh_context *ctx, void *graph);
+gh_status gh_graph_destroy(void *graph);
+
+/* ---- quantization: src/quant.zig ------------------------------------------ */
+/* getQuantizedRowWords (quant.zig:164-171). */
+size_t gh_quantized_row_words(size_t cols, gh_quant_mode mode);
+/* getQuantizedSizeBytes (quant.zig:173-175). */
+size_t gh_quantized_size_bytes(size_t rows, size_t cols, gh_quant_mode mode);
+/* quantizeMatrix (quant.zig:92-162) on the host, nthreads <= 0 means 16. */
+gh_status gh_quantize_matrix(uint32_t *dst, const uint16_t *src_bf16, size_t rows,
+                             size_t cols, gh_quant_mode mode, int nthreads);
+/* quantizeMatrix on the device: bf16 [rows][cols] in HBM -> blocks in HBM,
+ * byte-identical to the host routine.  cols % 32 == 0. */
+gh_status gh_quantize_matrix_dev(gh_context *ctx, void *dst_dev, const void *src_bf16_dev,
+                                 size_t rows, size_t cols, gh_quant_mode mode);
+
+/* ---- synthetic inputs (no reference counterpart) --------------------------
+ * Deterministic N(mean, std) draws: element i of (seed, stream) has the same
+ * bits on the host and on the device.  Used for random-init weights and
+ * inputs; bf16 variants round with src/tensor.zig's RNE. */
+gh_status gh_synth_normal_f32(float *dst, size_t n, uint64_t seed, uint64_t stream,
+                              double mean, double stddev, uint64_t offset);
+gh_status gh_synth_normal_bf16(uint16_t *dst, size_t n, uint64_t seed, uint64_t stream,
+                               double mean, double stddev, uint64_t offset);
+gh_status gh_synth_normal_f32_dev(gh_context *ctx, float *dst_dev, size_t n, uint64_t seed,
+                                  uint64_t stream, double mean, double stddev, uint64_t offset);
+gh_status gh_synth_normal_bf16_dev(gh_context *ctx, uint16_t *dst_dev, size_t n, uint64_t seed,
+                                   uint64_t stream, double mean, double stddev, uint64_t offset);
+gh_status gh_synth_uniform_u32(uint32_t *dst, size_t n, uint64_t seed, uint64_t stream,
+                               uint32_t bound);
+
+/* ---- engine kernels: GpuEngine.record* (src/gpu/kernels.zig:80-142) ------ */
+/* recordGemv (kernels.zig:80-83), shaders/gemv_q4.wgsl: Y[M] = deq(W)[M x K] . X[K].
+ * K % 128 == 0 (the reference's 4-block unroll), W 16-byte aligned. */
+gh_status gh_gemv_q4(gh_context *ctx, const void *W, const float *X, float *Y,
+                     uint32_t M, uint32_t K);
+/* recordGemvLogits / Q8 pipeline (kernels.zig:88-91), shaders/gemv_q8.wgsl. */
+gh_status gh_gemv_q8(gh_context *ctx, const void *W, const float *X, float *Y,
+                     uint32_t M, uint32_t K);
+/* recordGateUpSwiGlu (kernels.zig:92-95), shaders/fused_mlp_q4.wgsl:
+ * Y[r] = gelu_tanh(Wg[r] . X) * (Wu[r] . X) for r < M. */
+gh_status gh_gate_up_geglu_q4(gh_context *ctx, const void *Wg, const void *Wu,
+                              const float *X, float *Y, uint32_t M, uint32_t K);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,138 @@
+/*
+ * oracle.h -- CPU restatement of the reference's decode math (TEST INFRASTRUCTURE).
+ *
+ * This library is the checker, never the product.  Only tests/, the smoke()
+ * entry of __graft_entry__.py and the cpu_baseline leg of bench.py may load it.
+ * The product path (ai-research_amd/) never links or calls it.
+ *
+ * Every function restates one piece of the reference (Sullux/ai-research, Zig)
+ * and cites the file:line it follows.  The reference itself is Zig and cannot
+ * be built here (no zig toolchain), so there is no oracle/_ref build; the
+ * restatement is pinned instead by known answers, invariants and an
+ * independent numpy restatement (tests/test_oracle_*.py).
+ *
+ * Parity status per function (what pins it):
+ *   orc_bf16_*                 pinned: tensor.zig:30-41 KAT + RNE tie cases
+ *   orc_quantize_row_q4_0/q8_0 pinned: hand-derived known answers, invariants,
+ *                              independent numpy restatement (bit-exact)
+ *   orc_gemv_q4 / q8 / bf16    pinned: kernels.zig:176-183 KAT, constant-weight
+ *                              closed form, fp64 brute force
+ *   orc_rmsnorm / unit         pinned: closed form (output RMS = 1)
+ *   orc_gelu_tanh              pinned: fp64 closed form (tolerance only; the
+ *                              reference's std.math.tanh is ulp-level unpinned)
+ *   orc_rope_partial           pinned: pos 0 identity, pair norms, angle
+ *                              additivity, suffix pass-through
+ *   orc_softmax / orc_argmax   pinned: sum to 1; lowest index on ties
+ *   orc_ring_*                 pinned: ring_buffer.zig:149-187 KATs + wraparound
+ *   orc_attention              pinned: equal scores -> mean(V), S=1 -> V,
+ *                              dominant score -> that V, fp64 brute force
+ *   orc_forward_token          pinned by composition of the above plus an
+ *                              fp64 numpy restatement of the layer op order
+ */
+#ifndef ORACLE_H
+#define ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- bf16 (src/tensor.zig:7-18) ---------------------------------------- */
+uint16_t orc_bf16_from_f32(float v);
+float orc_bf16_to_f32(uint16_t b);
+void orc_bf16_from_f32_n(const float *src, uint16_t *dst, size_t n);
+
+/* ---- quantizers (src/quant.zig) ----------------------------------------- */
+enum { ORC_QUANT_NONE = 0, ORC_QUANT_Q8 = 1, ORC_QUANT_Q4 = 2 };
+void orc_quantize_row_q8_0(uint32_t *dst, const uint16_t *src, size_t n);
+void orc_quantize_row_q4_0(uint32_t *dst, const uint16_t *src, size_t n);
+size_t orc_quantized_row_words(size_t cols, int mode);
+size_t orc_quantized_size_bytes(size_t rows, size_t cols, int mode);
+void orc_quantize_matrix(uint32_t *dst, const uint16_t *src, size_t rows,
+                         size_t cols, int mode, int nthreads);
+
+/* ---- GEMVs -------------------------------------------------------------- */
+void orc_gemv_q4(const uint32_t *w, const float *x, float *y, size_t rows,
+                 size_t cols, int nthreads);
+void orc_gemv_q8(const uint32_t *w, const float *x, float *y, size_t rows,
+                 size_t cols, int nthreads);
+void orc_gemv_bf16(const uint16_t *w, const float *x, float *y, size_t rows,
+                   size_t cols);
+
+/* ---- elementwise / reductions (src/kernels.zig) ------------------------- */
+float orc_dot_f32(const float *a, const float *b, size_t n);
+void orc_rmsnorm(float *out, const float *in, const float *w, size_t n, float eps);
+void orc_unit_rmsnorm(float *out, const float *in, size_t n, float eps);
+float orc_gelu_tanh(float x);
+void orc_gate_up_geglu_q4(float *act, const float *x, const uint32_t *wg,
+                          const uint32_t *wu, size_t inter, size_t h, int nthreads);
+void orc_gated_mlp_q4(float *out, float *act, const float *x,
+                      const uint32_t *wg, const uint32_t *wu, const uint32_t *wd,
+                      size_t h, size_t inter, int nthreads);
+void orc_rope_partial(float *vec, size_t len, size_t pos, size_t head_dim,
+                      size_t rotary_dim, float theta);
+void orc_softmax(float *v, size_t n);
+uint32_t orc_argmax(const float *v, size_t n);
+
+/* ---- ring buffer (src/ring_buffer.zig) ---------------------------------- */
+typedef struct orc_ring {
+  size_t num_layers, max_kv_dim, num_anchors, window_size, num_recall, total_slots;
+  float *k, *v;
+  uint64_t *clocks;
+  uint8_t *active;
+  uint64_t total_ingested;
+} orc_ring;
+int orc_ring_init(orc_ring *r, size_t num_layers, size_t max_kv_dim,
+                  size_t num_anchors, size_t window_size, size_t num_recall);
+void orc_ring_deinit(orc_ring *r);
+size_t orc_ring_slot_index(const orc_ring *r, uint64_t clock);
+size_t orc_ring_activate_slot(orc_ring *r, size_t layer, uint64_t clock);
+void orc_ring_write_kv(orc_ring *r, size_t layer, uint64_t clock,
+                       const float *k, const float *v, size_t len);
+void orc_ring_clear_recall(orc_ring *r);
+void orc_ring_write_recall_kv(orc_ring *r, size_t layer, size_t rank,
+                              const float *k, const float *v, size_t len, uint64_t clock);
+size_t orc_ring_active_slots(const orc_ring *r, size_t layer, uint64_t clock,
+                             uint32_t *out);
+
+/* ---- attention pieces (src/model/forward.zig) --------------------------- */
+void orc_qkv_norm_rope(float *q, float *k, float *v, const float *q_norm,
+                       const float *k_norm, size_t nq, size_t nkv, size_t head_dim,
+                       size_t rotary_dim, int k_eq_v, float theta, float eps,
+                       uint64_t clock);
+void orc_attention(const float *q, const float *k_cache, const float *v_cache,
+                   size_t slot_stride, const uint32_t *active, size_t n_active,
+                   size_t nq, size_t nkv, size_t head_dim, float *out);
+
+/* ---- one decode step (src/gpu/model_dispatch.zig op order) -------------- */
+typedef struct orc_layer {
+  int full_attention;
+  size_t head_dim, rotary_dim, num_kv_heads;
+  int k_eq_v;
+  const float *input_norm, *q_norm, *k_norm, *post_attn_norm, *pre_ffn_norm,
+      *post_ffn_norm; /* post_* may be NULL */
+  float layer_scalar;
+  const uint32_t *wq, *wk, *wv, *wo, *wg, *wu, *wd; /* Q4_0 (or Q8_0) rows */
+  float *k_cache, *v_cache; /* [total_slots][num_kv_heads*head_dim] */
+} orc_layer;
+
+typedef struct orc_model {
+  size_t hidden, intermediate, vocab, num_q_heads, num_layers;
+  int layer_mode; /* ORC_QUANT_Q4 or ORC_QUANT_Q8 */
+  float eps, rope_theta, rope_theta_full;
+  const uint32_t *lm_head_q8;
+  const float *final_norm;
+  const orc_layer *layers;
+} orc_model;
+
+void orc_embed(const uint16_t *embed_bf16, uint32_t token, size_t hidden, float *x);
+uint32_t orc_forward_token(const orc_model *m, float *x, uint64_t clock,
+                           size_t slot_idx, const uint32_t *active, size_t n_active,
+                           int want_logits, float *logits, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,284 @@
+"""Pins the C oracle (oracle/liboracle.so) before anything is checked against it.
+
+Each test names what fixes the answer: a known-answer test the reference's own
+suite holds, a hand-derived value, a closed form / invariant, or the
+independent numpy restatement in tests/numpy_ref.py.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+import numpy_ref as nr
+import oracle as orc
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---------------------------------------------------------------- bf16 ----
+def test_bf16_roundtrip_reference_kat():
+    # src/tensor.zig:30-41
+    assert abs(orc.bf16_to_f32(orc.bf16_from_f32(np.float32(3.1415926)))[()] - 3.1415926) < 0.02
+    assert orc.bf16_to_f32(orc.bf16_from_f32(np.float32(0.0)))[()] == 0.0
+    assert abs(orc.bf16_to_f32(orc.bf16_from_f32(np.float32(-42.5)))[()] + 42.5) < 0.1
+
+
+def test_bf16_rne_ties():
+    # 0x3F808000 is exactly half-way between 0x3F80 and 0x3F81: ties to even.
+    v = np.array([0x3F808000, 0x3F818000, 0x3F80FFFF, 0x3F807FFF, 0xBF808000], np.uint32).view(np.float32)
+    got = orc.bf16_from_f32(v)
+    assert list(got) == [0x3F80, 0x3F82, 0x3F81, 0x3F80, 0xBF80]
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(100000).astype(np.float32) * 10
+    assert np.array_equal(orc.bf16_from_f32(x), nr.bf16_rne(x))
+
+
+# ------------------------------------------------------------ quantizers ----
+def test_q4_known_answers():
+    ones = np.full((1, 32), 0x3F80, np.uint16)  # bf16 1.0
+    q = orc.quantize_q4(ones)
+    assert q[0, 0] == 0x3E124925  # f32 bits of 1/7
+    assert list(q[0, 1:]) == [0xFFFFFFFF] * 4  # nibble 15 = 7 + 8
+    zeros = np.zeros((1, 32), np.uint16)
+    q = orc.quantize_q4(zeros)
+    assert q[0, 0] == 0 and list(q[0, 1:]) == [0x88888888] * 4
+    # amax 7 -> d = 1, id = 1: values round half away from zero
+    v = np.array([7, -7, 3.5, -3.5, 0.5, -0.5, 1.5, -1.5] * 4, np.float32)
+    q = orc.quantize_q4(nr.bf16_rne(v)[None, :])
+    assert q[0, 0] == np.float32(1.0).view(np.uint32)
+    # nibbles 15, 1, 12, 4, 9, 7, 10, 6 packed sequentially from bit 0
+    want = 15 | (1 << 4) | (12 << 8) | (4 << 12) | (9 << 16) | (7 << 20) | (10 << 24) | (6 << 28)
+    assert list(q[0, 1:]) == [want] * 4
+
+
+def test_q8_known_answers():
+    ones = np.full((1, 32), 0x3F80, np.uint16)
+    q = orc.quantize_q8(ones)
+    assert q[0, 0] == np.float32(np.float32(1.0) / np.float32(127.0)).view(np.uint32)
+    assert list(q[0, 1:]) == [0x7F7F7F7F] * 8
+    q = orc.quantize_q8(np.zeros((1, 32), np.uint16))
+    assert list(q[0]) == [0] * 9
+    v = np.array([127, -127, 0.5, -0.5] * 8, np.float32)
+    q = orc.quantize_q8(nr.bf16_rne(v)[None, :])
+    # bytes 0x7F, 0x81 (-127), 0x01, 0xFF (-1) little-endian in one word
+    assert list(q[0, 1:]) == [0xFF01817F] * 8
+
+
+def test_quant_matches_numpy_fixtures():
+    f = np.load(os.path.join(GOLD, "quant_fixtures.npz"))
+    assert np.array_equal(orc.bf16_from_f32(f["w_f32"]), f["w_bf16"])
+    assert np.array_equal(orc.quantize_q4(f["w_bf16"]), f["q4"])
+    assert np.array_equal(orc.quantize_q8(f["w_bf16"]), f["q8"])
+
+
+def test_quant_random_rows_match_numpy_and_threads():
+    rng = np.random.default_rng(11)
+    w = nr.bf16_rne(rng.standard_normal((300, 3840)).astype(np.float32) * 0.02)
+    q4 = orc.quantize_q4(w)
+    assert np.array_equal(q4, nr.quantize_q4(w))
+    assert np.array_equal(orc.quantize_q4(w, nthreads=8), q4)  # threading never changes bytes
+    q8 = orc.quantize_q8(w)
+    assert np.array_equal(q8, nr.quantize_q8(w))
+    assert np.array_equal(orc.quantize_q8(w, nthreads=8), q8)
+
+
+def test_quant_invariants():
+    rng = np.random.default_rng(3)
+    wf = rng.standard_normal((64, 256)).astype(np.float32) * 0.02
+    w = nr.bf16_rne(wf)
+    wn = w ^ np.uint16(0x8000)  # exact negation in bf16
+    q, qn = orc.quantize_q4(w), orc.quantize_q4(wn)
+    shifts = np.arange(8, dtype=np.uint64) * 4
+    nib = lambda a: ((a.reshape(64, 8, 5)[:, :, 1:].astype(np.uint64)[..., None] >> shifts) & 0xF)
+    n, nn = nib(q), nib(qn)
+    assert np.all(n >= 1) and np.all(n <= 15)  # nibble 0 never occurs
+    assert np.array_equal(nn, 16 - n)  # negation maps n -> 16 - n
+    # |w - deq(w)| <= d/2 (+ a few ulps)
+    deq = nr.dequant_q4(q, 256)
+    d = np.repeat(q.reshape(64, 8, 5)[:, :, 0].view(np.float32), 32, axis=1).astype(np.float64)
+    err = np.abs(deq - nr.bf16_to_f32(w).astype(np.float64))
+    assert np.all(err <= d * 0.5 * (1 + 1e-5) + 1e-12)
+    q8, q8n = orc.quantize_q8(w), orc.quantize_q8(wn)
+    b = q8.reshape(64, 8, 9)[:, :, 1:].copy().view(np.int8)
+    bn = q8n.reshape(64, 8, 9)[:, :, 1:].copy().view(np.int8)
+    assert np.all(b != -128)
+    assert np.array_equal(bn.astype(np.int32), -b.astype(np.int32))
+
+
+# ------------------------------------------------------------------ GEMV ----
+def test_gemv_bf16_reference_kat():
+    # src/kernels.zig:176-183: [[1,2],[3,4]] . [1,2] = [5, 11]
+    w = nr.bf16_rne(np.array([[1, 2], [3, 4]], np.float32))
+    y = orc.gemv_bf16(w, np.array([1, 2], np.float32))
+    assert abs(y[0] - 5) < 0.01 and abs(y[1] - 11) < 0.01
+
+
+def test_gemv_q4_constant_weight_closed_form():
+    # all-ones weights: every dequantized weight is (15-8) * f32(1/7)
+    w = np.full((8, 128), 0x3F80, np.uint16)
+    x = (np.arange(128) % 5).astype(np.float32) * 0.25  # src/gpu.zig:43 input
+    y = orc.gemv_q4(orc.quantize_q4(w), x, 128)
+    wv = np.float64(np.float32(7.0) * np.float32(np.float32(1.0) / np.float32(7.0)))
+    assert np.allclose(y, wv * x.astype(np.float64).sum(), rtol=1e-6)
+    assert np.all(y > 0)  # src/gpu.zig:58
+
+
+@pytest.mark.parametrize("mode", ["q4", "q8"])
+def test_gemv_matches_fp64_brute_force(mode):
+    rng = np.random.default_rng(5)
+    M, K = 256, 3840
+    w = nr.bf16_rne(rng.standard_normal((M, K)).astype(np.float32) * 0.02)
+    x = rng.standard_normal(K).astype(np.float32)
+    if mode == "q4":
+        wq = orc.quantize_q4(w)
+        y = orc.gemv_q4(wq, x, K, nthreads=4)
+        ref = nr.dequant_q4(wq, K) @ x.astype(np.float64)
+    else:
+        wq = orc.quantize_q8(w)
+        y = orc.gemv_q8(wq, x, K, nthreads=4)
+        ref = nr.dequant_q8(wq, K) @ x.astype(np.float64)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-5
+
+
+# --------------------------------------------------------------- norms -----
+def test_rmsnorm_closed_form():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(3840).astype(np.float32) * 3
+    y = orc.rmsnorm(x, np.ones(3840, np.float32))
+    assert abs(np.sqrt(np.mean(y.astype(np.float64) ** 2)) - 1) < 1e-5
+    w = (1 + rng.standard_normal(3840) * 0.1).astype(np.float32)
+    assert np.allclose(orc.rmsnorm(x, w), nr.rmsnorm64(x, w), rtol=1e-5, atol=1e-6)
+    u = orc.unit_rmsnorm(x)
+    assert abs(np.sqrt(np.mean(u.astype(np.float64) ** 2)) - 1) < 1e-5
+    # the norm of an all-zero vector stays zero (eps keeps it finite)
+    assert np.all(orc.rmsnorm(np.zeros(16, np.float32), np.ones(16, np.float32)) == 0)
+
+
+def test_gelu_tanh():
+    xs = np.linspace(-8, 8, 161).astype(np.float32)
+    got = np.array([orc.gelu_tanh(v) for v in xs])
+    assert np.allclose(got, nr.gelu64(xs), rtol=2e-6, atol=1e-7)
+    assert orc.gelu_tanh(0.0) == 0.0
+    assert abs(orc.gelu_tanh(20.0) - 20.0) < 1e-5 and abs(orc.gelu_tanh(-20.0)) < 1e-5
+
+
+# ---------------------------------------------------------------- RoPE -----
+def test_rope_properties():
+    rng = np.random.default_rng(21)
+    hd, rot, theta = 256, 64, 10000.0
+    v = rng.standard_normal(2 * hd).astype(np.float32)
+    assert np.array_equal(orc.rope_partial(v, 0, hd, rot, theta), v)  # pos 0 is identity
+    r = orc.rope_partial(v, 1234, hd, rot, theta)
+    vh, rh = v.reshape(2, hd), r.reshape(2, hd)
+    assert np.array_equal(rh[:, rot:], vh[:, rot:])  # suffix passes through
+    n0 = vh[:, :32] ** 2 + vh[:, 32:64] ** 2
+    n1 = rh[:, :32] ** 2 + rh[:, 32:64] ** 2
+    assert np.allclose(n0, n1, rtol=1e-5)  # each (i, i+rot/2) pair keeps its norm
+    assert np.allclose(r, nr.rope64(v, 1234, hd, rot, theta), atol=5e-4)
+    # angle additivity R(a) R(b) = R(a + b)
+    ab = orc.rope_partial(orc.rope_partial(v, 3, hd, rot, theta), 5, hd, rot, theta)
+    assert np.allclose(ab, orc.rope_partial(v, 8, hd, rot, theta), atol=1e-5)
+    # full rotation (sliding layers): rot = head_dim
+    assert np.allclose(orc.rope_partial(v, 77, hd, hd, theta), nr.rope64(v, 77, hd, hd, theta), atol=5e-5)
+
+
+# ------------------------------------------------------- softmax / argmax --
+def test_softmax_and_argmax():
+    rng = np.random.default_rng(2)
+    s = rng.standard_normal(640).astype(np.float32) * 16
+    p = orc.softmax(s)
+    assert abs(p.astype(np.float64).sum() - 1) < 1e-5 and np.all(p >= 0)
+    v = np.array([1, 5, 3, 5, 2], np.float32)
+    assert orc.argmax(v) == 1  # ties go to the lowest index
+    assert orc.argmax(np.zeros(100, np.float32)) == 0
+    w = rng.standard_normal(262144).astype(np.float32)
+    assert orc.argmax(w) == int(np.argmax(w))
+
+
+# ---------------------------------------------------------------- ring -----
+def test_ring_tiers_and_window_eviction():
+    # src/ring_buffer.zig:149-166
+    r = orc.Ring(2, 64, 4, 8, 4)
+    assert r.total_slots == 16
+    k, v = np.ones(64, np.float32), np.full(64, 2.0, np.float32)
+    for c in range(20):
+        r.write_kv(0, c, k, v)
+    s = r.active_slots(0, 19)
+    assert len(s) == 12 and s[0] == 0 and s[3] == 3
+
+
+def test_ring_recall_slots():
+    # src/ring_buffer.zig:168-187
+    r = orc.Ring(1, 8, 2, 4, 3)
+    k, v = np.ones(8, np.float32), np.full(8, 2.0, np.float32)
+    r.write_recall_kv(0, 0, k, v, 100)
+    r.write_recall_kv(0, 1, k, v, 50)
+    assert len(r.active_slots(0, 101)) == 2
+    r.clear_recall()
+    assert len(r.active_slots(0, 101)) == 0
+
+
+def test_ring_wraparound():
+    r = orc.Ring(1, 4, 32, 512, 96)
+    assert r.slot_index(0) == 0 and r.slot_index(31) == 31
+    assert r.slot_index(32) == 32 and r.slot_index(543) == 543
+    assert r.slot_index(544) == 32 and r.slot_index(1000) == 32 + (1000 - 32) % 512
+    for c in range(600):
+        r.activate_slot(0, c)
+    s = r.active_slots(0, 599)
+    # 32 anchors + the 512 newest window clocks (88..599)
+    assert len(s) == 544 and list(s[:32]) == list(range(32))
+    assert sorted(s[32:]) == list(range(32, 544))
+
+
+# ----------------------------------------------------------- attention -----
+def test_attention_closed_forms():
+    rng = np.random.default_rng(4)
+    nq, nkv, hd, S = 4, 2, 64, 10
+    kc = rng.standard_normal((S, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((S, nkv * hd)).astype(np.float32)
+    act = np.arange(S, dtype=np.uint32)
+    # equal scores -> mean of V
+    out = orc.attention(np.zeros(nq * hd, np.float32), kc, vc, act, nq, nkv, hd).reshape(nq, hd)
+    mean = vc.reshape(S, nkv, hd).mean(axis=0)
+    assert np.allclose(out[0], mean[0], atol=1e-6) and np.allclose(out[3], mean[1], atol=1e-6)
+    # S = 1 -> that V
+    out = orc.attention(rng.standard_normal(nq * hd).astype(np.float32), kc, vc,
+                        np.array([7], np.uint32), nq, nkv, hd).reshape(nq, hd)
+    assert np.allclose(out[1], vc[7].reshape(nkv, hd)[0], atol=1e-6)
+    # dominant score -> that slot's V
+    q = np.zeros(nq * hd, np.float32)
+    q[:hd] = kc[5, :hd] * 50
+    out = orc.attention(q, kc, vc, act, nq, nkv, hd).reshape(nq, hd)
+    assert np.allclose(out[0], vc[5, :hd], atol=1e-4)
+
+
+def test_attention_fp64_brute_force():
+    rng = np.random.default_rng(8)
+    nq, nkv, hd, slots = 16, 8, 256, 640
+    kc = rng.standard_normal((slots, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((slots, nkv * hd)).astype(np.float32)
+    q = rng.standard_normal(nq * hd).astype(np.float32) * 0.1
+    act = rng.permutation(slots)[:300].astype(np.uint32)
+    out = orc.attention(q, kc, vc, act, nq, nkv, hd)
+    ref = nr.attention64(q, kc, vc, act, nq, nkv, hd)
+    assert np.max(np.abs(out - ref)) < 1e-5 * max(1.0, np.max(np.abs(ref)))
+
+
+def test_qkv_norm_rope_composition():
+    rng = np.random.default_rng(6)
+    nq, nkv, hd, rot = 4, 2, 256, 64
+    q, k, v = (rng.standard_normal(n * hd).astype(np.float32) for n in (nq, nkv, nkv))
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    q2, k2, v2 = orc.qkv_norm_rope(q, k, v, qn, kn, nq, nkv, hd, rot, False, 1e4, 1e-6, 37)
+    qref = np.concatenate([nr.rmsnorm64(q[h * hd:(h + 1) * hd], qn) for h in range(nq)])
+    assert np.allclose(q2, nr.rope64(qref, 37, hd, rot, 1e4), atol=1e-4)
+    for h in range(nkv):
+        vh = v[h * hd:(h + 1) * hd].astype(np.float64)
+        assert np.allclose(v2[h * hd:(h + 1) * hd], vh / np.sqrt(np.mean(vh ** 2) + 1e-6), atol=1e-5)
+    # k_eq_v: V is the raw K, unit-RMS normalised
+    _, _, v3 = orc.qkv_norm_rope(q, k, v, qn, kn, nq, nkv, hd, rot, True, 1e4, 1e-6, 37)
+    kh = k[:hd].astype(np.float64)
+    assert np.allclose(v3[:hd], kh / np.sqrt(np.mean(kh ** 2) + 1e-6), atol=1e-5)

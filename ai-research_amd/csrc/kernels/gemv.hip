@@ -25,52 +25,76 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#define WG 256
 #define GROUP_STRIDE 132  // floats per 128-element x group in LDS (+4 pad)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 
-// Weights are streamed once per token: non-temporal 16-byte loads.
-__device__ __forceinline__ u32x4 ldnt(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+// 16-byte weight loads.  Plain loads, not non-temporal: lanes read 80 B
+// (Q4) or 144 B (Q8) apart, so each 128-B line is touched by several load
+// instructions of the same wave, and the streaming hint evicts it between
+// them (measured: 3.4 vs 6.4 TB/s on MI355X for this pattern).
+// Explicitly in the global address space: a pointer chosen at run time
+// between two arguments otherwise degrades to a FLAT load, which also counts
+// against lgkmcnt and so is drained by every LDS wait.
+typedef const u32x4 __attribute__((address_space(1)))* gvec_ptr;
+__device__ __forceinline__ u32x4 ldw(const void* p) {
+  return *(gvec_ptr)(p);
 }
 
 // Stage x[K] into LDS (padded by group) and write the per-block sums.
-// K % 128 == 0.  All threads of the block must call it.
+// K % 128 == 0.  All NT threads of the block must call it.  The loads of a
+// chunk of up to 8 float4 per thread are all issued before any is consumed,
+// so staging costs one L2 round trip per chunk rather than one per float4.
+template <int NT>
 __device__ __forceinline__ void stage_x(const float* __restrict__ X, uint32_t K,
                                         float* xs, float* bsum) {
+  constexpr uint32_t U = 8;
   const uint32_t n4 = K >> 2;
-  for (uint32_t i = threadIdx.x; i < n4; i += WG) {
-    float4 v = reinterpret_cast<const float4*>(X)[i];
-    uint32_t e = i << 2;                     // element index
-    uint32_t g = e >> 7, o = e & 127;        // group, offset in group
-    *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v;
-    float s = (v.x + v.y) + (v.z + v.w);
-    // a block is 8 consecutive float4s = 8 consecutive lanes (n4 % 8 == 0,
-    // so a lane group of 8 is either fully active or fully inactive)
-    s += __shfl_xor(s, 1, 8);
-    s += __shfl_xor(s, 2, 8);
-    s += __shfl_xor(s, 4, 8);
-    if ((i & 7) == 0) bsum[i >> 3] = s;
+  for (uint32_t base = 0; base < n4; base += NT * U) {
+    float4 v[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t i = base + u * NT + threadIdx.x;
+      if (i < n4) v[u] = reinterpret_cast<const float4*>(X)[i];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t i = base + u * NT + threadIdx.x;
+      if (base + u * NT >= n4) break;  // uniform: no thread has work from here on
+      float s = 0.f;
+      if (i < n4) {
+        const uint32_t e = i << 2;       // element index
+        const uint32_t g = e >> 7, o = e & 127;  // group, offset in group
+        *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v[u];
+        s = (v[u].x + v[u].y) + (v[u].z + v[u].w);
+      }
+      // a block is 8 consecutive float4s = 8 consecutive lanes (n4 % 8 == 0,
+      // so a lane group of 8 is either fully in range or fully out)
+      s += __shfl_xor(s, 1, 8);
+      s += __shfl_xor(s, 2, 8);
+      s += __shfl_xor(s, 4, 8);
+      if (i < n4 && (i & 7) == 0) bsum[i >> 3] = s;
+    }
   }
   __syncthreads();
 }
 
-// v_cvt_f32_ubyte{0..3}: byte k of a dword to float in one instruction.  The
-// compiler folds the 0x0F0F0F0F masks into bit-field extracts and loses this
-// form, so it is spelled out.
-#define GH_CVT_UB(N)                                                    \
-  __device__ __forceinline__ float cvt_ub##N(uint32_t x) {              \
-    float r;                                                            \
-    asm("v_cvt_f32_ubyte" #N " %0, %1" : "=v"(r) : "v"(x));             \
-    return r;                                                           \
-  }
-GH_CVT_UB(0)
-GH_CVT_UB(1)
-GH_CVT_UB(2)
-GH_CVT_UB(3)
+// Nibble/byte masks go through an opaque v_and_b32: when the compiler sees
+// the 0x0F0F0F0F mask it folds "(lo >> 8) & 0xFF" into a 4-bit field extract
+// and loses the one-instruction v_cvt_f32_ubyte{0..3} form.  With the mask
+// hidden it selects v_cvt_f32_ubyteN for every byte itself and schedules it.
+__device__ __forceinline__ uint32_t opaque_and(uint32_t w, uint32_t m) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(m), "v"(w));
+  return r;
+}
+
+__device__ __forceinline__ float ub0(uint32_t x) { return (float)(x & 0xFFu); }
+__device__ __forceinline__ float ub1(uint32_t x) { return (float)((x >> 8) & 0xFFu); }
+__device__ __forceinline__ float ub2(uint32_t x) { return (float)((x >> 16) & 0xFFu); }
+__device__ __forceinline__ float ub3(uint32_t x) { return (float)(x >> 24); }
 
 // sum_j n_j x_j over one Q4 block, n_j = nibble j (0..15).
 __device__ __forceinline__ float q4_nx(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
@@ -79,18 +103,18 @@ __device__ __forceinline__ float q4_nx(uint32_t w0, uint32_t w1, uint32_t w2, ui
   float sl = 0.f, sh = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint32_t lo = w[k] & 0x0F0F0F0Fu;  // nibbles 0,2,4,6 -> elements 8k+0,2,4,6
-    const uint32_t hi = w[k] & 0xF0F0F0F0u;  // 16 x nibbles 1,3,5,7
+    const uint32_t lo = opaque_and(w[k], 0x0F0F0F0Fu);  // nibbles 0,2,4,6 -> elements 8k+0,2,4,6
+    const uint32_t hi = opaque_and(w[k], 0xF0F0F0F0u);  // 16 x nibbles 1,3,5,7
     const float4 xa = *reinterpret_cast<const float4*>(xb + 8 * k);
     const float4 xc = *reinterpret_cast<const float4*>(xb + 8 * k + 4);
-    sl += cvt_ub0(lo) * xa.x;
-    sh += cvt_ub0(hi) * xa.y;
-    sl += cvt_ub1(lo) * xa.z;
-    sh += cvt_ub1(hi) * xa.w;
-    sl += cvt_ub2(lo) * xc.x;
-    sh += cvt_ub2(hi) * xc.y;
-    sl += cvt_ub3(lo) * xc.z;
-    sh += cvt_ub3(hi) * xc.w;
+    sl += ub0(lo) * xa.x;
+    sh += ub0(hi) * xa.y;
+    sl += ub1(lo) * xa.z;
+    sh += ub1(hi) * xa.w;
+    sl += ub2(lo) * xc.x;
+    sh += ub2(hi) * xc.y;
+    sl += ub3(lo) * xc.z;
+    sh += ub3(hi) * xc.w;
   }
   return sl + sh * 0.0625f;
 }
@@ -100,12 +124,12 @@ __device__ __forceinline__ float q8_ux(const uint32_t* w, const float* __restric
   float s0 = 0.f, s1 = 0.f;
 #pragma unroll
   for (int k = 0; k < 8; k++) {
-    const uint32_t u = w[k] ^ 0x80808080u;  // int8 q -> uint8 q + 128
+    const uint32_t u = opaque_and(w[k] ^ 0x80808080u, 0xFFFFFFFFu);  // int8 q -> uint8 q + 128
     const float4 xa = *reinterpret_cast<const float4*>(xb + 4 * k);
-    s0 += cvt_ub0(u) * xa.x;
-    s1 += cvt_ub1(u) * xa.y;
-    s0 += cvt_ub2(u) * xa.z;
-    s1 += cvt_ub3(u) * xa.w;
+    s0 += ub0(u) * xa.x;
+    s1 += ub1(u) * xa.y;
+    s0 += ub2(u) * xa.z;
+    s1 += ub3(u) * xa.w;
   }
   return s0 + s1;
 }
@@ -116,11 +140,11 @@ struct Q4G {
 
 __device__ __forceinline__ Q4G load_q4g(const uint8_t* p) {
   Q4G g;
-  g.a0 = ldnt(p + 0);
-  g.a1 = ldnt(p + 16);
-  g.a2 = ldnt(p + 32);
-  g.a3 = ldnt(p + 48);
-  g.a4 = ldnt(p + 64);
+  g.a0 = ldw(p + 0);
+  g.a1 = ldw(p + 16);
+  g.a2 = ldw(p + 32);
+  g.a3 = ldw(p + 48);
+  g.a4 = ldw(p + 64);
   return g;
 }
 
@@ -149,167 +173,204 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 // ------------------------------------------------------------------------
-// Q4_0 GEMV
+// Weight formats: one "item" = one 4-block group of one row.
 // ------------------------------------------------------------------------
-template <int TPR, int RPT>
-__device__ __forceinline__ void gemv_q4_body(const uint8_t* __restrict__ W,
-                                             const float* __restrict__ X,
-                                             float* __restrict__ Y, uint32_t M, uint32_t K) {
+struct Q4Fmt {  // shaders/gemv_q4.wgsl
+  static constexpr uint32_t kGroupBytes = 80, kBlockBytes = 20, kSub = 1;
+  struct Item {
+    Q4G w;
+  };
+  struct Acc {
+    float s;
+  };
+  struct Args {
+    const uint8_t* W;
+    float* Y;
+  };
+  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
+    it.w = load_q4g(a.W + off);
+  }
+  __device__ static void zero(Acc& c) { c.s = 0.f; }
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
+                             uint32_t) {
+    c.s += valid * q4_group_dot(it.w, xg, bs);
+  }
+  template <int TPR>
+  __device__ static void finish(const Acc& c, const Args& a, uint32_t row, bool writer) {
+    const float v = team_sum<TPR>(c.s);
+    if (writer) a.Y[row] = v;
+  }
+};
+
+struct GateUpFmt {  // shaders/fused_mlp_q4.wgsl: act = gelu_tanh(Wg x) * (Wu x)
+  static constexpr uint32_t kGroupBytes = 80, kBlockBytes = 20;
+  // Sub-items: each (row, group) is walked twice, gate then up, so a lane
+  // holds one 80-B group per look-ahead slot instead of two.
+  static constexpr uint32_t kSub = 2;
+  struct Item {
+    Q4G w;
+  };
+  struct Acc {
+    float g, u;
+  };
+  struct Args {
+    const uint8_t* Wg;
+    const uint8_t* Wu;
+    float* Y;
+  };
+  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t sub) {
+    it.w = load_q4g((sub ? a.Wu : a.Wg) + off);
+  }
+  __device__ static void zero(Acc& c) { c.g = c.u = 0.f; }
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
+                             uint32_t sub) {
+    const float d = valid * q4_group_dot(it.w, xg, bs);
+    if (sub) c.u += d; else c.g += d;
+  }
+  template <int TPR>
+  __device__ static void finish(const Acc& c, const Args& a, uint32_t row, bool writer) {
+    const float g = team_sum<TPR>(c.g);
+    const float u = team_sum<TPR>(c.u);
+    if (writer) a.Y[row] = gelu_tanh(g) * u;
+  }
+};
+
+struct Q8Fmt {  // shaders/gemv_q8.wgsl
+  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 1;
+  struct Item {
+    u32x4 v[9];
+  };
+  struct Acc {
+    float s;
+  };
+  struct Args {
+    const uint8_t* W;
+    float* Y;
+  };
+  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
+#pragma unroll
+    for (int k = 0; k < 9; k++) it.v[k] = ldw(a.W + off + 16 * k);
+  }
+  __device__ static void zero(Acc& c) { c.s = 0.f; }
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
+                             uint32_t) {
+    uint32_t w[36];
+#pragma unroll
+    for (int k = 0; k < 9; k++) {
+      w[4 * k + 0] = it.v[k].x;
+      w[4 * k + 1] = it.v[k].y;
+      w[4 * k + 2] = it.v[k].z;
+      w[4 * k + 3] = it.v[k].w;
+    }
+    float r = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) r += u2f(w[9 * j]) * (q8_ux(&w[9 * j + 1], xg + 32 * j) - 128.0f * bs[j]);
+    c.s += valid * r;
+  }
+  template <int TPR>
+  __device__ static void finish(const Acc& c, const Args& a, uint32_t row, bool writer) {
+    const float v = team_sum<TPR>(c.s);
+    if (writer) a.Y[row] = v;
+  }
+};
+
+// ------------------------------------------------------------------------
+// Persistent row-team streaming.  Team t (TPR lanes) owns rows t, t + T,
+// t + 2T, ... (T = teams in the grid); lane l of a team owns groups
+// l, l + TPR, ..., l + (GPL-1) TPR of each of its rows.  A lane walks its
+// items in order through a ring of D item buffers: while item i is reduced,
+// items i+1 .. i+D-1 are in flight, so each wave keeps D-1 groups of HBM
+// traffic outstanding through its compute.  The ring is unrolled so no
+// register copies (which would force an early wait) are needed.  Items past
+// the end (group >= ng, or look-ahead beyond the last row) load an in-range
+// duplicate and contribute zero.
+// ------------------------------------------------------------------------
+template <class F, int TPR, int GPL, int D, int NT>
+__device__ __forceinline__ void stream_rows(const typename F::Args& a, const float* __restrict__ X,
+                                            uint32_t M, uint32_t K) {
   extern __shared__ float lds[];
   const uint32_t nb = K >> 5, ng = nb >> 2;
   float* xs = lds;
   float* bsum = lds + ng * GROUP_STRIDE;
-  stage_x(X, K, xs, bsum);
 
-  constexpr int TEAMS = WG / TPR;
+  constexpr uint32_t TEAMS = NT / TPR;
   const uint32_t lr = threadIdx.x % TPR;
-  const uint32_t row0 = (blockIdx.x * TEAMS + threadIdx.x / TPR) * RPT;
-  const size_t row_bytes = (size_t)nb * 20;
-  float acc[RPT];
-#pragma unroll
-  for (int r = 0; r < RPT; r++) acc[r] = 0.f;
+  const uint32_t team = blockIdx.x * TEAMS + threadIdx.x / TPR;
+  const uint32_t nteams = gridDim.x * TEAMS;
+  // Idle teams (team >= M) still stage x with the block, then exit.
+  const bool active = team < M;
+  constexpr uint32_t PER_ROW = GPL * F::kSub;  // items per row for one lane
+  const uint32_t n_items = active ? ((M - 1 - team) / nteams + 1) * PER_ROW : 0;
+  const size_t row_bytes = (size_t)nb * F::kBlockBytes;
 
-  for (uint32_t g = lr; g < ng; g += TPR) {
-    Q4G q[RPT];
+  // item i -> row (i / PER_ROW), lane group slot ((i % PER_ROW) / kSub),
+  // sub-matrix (i % kSub)
+  auto group_of = [&](uint32_t i) -> uint32_t { return lr + ((i % PER_ROW) / F::kSub) * TPR; };
+  auto offset_of = [&](uint32_t i) -> size_t {
+    i = i < n_items ? i : n_items - 1;
+    const uint32_t row = team + (i / PER_ROW) * nteams;
+    uint32_t g = group_of(i);
+    g = g < ng ? g : ng - 1;
+    return (size_t)row * row_bytes + (size_t)g * F::kGroupBytes;
+  };
+
+  // The first D items' weight loads go out before x is staged, so the x
+  // round trip through L2 overlaps the weight latency.
+  typename F::Item buf[D];
+  if (active) {
 #pragma unroll
-    for (int r = 0; r < RPT; r++) {
-      const uint32_t row = row0 + r < M ? row0 + r : M - 1;  // clamp: tail rows are discarded
-      q[r] = load_q4g(W + (size_t)row * row_bytes + (size_t)g * 80);
-    }
-    const float* xg = xs + g * GROUP_STRIDE;
-    const float* bs = bsum + g * 4;
-#pragma unroll
-    for (int r = 0; r < RPT; r++) acc[r] += q4_group_dot(q[r], xg, bs);
+    for (int d = 0; d < D; d++) F::load(buf[d], a, offset_of(d), d % F::kSub);
   }
+  stage_x<NT>(X, K, xs, bsum);
+  if (!active) return;
+  typename F::Acc acc;
+  F::zero(acc);
+  for (uint32_t base = 0; base < n_items; base += D) {
 #pragma unroll
-  for (int r = 0; r < RPT; r++) {
-    const float v = team_sum<TPR>(acc[r]);
-    if (lr == 0 && row0 + r < M) Y[row0 + r] = v;
-  }
-}
-
-// ------------------------------------------------------------------------
-// fused gate + up GeGLU on Q4_0 rows
-// ------------------------------------------------------------------------
-template <int TPR, int RPT>
-__device__ __forceinline__ void gateup_q4_body(const uint8_t* __restrict__ Wg,
-                                               const uint8_t* __restrict__ Wu,
-                                               const float* __restrict__ X,
-                                               float* __restrict__ Y, uint32_t M, uint32_t K) {
-  extern __shared__ float lds[];
-  const uint32_t nb = K >> 5, ng = nb >> 2;
-  float* xs = lds;
-  float* bsum = lds + ng * GROUP_STRIDE;
-  stage_x(X, K, xs, bsum);
-
-  constexpr int TEAMS = WG / TPR;
-  const uint32_t lr = threadIdx.x % TPR;
-  const uint32_t row0 = (blockIdx.x * TEAMS + threadIdx.x / TPR) * RPT;
-  const size_t row_bytes = (size_t)nb * 20;
-  float ag[RPT], au[RPT];
-#pragma unroll
-  for (int r = 0; r < RPT; r++) ag[r] = au[r] = 0.f;
-
-  for (uint32_t g = lr; g < ng; g += TPR) {
-    Q4G qg[RPT], qu[RPT];
-#pragma unroll
-    for (int r = 0; r < RPT; r++) {
-      const uint32_t row = row0 + r < M ? row0 + r : M - 1;
-      const size_t off = (size_t)row * row_bytes + (size_t)g * 80;
-      qg[r] = load_q4g(Wg + off);
-      qu[r] = load_q4g(Wu + off);
-    }
-    const float* xg = xs + g * GROUP_STRIDE;
-    const float* bs = bsum + g * 4;
-#pragma unroll
-    for (int r = 0; r < RPT; r++) {
-      ag[r] += q4_group_dot(qg[r], xg, bs);
-      au[r] += q4_group_dot(qu[r], xg, bs);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < RPT; r++) {
-    const float gsum = team_sum<TPR>(ag[r]);
-    const float usum = team_sum<TPR>(au[r]);
-    if (lr == 0 && row0 + r < M) Y[row0 + r] = gelu_tanh(gsum) * usum;
-  }
-}
-
-// ------------------------------------------------------------------------
-// Q8_0 GEMV
-// ------------------------------------------------------------------------
-template <int TPR, int RPT>
-__device__ __forceinline__ void gemv_q8_body(const uint8_t* __restrict__ W,
-                                             const float* __restrict__ X,
-                                             float* __restrict__ Y, uint32_t M, uint32_t K) {
-  extern __shared__ float lds[];
-  const uint32_t nb = K >> 5, ng = nb >> 2;
-  float* xs = lds;
-  float* bsum = lds + ng * GROUP_STRIDE;
-  stage_x(X, K, xs, bsum);
-
-  constexpr int TEAMS = WG / TPR;
-  const uint32_t lr = threadIdx.x % TPR;
-  const uint32_t row0 = (blockIdx.x * TEAMS + threadIdx.x / TPR) * RPT;
-  const size_t row_bytes = (size_t)nb * 36;
-  float acc[RPT];
-#pragma unroll
-  for (int r = 0; r < RPT; r++) acc[r] = 0.f;
-
-  for (uint32_t g = lr; g < ng; g += TPR) {
-    uint32_t w[RPT][36];
-#pragma unroll
-    for (int r = 0; r < RPT; r++) {
-      const uint32_t row = row0 + r < M ? row0 + r : M - 1;
-      const uint8_t* p = W + (size_t)row * row_bytes + (size_t)g * 144;
-#pragma unroll
-      for (int v = 0; v < 9; v++) {
-        const u32x4 t = ldnt(p + 16 * v);
-        w[r][4 * v + 0] = t.x;
-        w[r][4 * v + 1] = t.y;
-        w[r][4 * v + 2] = t.z;
-        w[r][4 * v + 3] = t.w;
+    for (int d = 0; d < D; d++) {
+      const uint32_t i = base + d;
+      if (i < n_items) {  // uniform within a team
+        const uint32_t g = group_of(i);
+        const uint32_t gc = g < ng ? g : ng - 1;
+        F::fma(acc, buf[d], xs + gc * GROUP_STRIDE, bsum + gc * 4, g < ng ? 1.0f : 0.0f,
+               i % F::kSub);
+        if (i % PER_ROW == PER_ROW - 1) {
+          F::template finish<TPR>(acc, a, team + (i / PER_ROW) * nteams, lr == 0);
+          F::zero(acc);
+        }
       }
+      F::load(buf[d], a, offset_of(i + D), (i + D) % F::kSub);
     }
-    const float* xg = xs + g * GROUP_STRIDE;
-    const float* bs = bsum + g * 4;
-#pragma unroll
-    for (int r = 0; r < RPT; r++) {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[r] += u2f(w[r][9 * j]) * (q8_ux(&w[r][9 * j + 1], xg + 32 * j) - 128.0f * bs[j]);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < RPT; r++) {
-    const float v = team_sum<TPR>(acc[r]);
-    if (lr == 0 && row0 + r < M) Y[row0 + r] = v;
   }
 }
 
-#define GH_GEMV_INST(T, R)                                                                     \
-  extern "C" __global__ __launch_bounds__(WG) void gh_gemv_q4_t##T##_r##R(                      \
-      const uint8_t* W, const float* X, float* Y, uint32_t M, uint32_t K) {                     \
-    gemv_q4_body<T, R>(W, X, Y, M, K);                                                          \
-  }                                                                                             \
-  extern "C" __global__ __launch_bounds__(WG) void gh_gateup_q4_t##T##_r##R(                    \
-      const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y, uint32_t M, uint32_t K) { \
-    gateup_q4_body<T, R>(Wg, Wu, X, Y, M, K);                                                   \
-  }                                                                                             \
-  extern "C" __global__ __launch_bounds__(WG) void gh_gemv_q8_t##T##_r##R(                      \
-      const uint8_t* W, const float* X, float* Y, uint32_t M, uint32_t K) {                     \
-    gemv_q8_body<T, R>(W, X, Y, M, K);                                                          \
+#define GH_GEMV_INST(T, G, D)                                                                   \
+  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q4_t##T##_g##G##_d##D(               \
+      const uint8_t* W, const float* X, float* Y, uint32_t M, uint32_t K) {                       \
+    stream_rows<Q4Fmt, T, G, D, 256>(Q4Fmt::Args{W, Y}, X, M, K);                                \
+  }                                                                                               \
+  extern "C" __global__ __launch_bounds__(256) void gh_gateup_q4_t##T##_g##G##_d##D(             \
+      const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y, uint32_t M, uint32_t K) {   \
+    stream_rows<GateUpFmt, T, G, D, 256>(GateUpFmt::Args{Wg, Wu, Y}, X, M, K);                   \
+  }                                                                                               \
+  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q8_t##T##_g##G##_d##D(               \
+      const uint8_t* W, const float* X, float* Y, uint32_t M, uint32_t K) {                       \
+    stream_rows<Q8Fmt, T, G, D, 256>(Q8Fmt::Args{W, Y}, X, M, K);                                \
   }
 
-GH_GEMV_INST(8, 1)
-GH_GEMV_INST(8, 2)
-GH_GEMV_INST(8, 4)
-GH_GEMV_INST(16, 1)
-GH_GEMV_INST(16, 2)
-GH_GEMV_INST(16, 4)
-GH_GEMV_INST(32, 1)
-GH_GEMV_INST(32, 2)
-GH_GEMV_INST(32, 4)
-GH_GEMV_INST(64, 1)
-GH_GEMV_INST(64, 2)
-GH_GEMV_INST(64, 4)
+#define GH_GEMV_INST_D(T, G) \
+  GH_GEMV_INST(T, G, 2)      \
+  GH_GEMV_INST(T, G, 3)      \
+  GH_GEMV_INST(T, G, 4)
+
+GH_GEMV_INST_D(8, 1)
+GH_GEMV_INST_D(8, 2)
+GH_GEMV_INST_D(16, 1)
+GH_GEMV_INST_D(16, 2)
+GH_GEMV_INST_D(16, 4)
+GH_GEMV_INST_D(32, 1)
+GH_GEMV_INST_D(32, 2)
+GH_GEMV_INST_D(32, 4)
+GH_GEMV_INST_D(64, 1)
+GH_GEMV_INST_D(64, 2)
+GH_GEMV_INST_D(64, 4)

@@ -12,28 +12,45 @@ using gh::fail;
 namespace {
 
 struct GemvCfg {
-  int tpr, rpt;
+  int tpr, gpl, wgs_per_cu, depth;
 };
 
-// Lanes per row team: the smallest power of two (8..64) covering the row's
-// 4-block groups, so one pass over the groups needs no second iteration
-// unless a row has more than 64 groups.  Rows per lane: 2 when that still
-// leaves >= 2 workgroups per CU, else 1.
+unsigned x_lds_bytes(uint32_t K);
+
+// Lanes per row team (TPR) and 4-block groups per lane per row (GPL) with
+// TPR * GPL >= the row's group count and the least idle lanes; then a
+// persistent grid of wgs_per_cu workgroups per CU (bounded by LDS).
 GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K) {
   const uint32_t ng = K / 128;
-  int tpr = 8;
-  while (tpr < 64 && (uint32_t)tpr < ng) tpr <<= 1;
-  const uint32_t teams = 256 / tpr;
-  int rpt = (M / (teams * 2) >= (uint32_t)ctx->num_cus * 2) ? 2 : 1;
-  if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning override "tpr,rpt"
-    int t = 0, r = 0;
-    if (sscanf(env, "%d,%d", &t, &r) == 2 && (t == 8 || t == 16 || t == 32 || t == 64) &&
-        (r == 1 || r == 2 || r == 4)) {
-      tpr = t;
-      rpt = r;
+  static const int kT[] = {8, 16, 32, 64};
+  int best_t = 64, best_g = 4;
+  uint32_t best_waste = ~0u;
+  for (int g : {1, 2, 4}) {
+    for (int t : kT) {
+      if ((uint32_t)(t * g) < ng) continue;
+      if (t == 8 && g == 4) continue;
+      const uint32_t waste = t * g - ng;
+      if (waste < best_waste || (waste == best_waste && t > best_t)) {
+        best_waste = waste;
+        best_t = t;
+        best_g = g;
+      }
+    }
+    if (best_waste != ~0u) break;  // prefer one group per lane per row
+  }
+  GemvCfg c{best_t, best_g, 4, 3};
+  if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning override "tpr,gpl,wgs_per_cu,depth"
+    int t = 0, g = 0, w = 0, d = 0;
+    if (sscanf(env, "%d,%d,%d,%d", &t, &g, &w, &d) == 4 && (t == 8 || t == 16 || t == 32 || t == 64) &&
+        (g == 1 || g == 2 || g == 4) && !(t == 8 && g == 4) && w >= 1 && w <= 32 &&
+        (uint32_t)(t * g) >= ng && d >= 2 && d <= 4) {
+      c = {t, g, w, d};
     }
   }
-  return {tpr, rpt};
+  const unsigned lds_cap = (unsigned)(ctx->max_lds / std::max(1u, x_lds_bytes(K)));
+  c.wgs_per_cu = std::max(1, std::min<int>(c.wgs_per_cu, (int)lds_cap));
+  (void)M;
+  return c;
 }
 
 unsigned x_lds_bytes(uint32_t K) { return (K / 128) * 132 * 4 + (K / 32) * 4; }
@@ -44,6 +61,8 @@ gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const
   if (M == 0 || K == 0) return fail(GH_ERR_INVALID, std::string(who) + ": M or K is zero");
   if (K % 128 != 0)
     return fail(GH_ERR_UNSUPPORTED, std::string(who) + ": K must be a multiple of 128");
+  if (K > 32768)  // a row team covers at most 64 lanes x 4 groups of 128
+    return fail(GH_ERR_UNSUPPORTED, std::string(who) + ": K above 32768");
   if ((reinterpret_cast<uintptr_t>(W) & 15) || (reinterpret_cast<uintptr_t>(X) & 15))
     return fail(GH_ERR_INVALID, std::string(who) + ": W and X must be 16-byte aligned");
   if (x_lds_bytes(K) > ctx->max_lds)
@@ -53,9 +72,11 @@ gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const
 
 gh_status launch_gemv(gh_context* ctx, const char* family, void** args, uint32_t M, uint32_t K) {
   GemvCfg c = pick_gemv(ctx, M, K);
-  const uint32_t rows_per_wg = (256 / c.tpr) * c.rpt;
-  const unsigned grid = (M + rows_per_wg - 1) / rows_per_wg;
-  std::string name = std::string(family) + "_t" + std::to_string(c.tpr) + "_r" + std::to_string(c.rpt);
+  const uint32_t teams_per_wg = 256 / c.tpr;
+  const uint32_t max_grid = (M + teams_per_wg - 1) / teams_per_wg;
+  const unsigned grid = std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * c.wgs_per_cu);
+  std::string name = std::string(family) + "_t" + std::to_string(c.tpr) + "_g" +
+                     std::to_string(c.gpl) + "_d" + std::to_string(c.depth);
   return ctx->launch(name, dim3(grid), dim3(256), x_lds_bytes(K), args);
 }
 

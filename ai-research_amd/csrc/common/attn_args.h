@@ -1,0 +1,21 @@
+// attn_args.h -- kernel argument block of the split-K decode attention,
+// shared by the gfx950 kernel and the host launcher (passed by value).
+#pragma once
+#include <stdint.h>
+
+struct AttnArgs {
+  const float* q;          // [nq][D]: raw projections when fuse, else normalised + roped
+  const float* k_in;       // fuse: raw k [nkv][D]
+  const float* v_in;       // fuse: raw v [nkv][D]
+  const float* q_norm;     // fuse: [D]
+  const float* k_norm;     // fuse: [D]
+  float* k_cache;          // [slots][nkv * D]
+  float* v_cache;
+  const uint32_t* active;  // [S] slot numbers (src/ring_buffer.zig getActiveSlots)
+  const uint32_t* step;    // {clock, slot_idx, S, 0}
+  float* part;             // [nkv][nsplit][G][D + 2] partial (o, m, l)
+  uint32_t* counters;      // [nkv], zero between launches
+  float* out;              // [nq][D]
+  uint32_t nq, nkv, D, rot, k_eq_v, nsplit, fuse;
+  float theta, eps, scale;
+};

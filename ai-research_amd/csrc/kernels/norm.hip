@@ -1,0 +1,144 @@
+// norm.hip -- RMSNorm, residual add + RMSNorm and greedy argmax for gfx950.
+//
+//   rmsnorm      shaders/rmsnorm.wgsl:13-48, src/kernels.zig:46-52
+//                Y = X * (mean(X^2) + eps)^-1/2 * W
+//   add_rmsnorm  shaders/add_rmsnorm.wgsl:15-51
+//                X <- (X + R) * scalar (in place); Y = RMSNorm(X) * W
+//   argmax       shaders/argmax.wgsl:12-48, src/kernels.zig:164-174
+//                index of the largest logit; ties go to the LOWEST index, as
+//                the CPU path does (the reference shader does not guarantee it)
+//
+// The decode step fuses the norms into the GEMV prologues and the argmax
+// into the vocab GEMV; these standalone kernels are the reference-shaped
+// entry points (one workgroup for a norm, as in the reference) and the
+// building blocks they share.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define NORM_NT 1024
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  const uint32_t nw = blockDim.x >> 6;
+  for (uint32_t w = 0; w < nw; w++) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+extern "C" __global__ __launch_bounds__(NORM_NT) void gh_rmsnorm_k(const float* X,
+                                                                   const float* __restrict__ W,
+                                                                   float* Y, uint32_t dim,
+                                                                   float eps) {
+  __shared__ float red[NORM_NT / 64];
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) ss += X[i] * X[i];
+  const float r = 1.0f / sqrtf(block_sum(ss, red) / (float)dim + eps);
+  for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) Y[i] = X[i] * r * W[i];
+}
+
+extern "C" __global__ __launch_bounds__(NORM_NT) void gh_add_rmsnorm_k(
+    float* X, const float* __restrict__ R, const float* __restrict__ W, float* Y, uint32_t dim,
+    float eps, float scalar) {
+  __shared__ float red[NORM_NT / 64];
+  float ss = 0.f;
+  for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) {
+    const float v = (X[i] + R[i]) * scalar;
+    X[i] = v;
+    ss += v * v;
+  }
+  const float r = 1.0f / sqrtf(block_sum(ss, red) / (float)dim + eps);
+  for (uint32_t i = threadIdx.x; i < dim; i += blockDim.x) Y[i] = X[i] * r * W[i];
+}
+
+// (value, index) order for the greedy pick: larger value wins, equal values
+// go to the smaller index.
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const uint32_t oi = __shfl_xor(i, off, 64);
+    if (better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// Two levels: every workgroup reduces a contiguous slice into a partial, the
+// last workgroup to finish reduces the partials (deterministic order) and
+// writes out_token.  partial: 2 * gridDim.x words; counter: 1 word, zero
+// between launches (reset by the last workgroup).
+extern "C" __global__ __launch_bounds__(256) void gh_argmax_k(const float* __restrict__ logits,
+                                                              uint32_t n, uint32_t* out_token,
+                                                              uint32_t* partial,
+                                                              uint32_t* counter) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
+  __shared__ uint32_t last;
+  const uint32_t per = (n + gridDim.x - 1) / gridDim.x;
+  const uint32_t b0 = blockIdx.x * per, b1 = min(n, b0 + per);
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t i = b0 + threadIdx.x; i < b1; i += blockDim.x) {
+    const float v = logits[i];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  wave_argmax(bv, bi);
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    partial[2 * blockIdx.x] = __float_as_uint(bv);
+    partial[2 * blockIdx.x + 1] = bi;
+    __threadfence();
+    last = (atomicAdd(counter, 1u) == gridDim.x - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  bv = -INFINITY;
+  bi = 0xFFFFFFFFu;
+  for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
+    const float v = __uint_as_float(__builtin_nontemporal_load(&partial[2 * b]));
+    const uint32_t i = __builtin_nontemporal_load(&partial[2 * b + 1]);
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    out_token[0] = bi == 0xFFFFFFFFu ? 0u : bi;
+    counter[0] = 0;
+  }
+}

@@ -111,4 +111,119 @@ gh_status gh_gate_up_geglu_q4(gh_context* ctx, const void* Wg, const void* Wu, c
   return launch_gemv(ctx, "gh_gateup_q4", args, M, K);
 }
 
+gh_status gh_rmsnorm(gh_context* ctx, const float* X, const float* W, float* Y, uint32_t dim,
+                     float eps) {
+  if (!ctx || !X || !W || !Y || dim == 0) return fail(GH_ERR_INVALID, "gh_rmsnorm: bad argument");
+  void* args[] = {const_cast<float**>(&X), const_cast<float**>(&W), &Y, &dim, &eps};
+  return ctx->launch("gh_rmsnorm_k", dim3(1), dim3(1024), 0, args);
+}
+
+gh_status gh_add_rmsnorm(gh_context* ctx, float* X, const float* R, const float* W, float* Y,
+                         uint32_t dim, float eps, float scalar) {
+  if (!ctx || !X || !R || !W || !Y || dim == 0)
+    return fail(GH_ERR_INVALID, "gh_add_rmsnorm: bad argument");
+  void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&W), &Y, &dim, &eps, &scalar};
+  return ctx->launch("gh_add_rmsnorm_k", dim3(1), dim3(1024), 0, args);
+}
+
+gh_status gh_qkv_rope(gh_context* ctx, const float* Q_in, const float* K_in, const float* V_in,
+                      const float* Q_norm, const float* K_norm, float* Q_out, float* K_cache,
+                      float* V_cache, const uint32_t* step_params, uint32_t num_q,
+                      uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim, uint32_t k_eq_v,
+                      float theta, float eps) {
+  if (!ctx || !Q_in || !K_in || (!V_in && !k_eq_v) || !Q_norm || !K_norm || !Q_out || !K_cache ||
+      !V_cache || !step_params)
+    return fail(GH_ERR_INVALID, "gh_qkv_rope: null pointer");
+  if (num_q == 0 || num_kv == 0 || head_dim == 0 || rotary_dim > head_dim || rotary_dim % 2)
+    return fail(GH_ERR_INVALID, "gh_qkv_rope: bad head shape");
+  if (!V_in) V_in = K_in;
+  void* args[] = {const_cast<float**>(&Q_in), const_cast<float**>(&K_in),
+                  const_cast<float**>(&V_in), const_cast<float**>(&Q_norm),
+                  const_cast<float**>(&K_norm), &Q_out, &K_cache, &V_cache,
+                  const_cast<uint32_t**>(&step_params), &num_q, &num_kv, &head_dim,
+                  &rotary_dim, &k_eq_v, &theta, &eps};
+  return ctx->launch("gh_qkv_rope_k", dim3(num_q + num_kv), dim3(64), 0, args);
+}
+
+}  // extern "C"
+
+namespace gh {
+
+// Attention launch shared by the standalone entry point and the model.
+gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
+  const uint32_t G = L.args.nq / L.args.nkv;
+  const uint32_t D = L.args.D;
+  if (L.args.nkv == 0 || L.args.nq % L.args.nkv != 0 || G > 4)
+    return fail(GH_ERR_UNSUPPORTED, "attention: query heads per kv head must be 1..4");
+  int dpl = D <= 128 ? 2 : (D <= 256 ? 4 : 8);
+  if (D > 512 || D % dpl != 0 || D % 4 != 0)
+    return fail(GH_ERR_UNSUPPORTED, "attention: head_dim must be a multiple of 4 up to 512");
+  void* args[] = {const_cast<AttnArgs*>(&L.args)};
+  const char* name = dpl == 2 ? "gh_attn_d2_k" : (dpl == 4 ? "gh_attn_d4_k" : "gh_attn_d8_k");
+  return ctx->launch(name, dim3(L.args.nkv * L.args.nsplit), dim3(256), 0, args);
+}
+
+uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {
+  uint32_t ns = (2u * (uint32_t)ctx->num_cus + nkv - 1) / nkv;  // about two workgroups per CU
+  ns = std::min<uint32_t>(ns, std::max<uint32_t>(1u, (max_slots + 7) / 8));  // >= 8 slots a split
+  if (const char* env = getenv("GH_ATTN_SPLITS")) {
+    int v = atoi(env);
+    if (v >= 1 && v <= 256) ns = (uint32_t)v;
+  }
+  return std::max<uint32_t>(1u, std::min<uint32_t>(ns, 256u));
+}
+
+}  // namespace gh
+
+extern "C" {
+
+gh_status gh_decode_attn(gh_context* ctx, const float* Q, const float* K_cache,
+                         const float* V_cache, const uint32_t* active_slots, float* out,
+                         const uint32_t* step_params, uint32_t head_dim, uint32_t kv_dim,
+                         uint32_t gqa_ratio, float inv_sqrt_dim, uint32_t num_q_heads) {
+  if (!ctx || !Q || !K_cache || !V_cache || !active_slots || !out || !step_params)
+    return fail(GH_ERR_INVALID, "gh_decode_attn: null pointer");
+  if (gqa_ratio == 0 || num_q_heads % gqa_ratio || head_dim == 0 ||
+      kv_dim != (num_q_heads / gqa_ratio) * head_dim)
+    return fail(GH_ERR_INVALID, "gh_decode_attn: kv_dim must equal (num_q / gqa) * head_dim");
+  gh::AttnLaunch L{};
+  AttnArgs& a = L.args;
+  a.q = Q;
+  a.k_cache = const_cast<float*>(K_cache);
+  a.v_cache = const_cast<float*>(V_cache);
+  a.active = active_slots;
+  a.step = step_params;
+  a.out = out;
+  a.nq = num_q_heads;
+  a.nkv = num_q_heads / gqa_ratio;
+  a.D = head_dim;
+  a.rot = 0;
+  a.fuse = 0;
+  a.scale = inv_sqrt_dim;
+  a.nsplit = gh::attention_splits(ctx, a.nkv, 1024);
+  const size_t part_bytes = (size_t)a.nkv * a.nsplit * gqa_ratio * (head_dim + 2) * 4;
+  if (a.nkv > 256) return fail(GH_ERR_UNSUPPORTED, "gh_decode_attn: more than 256 kv heads");
+  // counters first, at a fixed offset, so a later call with a different
+  // partial size still finds them at zero
+  gh_status st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes,
+                                    256 * 4 + part_bytes);
+  if (st != GH_OK) return st;
+  a.counters = static_cast<uint32_t*>(ctx->attn_scratch);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(ctx->attn_scratch) + 256 * 4);
+  return gh::launch_attention(ctx, L);
+}
+
+gh_status gh_argmax(gh_context* ctx, const float* logits, uint32_t* out_token, uint32_t vocab) {
+  if (!ctx || !logits || !out_token || vocab == 0)
+    return fail(GH_ERR_INVALID, "gh_argmax: bad argument");
+  const uint32_t grid = std::min<uint32_t>(256u, (vocab + 1023) / 1024);
+  gh_status st = ctx->ensure_zeroed(&ctx->argmax_scratch, &ctx->argmax_scratch_bytes,
+                                    (2 * 256 + 64) * 4);
+  if (st != GH_OK) return st;
+  uint32_t* partial = static_cast<uint32_t*>(ctx->argmax_scratch);
+  uint32_t* counter = partial + 2 * 256;
+  void* args[] = {const_cast<float**>(&logits), &vocab, &out_token, &partial, &counter};
+  return ctx->launch("gh_argmax_k", dim3(grid), dim3(256), 0, args);
+}
+
 }  // extern "C"

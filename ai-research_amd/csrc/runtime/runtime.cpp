@@ -91,9 +91,34 @@ gh_status gh_context::launch(const std::string& name, dim3 grid, dim3 block, uns
   return GH_OK;
 }
 
+gh_status gh_context::ensure_zeroed(void** buf, size_t* have, size_t need) {
+  if (*have >= need) return GH_OK;
+  if (*buf) {
+    hipStreamSynchronize(stream);
+    hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+  }
+  hipError_t e = hipMalloc(buf, need);
+  if (e != hipSuccess) return fail(GH_ERR_ALLOC, std::string("scratch hipMalloc: ") + hipGetErrorString(e));
+  uint64_t n = need / 4;
+  void* args[] = {buf, nullptr, &n};
+  uint32_t zero = 0;
+  args[1] = &zero;
+  gh_status st = launch("gh_fill_u32_k", dim3((unsigned)std::min<uint64_t>((n + 255) / 256, 4096)),
+                        dim3(256), 0, args);
+  if (st != GH_OK) return st;
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "scratch zero-fill");
+  *have = need;
+  return GH_OK;
+}
+
 gh_context::~gh_context() {
   if (stream) {
     hipStreamSynchronize(stream);
+    if (attn_scratch) hipFree(attn_scratch);
+    if (argmax_scratch) hipFree(argmax_scratch);
     hipStreamDestroy(stream);
   }
   for (hipModule_t m : modules) hipModuleUnload(m);

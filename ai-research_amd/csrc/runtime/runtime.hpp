@@ -17,6 +17,14 @@ struct gh_context {
   int num_cus = 0;
   size_t max_lds = 0;
   std::vector<hipModule_t> modules;
+  // Scratch of the standalone split-K attention and argmax entry points:
+  // partial records plus last-block counters, zero-filled when (re)allocated
+  // and left at zero by every launch.
+  void* attn_scratch = nullptr;
+  size_t attn_scratch_bytes = 0;
+  void* argmax_scratch = nullptr;
+  size_t argmax_scratch_bytes = 0;
+  gh_status ensure_zeroed(void** buf, size_t* have, size_t need);
   std::unordered_map<std::string, hipFunction_t> fns;
   std::mutex mu;
 
@@ -26,8 +34,15 @@ struct gh_context {
   ~gh_context();
 };
 
+#include "../common/attn_args.h"
+
 namespace gh {
 using Context = gh_context;
+struct AttnLaunch {
+  AttnArgs args;
+};
+gh_status launch_attention(gh_context* ctx, const AttnLaunch& L);
+uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);
 }  // namespace gh

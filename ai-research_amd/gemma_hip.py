@@ -61,6 +61,12 @@ _SIGS = {
     "gh_gemv_q4": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
     "gh_gemv_q8": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
     "gh_gate_up_geglu_q4": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32]),
+    "gh_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _u32, _f32]),
+    "gh_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _f32, _f32]),
+    "gh_qkv_rope": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                         _u32, _f32, _f32]),
+    "gh_decode_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _u32]),
+    "gh_argmax": (_i, [_vp, _vp, _vp, _u32]),
 }
 
 _lib = None
@@ -254,6 +260,29 @@ class Context:
     def gate_up_geglu_q4(self, Wg, Wu, X, Y, M, K):
         _check(lib().gh_gate_up_geglu_q4(self.h, _addr(Wg), _addr(Wu), _addr(X), _addr(Y), M, K),
                "gh_gate_up_geglu_q4")
+
+    def rmsnorm(self, X, W, Y, dim, eps=1e-6):
+        _check(lib().gh_rmsnorm(self.h, _addr(X), _addr(W), _addr(Y), dim, eps), "gh_rmsnorm")
+
+    def add_rmsnorm(self, X, R, W, Y, dim, eps=1e-6, scalar=1.0):
+        _check(lib().gh_add_rmsnorm(self.h, _addr(X), _addr(R), _addr(W), _addr(Y), dim, eps,
+                                    scalar), "gh_add_rmsnorm")
+
+    def qkv_rope(self, Q_in, K_in, V_in, Qn, Kn, Q_out, K_cache, V_cache, step, num_q, num_kv,
+                 head_dim, rotary_dim, k_eq_v, theta, eps=1e-6):
+        _check(lib().gh_qkv_rope(self.h, _addr(Q_in), _addr(K_in), _addr(V_in) if V_in else None,
+                                 _addr(Qn), _addr(Kn), _addr(Q_out), _addr(K_cache),
+                                 _addr(V_cache), _addr(step), num_q, num_kv, head_dim, rotary_dim,
+                                 int(k_eq_v), theta, eps), "gh_qkv_rope")
+
+    def decode_attn(self, Q, K_cache, V_cache, active, out, step, head_dim, kv_dim, gqa_ratio,
+                    num_q_heads, inv_sqrt_dim=1.0):
+        _check(lib().gh_decode_attn(self.h, _addr(Q), _addr(K_cache), _addr(V_cache),
+                                    _addr(active), _addr(out), _addr(step), head_dim, kv_dim,
+                                    gqa_ratio, inv_sqrt_dim, num_q_heads), "gh_decode_attn")
+
+    def argmax(self, logits, out_token, vocab):
+        _check(lib().gh_argmax(self.h, _addr(logits), _addr(out_token), vocab), "gh_argmax")
 
 
 def _addr(b):

@@ -130,6 +130,41 @@ gh_status gh_gemv_q8(gh_context *ctx, const void *W, const float *X, float *Y,
 gh_status gh_gate_up_geglu_q4(gh_context *ctx, const void *Wg, const void *Wu,
                               const float *X, float *Y, uint32_t M, uint32_t K);
 
+/* recordRmsNorm (kernels.zig:108-111), shaders/rmsnorm.wgsl:
+ * Y = X * (mean(X^2) + eps)^-1/2 * W.  Y may alias X. */
+gh_status gh_rmsnorm(gh_context *ctx, const float *X, const float *W, float *Y, uint32_t dim,
+                     float eps);
+/* recordAddRmsNorm (kernels.zig:100-103), shaders/add_rmsnorm.wgsl:
+ * X <- (X + R) * scalar in place, then Y = RMSNorm(X) * W. */
+gh_status gh_add_rmsnorm(gh_context *ctx, float *X, const float *R, const float *W, float *Y,
+                         uint32_t dim, float eps, float scalar);
+/* recordQkvRope (kernels.zig:124-129), shaders/qkv_rope.wgsl: per-head
+ * RMSNorm(q_norm) + split-half RoPE on the first rotary_dim dims of every
+ * query head (into Q_out, which may be Q_in); RMSNorm(k_norm) + RoPE of each
+ * key head into K_cache and unit-RMS of each value head (the raw key head when
+ * k_eq_v) into V_cache, both at row step_params[1] of [slot][num_kv*head_dim].
+ * step_params (device, u32) = {clock, slot_idx, S, 0}. */
+gh_status gh_qkv_rope(gh_context *ctx, const float *Q_in, const float *K_in, const float *V_in,
+                      const float *Q_norm, const float *K_norm, float *Q_out, float *K_cache,
+                      float *V_cache, const uint32_t *step_params, uint32_t num_q,
+                      uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim, uint32_t k_eq_v,
+                      float theta, float eps);
+/* recordDecodeAttn (kernels.zig:116-119), shaders/decode_attn.wgsl: for
+ * every query head h (kv head h / gqa_ratio), softmax over the S =
+ * step_params[2] active slots of inv_sqrt_dim * (Q[h] . K[slot]), then the
+ * weighted sum of V[slot].  The reference passes inv_sqrt_dim = 1.0
+ * (model/forward.zig:80).  kv_dim = (num_q_heads / gqa_ratio) * head_dim;
+ * head_dim % 4 == 0, <= 512; gqa_ratio <= 4.  The first call allocates the
+ * context's split-K scratch (do not make that call inside graph capture). */
+gh_status gh_decode_attn(gh_context *ctx, const float *Q, const float *K_cache,
+                         const float *V_cache, const uint32_t *active_slots, float *out,
+                         const uint32_t *step_params, uint32_t head_dim, uint32_t kv_dim,
+                         uint32_t gqa_ratio, float inv_sqrt_dim, uint32_t num_q_heads);
+/* recordArgmax (kernels.zig:139-142), shaders/argmax.wgsl, with the CPU
+ * path's tie rule (sampleArgmax, src/kernels.zig:164-174): the lowest index
+ * of the largest value.  out_token is a device u32. */
+gh_status gh_argmax(gh_context *ctx, const float *logits, uint32_t *out_token, uint32_t vocab);
+
 #ifdef __cplusplus
 }
 #endif

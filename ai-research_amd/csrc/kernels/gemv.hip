@@ -25,6 +25,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../common/stream_args.h"  // XPro
+
 #define GROUP_STRIDE 132  // floats per 128-element x group in LDS (+4 pad)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -173,7 +175,104 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 }
 
 // ------------------------------------------------------------------------
+// x prologue.  The decode step fuses the reference's separate norm
+// dispatches (src/gpu/model_dispatch.zig:21,32-34,39-41,122) into the GEMV
+// that consumes their output; every workgroup recomputes the (cheap) norm of
+// one hidden vector while its first weight loads are in flight.
+//   mode 0: x as given
+//   mode 1: RMSNorm(x) * w                                   (input / final norm)
+//   mode 2: xn = (x + r') * s with r' = RMSNorm(r) * wr (r as given when wr
+//           is null); workgroup 0 writes xn to xout (the residual stream);
+//           the GEMV consumes RMSNorm(xn) * w                  (add + norm)
+// Every norm is in * (mean(in^2) + eps)^-1/2 * w, as src/kernels.zig:46-52.
+// ------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+// Extra LDS (floats) the prologue needs beyond the padded x and block sums.
+__host__ __device__ constexpr uint32_t pro_extra_floats(uint32_t K) { return 2 * K + 16; }
+
+template <int NT>
+__device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs, float* bsum,
+                                            float* ext) {
+  if (p.mode == 0) {
+    stage_x<NT>(p.x, K, xs, bsum);
+    return;
+  }
+  float* xr = ext;          // [K] raw / combined x
+  float* rr = ext + K;      // [K] raw r
+  float* red = ext + 2 * K; // [16]
+  const uint32_t n4 = K >> 2;
+  constexpr uint32_t U = 4;
+  float ssx = 0.f, ssr = 0.f;
+  for (uint32_t base = 0; base < n4; base += NT * U) {
+    float4 vx[U], vr[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t i = base + u * NT + threadIdx.x;
+      if (i < n4) {
+        vx[u] = reinterpret_cast<const float4*>(p.x)[i];
+        if (p.mode == 2) vr[u] = reinterpret_cast<const float4*>(p.r)[i];
+      }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const uint32_t i = base + u * NT + threadIdx.x;
+      if (i < n4) {
+        reinterpret_cast<float4*>(xr)[i] = vx[u];
+        ssx += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
+        if (p.mode == 2) {
+          reinterpret_cast<float4*>(rr)[i] = vr[u];
+          ssr += vr[u].x * vr[u].x + vr[u].y * vr[u].y + vr[u].z * vr[u].z + vr[u].w * vr[u].w;
+        }
+      }
+    }
+  }
+  if (p.mode == 2) {
+    const float inv_r = 1.0f / sqrtf(block_sum<NT>(ssr, red) / (float)K + p.eps);
+    ssx = 0.f;
+    for (uint32_t i = threadIdx.x; i < K; i += NT) {
+      const float rv = p.wr ? rr[i] * inv_r * p.wr[i] : rr[i];
+      const float xn = (xr[i] + rv) * p.s;
+      xr[i] = xn;
+      ssx += xn * xn;
+      if (blockIdx.x == 0) p.xout[i] = xn;
+    }
+  }
+  const float inv = 1.0f / sqrtf(block_sum<NT>(ssx, red) / (float)K + p.eps);
+  for (uint32_t i = threadIdx.x; i < n4; i += NT) {
+    const uint32_t e = i << 2, g = e >> 7, o = e & 127;
+    const float4 wv = reinterpret_cast<const float4*>(p.w)[i];
+    float4 v;
+    v.x = xr[e] * inv * wv.x;
+    v.y = xr[e + 1] * inv * wv.y;
+    v.z = xr[e + 2] * inv * wv.z;
+    v.w = xr[e + 3] * inv * wv.w;
+    *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v;
+    float s = (v.x + v.y) + (v.z + v.w);
+    s += __shfl_xor(s, 1, 8);
+    s += __shfl_xor(s, 2, 8);
+    s += __shfl_xor(s, 4, 8);
+    if ((i & 7) == 0) bsum[i >> 3] = s;
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------------------
 // Weight formats: one "item" = one 4-block group of one row.
+// init() sets the whole accumulator, zero() resets it for the next row,
+// finish() reduces a row over its team, block_end() runs once per workgroup
+// after the stream (all threads).
 // ------------------------------------------------------------------------
 struct Q4Fmt {  // shaders/gemv_q4.wgsl
   static constexpr uint32_t kGroupBytes = 80, kBlockBytes = 20, kSub = 1;
@@ -190,16 +289,19 @@ struct Q4Fmt {  // shaders/gemv_q4.wgsl
   __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
     it.w = load_q4g(a.W + off);
   }
+  __device__ static void init(Acc& c) { c.s = 0.f; }
   __device__ static void zero(Acc& c) { c.s = 0.f; }
   __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
                              uint32_t) {
     c.s += valid * q4_group_dot(it.w, xg, bs);
   }
   template <int TPR>
-  __device__ static void finish(const Acc& c, const Args& a, uint32_t row, bool writer) {
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
     const float v = team_sum<TPR>(c.s);
     if (writer) a.Y[row] = v;
   }
+  template <int NT>
+  __device__ static void block_end(const Acc&, const Args&, float*) {}
 };
 
 struct GateUpFmt {  // shaders/fused_mlp_q4.wgsl: act = gelu_tanh(Wg x) * (Wu x)
@@ -221,6 +323,7 @@ struct GateUpFmt {  // shaders/fused_mlp_q4.wgsl: act = gelu_tanh(Wg x) * (Wu x)
   __device__ static void load(Item& it, const Args& a, size_t off, uint32_t sub) {
     it.w = load_q4g((sub ? a.Wu : a.Wg) + off);
   }
+  __device__ static void init(Acc& c) { c.g = c.u = 0.f; }
   __device__ static void zero(Acc& c) { c.g = c.u = 0.f; }
   __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
                              uint32_t sub) {
@@ -228,17 +331,43 @@ struct GateUpFmt {  // shaders/fused_mlp_q4.wgsl: act = gelu_tanh(Wg x) * (Wu x)
     if (sub) c.u += d; else c.g += d;
   }
   template <int TPR>
-  __device__ static void finish(const Acc& c, const Args& a, uint32_t row, bool writer) {
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
     const float g = team_sum<TPR>(c.g);
     const float u = team_sum<TPR>(c.u);
     if (writer) a.Y[row] = gelu_tanh(g) * u;
   }
+  template <int NT>
+  __device__ static void block_end(const Acc&, const Args&, float*) {}
 };
+
+struct Q8G {
+  u32x4 v[9];
+};
+
+__device__ __forceinline__ void load_q8g(Q8G& g, const uint8_t* p) {
+#pragma unroll
+  for (int k = 0; k < 9; k++) g.v[k] = ldw(p + 16 * k);
+}
+
+__device__ __forceinline__ float q8_group_dot(const Q8G& g, const float* xg, const float* bs) {
+  uint32_t w[36];
+#pragma unroll
+  for (int k = 0; k < 9; k++) {
+    w[4 * k + 0] = g.v[k].x;
+    w[4 * k + 1] = g.v[k].y;
+    w[4 * k + 2] = g.v[k].z;
+    w[4 * k + 3] = g.v[k].w;
+  }
+  float r = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) r += u2f(w[9 * j]) * (q8_ux(&w[9 * j + 1], xg + 32 * j) - 128.0f * bs[j]);
+  return r;
+}
 
 struct Q8Fmt {  // shaders/gemv_q8.wgsl
   static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 1;
   struct Item {
-    u32x4 v[9];
+    Q8G w;
   };
   struct Acc {
     float s;
@@ -248,29 +377,160 @@ struct Q8Fmt {  // shaders/gemv_q8.wgsl
     float* Y;
   };
   __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
-#pragma unroll
-    for (int k = 0; k < 9; k++) it.v[k] = ldw(a.W + off + 16 * k);
+    load_q8g(it.w, a.W + off);
+  }
+  __device__ static void init(Acc& c) { c.s = 0.f; }
+  __device__ static void zero(Acc& c) { c.s = 0.f; }
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
+                             uint32_t) {
+    c.s += valid * q8_group_dot(it.w, xg, bs);
+  }
+  template <int TPR>
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
+    const float v = team_sum<TPR>(c.s);
+    if (writer) a.Y[row] = v;
+  }
+  template <int NT>
+  __device__ static void block_end(const Acc&, const Args&, float*) {}
+};
+
+struct GateUpQ8Fmt {  // shaders/fused_mlp_q8.wgsl (--q8 layers)
+  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 2;
+  struct Item {
+    Q8G w;
+  };
+  using Acc = GateUpFmt::Acc;
+  using Args = GateUpFmt::Args;
+  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t sub) {
+    load_q8g(it.w, (sub ? a.Wu : a.Wg) + off);
+  }
+  __device__ static void init(Acc& c) { c.g = c.u = 0.f; }
+  __device__ static void zero(Acc& c) { c.g = c.u = 0.f; }
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
+                             uint32_t sub) {
+    const float d = valid * q8_group_dot(it.w, xg, bs);
+    if (sub) c.u += d; else c.g += d;
+  }
+  template <int TPR>
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
+    GateUpFmt::finish<TPR>(c, a, row, writer);
+  }
+  template <int NT>
+  __device__ static void block_end(const Acc&, const Args&, float*) {}
+};
+
+// (value, index) order of the greedy pick: larger value wins, equal values go
+// to the smaller index (src/kernels.zig:164-174).
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Q8_0 vocab projection with the argmax fused in (shaders/gemv_q8.wgsl then
+// shaders/argmax.wgsl, src/gpu/model_dispatch.zig:124-126): every lane keeps
+// the best (logit, row) of its team's rows; block_end reduces the block,
+// writes one partial, and the last block to finish reduces the partials in
+// block order and writes the token.  Logits are stored only when Y != null.
+struct Q8ArgmaxFmt {
+  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 1;
+  using Item = Q8Fmt::Item;
+  struct Acc {
+    float s, bv;
+    uint32_t bi;
+  };
+  struct Args {
+    const uint8_t* W;
+    float* Y;
+    uint32_t* partial;  // 2 words per block
+    uint32_t* counter;  // zero between launches
+    uint32_t* token;
+  };
+  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
+    load_q8g(it.w, a.W + off);
+  }
+  __device__ static void init(Acc& c) {
+    c.s = 0.f;
+    c.bv = -INFINITY;
+    c.bi = 0xFFFFFFFFu;
   }
   __device__ static void zero(Acc& c) { c.s = 0.f; }
   __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
                              uint32_t) {
-    uint32_t w[36];
-#pragma unroll
-    for (int k = 0; k < 9; k++) {
-      w[4 * k + 0] = it.v[k].x;
-      w[4 * k + 1] = it.v[k].y;
-      w[4 * k + 2] = it.v[k].z;
-      w[4 * k + 3] = it.v[k].w;
-    }
-    float r = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) r += u2f(w[9 * j]) * (q8_ux(&w[9 * j + 1], xg + 32 * j) - 128.0f * bs[j]);
-    c.s += valid * r;
+    c.s += valid * q8_group_dot(it.w, xg, bs);
   }
   template <int TPR>
-  __device__ static void finish(const Acc& c, const Args& a, uint32_t row, bool writer) {
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
     const float v = team_sum<TPR>(c.s);
-    if (writer) a.Y[row] = v;
+    if (a.Y && writer) a.Y[row] = v;
+    if (better(v, row, c.bv, c.bi)) {
+      c.bv = v;
+      c.bi = row;
+    }
+  }
+  __device__ static void wave_best(float& v, uint32_t& i) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(v, off, 64);
+      const uint32_t oi = __shfl_xor(i, off, 64);
+      if (better(ov, oi, v, i)) {
+        v = ov;
+        i = oi;
+      }
+    }
+  }
+  template <int NT>
+  __device__ static void block_end(const Acc& c, const Args& a, float* red) {
+    constexpr int W = NT / 64;
+    float* rv = red;
+    uint32_t* ri = reinterpret_cast<uint32_t*>(red + W);
+    uint32_t* last = ri + W;
+    float bv = c.bv;
+    uint32_t bi = c.bi;
+    wave_best(bv, bi);
+    if ((threadIdx.x & 63) == 0) {
+      rv[threadIdx.x >> 6] = bv;
+      ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < W; w++)
+        if (better(rv[w], ri[w], bv, bi)) {
+          bv = rv[w];
+          bi = ri[w];
+        }
+      a.partial[2 * blockIdx.x] = __float_as_uint(bv);
+      a.partial[2 * blockIdx.x + 1] = bi;
+      __threadfence();
+      last[0] = (atomicAdd(a.counter, 1u) == gridDim.x - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last[0]) return;
+    __threadfence();
+    bv = -INFINITY;
+    bi = 0xFFFFFFFFu;
+    for (uint32_t b = threadIdx.x; b < gridDim.x; b += NT) {
+      const float v = __uint_as_float(__builtin_nontemporal_load(&a.partial[2 * b]));
+      const uint32_t i = __builtin_nontemporal_load(&a.partial[2 * b + 1]);
+      if (better(v, i, bv, bi)) {
+        bv = v;
+        bi = i;
+      }
+    }
+    wave_best(bv, bi);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+      rv[threadIdx.x >> 6] = bv;
+      ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < W; w++)
+        if (better(rv[w], ri[w], bv, bi)) {
+          bv = rv[w];
+          bi = ri[w];
+        }
+      a.token[0] = bi == 0xFFFFFFFFu ? 0u : bi;
+      a.counter[0] = 0;
+    }
   }
 };
 
@@ -283,21 +543,22 @@ struct Q8Fmt {  // shaders/gemv_q8.wgsl
 // traffic outstanding through its compute.  The ring is unrolled so no
 // register copies (which would force an early wait) are needed.  Items past
 // the end (group >= ng, or look-ahead beyond the last row) load an in-range
-// duplicate and contribute zero.
+// duplicate and contribute zero.  Teams with no rows skip the stream but
+// still take part in the block-wide prologue and epilogue.
 // ------------------------------------------------------------------------
 template <class F, int TPR, int GPL, int D, int NT>
-__device__ __forceinline__ void stream_rows(const typename F::Args& a, const float* __restrict__ X,
-                                            uint32_t M, uint32_t K) {
+__device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
+                                            uint32_t K) {
   extern __shared__ float lds[];
   const uint32_t nb = K >> 5, ng = nb >> 2;
   float* xs = lds;
   float* bsum = lds + ng * GROUP_STRIDE;
+  float* ext = bsum + nb;  // prologue scratch / epilogue reduction space
 
   constexpr uint32_t TEAMS = NT / TPR;
   const uint32_t lr = threadIdx.x % TPR;
   const uint32_t team = blockIdx.x * TEAMS + threadIdx.x / TPR;
   const uint32_t nteams = gridDim.x * TEAMS;
-  // Idle teams (team >= M) still stage x with the block, then exit.
   const bool active = team < M;
   constexpr uint32_t PER_ROW = GPL * F::kSub;  // items per row for one lane
   const uint32_t n_items = active ? ((M - 1 - team) / nteams + 1) * PER_ROW : 0;
@@ -321,10 +582,9 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const flo
 #pragma unroll
     for (int d = 0; d < D; d++) F::load(buf[d], a, offset_of(d), d % F::kSub);
   }
-  stage_x<NT>(X, K, xs, bsum);
-  if (!active) return;
+  stage_x_pro<NT>(xp, K, xs, bsum, ext);
   typename F::Acc acc;
-  F::zero(acc);
+  F::init(acc);
   for (uint32_t base = 0; base < n_items; base += D) {
 #pragma unroll
     for (int d = 0; d < D; d++) {
@@ -342,26 +602,34 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const flo
       F::load(buf[d], a, offset_of(i + D), (i + D) % F::kSub);
     }
   }
+  F::template block_end<NT>(acc, a, ext);
 }
 
-#define GH_GEMV_INST(T, G, D)                                                                   \
-  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q4_t##T##_g##G##_d##D(               \
-      const uint8_t* W, const float* X, float* Y, uint32_t M, uint32_t K) {                       \
-    stream_rows<Q4Fmt, T, G, D, 256>(Q4Fmt::Args{W, Y}, X, M, K);                                \
-  }                                                                                               \
-  extern "C" __global__ __launch_bounds__(256) void gh_gateup_q4_t##T##_g##G##_d##D(             \
-      const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y, uint32_t M, uint32_t K) {   \
-    stream_rows<GateUpFmt, T, G, D, 256>(GateUpFmt::Args{Wg, Wu, Y}, X, M, K);                   \
-  }                                                                                               \
-  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q8_t##T##_g##G##_d##D(               \
-      const uint8_t* W, const float* X, float* Y, uint32_t M, uint32_t K) {                       \
-    stream_rows<Q8Fmt, T, G, D, 256>(Q8Fmt::Args{W, Y}, X, M, K);                                \
+#define GH_GEMV_INST(T, G, D)                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q4_t##T##_g##G##_d##D(              \
+      Q4Fmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                        \
+    stream_rows<Q4Fmt, T, G, D, 256>(a, xp, M, K);                                             \
+  }                                                                                            \
+  extern "C" __global__ __launch_bounds__(256) void gh_gateup_q4_t##T##_g##G##_d##D(            \
+      GateUpFmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                    \
+    stream_rows<GateUpFmt, T, G, D, 256>(a, xp, M, K);                                         \
+  }                                                                                            \
+  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q8_t##T##_g##G##_d##D(              \
+      Q8Fmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                        \
+    stream_rows<Q8Fmt, T, G, D, 256>(a, xp, M, K);                                             \
+  }                                                                                            \
+  extern "C" __global__ __launch_bounds__(256) void gh_gateup_q8_t##T##_g##G##_d##D(            \
+      GateUpQ8Fmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                  \
+    stream_rows<GateUpQ8Fmt, T, G, D, 256>(a, xp, M, K);                                       \
+  }                                                                                            \
+  extern "C" __global__ __launch_bounds__(256) void gh_argmax_q8_t##T##_g##G##_d##D(            \
+      Q8ArgmaxFmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                  \
+    stream_rows<Q8ArgmaxFmt, T, G, D, 256>(a, xp, M, K);                                       \
   }
 
 #define GH_GEMV_INST_D(T, G) \
   GH_GEMV_INST(T, G, 2)      \
-  GH_GEMV_INST(T, G, 3)      \
-  GH_GEMV_INST(T, G, 4)
+  GH_GEMV_INST(T, G, 3)
 
 GH_GEMV_INST_D(8, 1)
 GH_GEMV_INST_D(8, 2)

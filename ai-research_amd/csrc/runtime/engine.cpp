@@ -6,10 +6,14 @@
 #include <string>
 
 #include "runtime.hpp"
+#include "../common/stream_args.h"
 
 using gh::fail;
 
 namespace {
+
+constexpr uint32_t kArgmaxMaxBlocks = 4096;
+constexpr size_t kArgmaxScratchBytes = (64 + 2 * kArgmaxMaxBlocks) * 4;
 
 struct GemvCfg {
   int tpr, gpl, wgs_per_cu, depth;
@@ -55,7 +59,7 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K) {
 
 unsigned x_lds_bytes(uint32_t K) { return (K / 128) * 132 * 4 + (K / 32) * 4; }
 
-gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const float* Y,
+gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const void* Y,
                      uint32_t M, uint32_t K, const char* who) {
   if (!ctx || !W || !X || !Y) return fail(GH_ERR_INVALID, std::string(who) + ": null pointer");
   if (M == 0 || K == 0) return fail(GH_ERR_INVALID, std::string(who) + ": M or K is zero");
@@ -70,14 +74,68 @@ gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const
   return GH_OK;
 }
 
-gh_status launch_gemv(gh_context* ctx, const char* family, void** args, uint32_t M, uint32_t K) {
+}  // namespace
+
+namespace gh {
+
+gh_status launch_stream(gh_context* ctx, const char* family, void* fmt_args, const XPro& xp,
+                        uint32_t M, uint32_t K) {
   GemvCfg c = pick_gemv(ctx, M, K);
   const uint32_t teams_per_wg = 256 / c.tpr;
   const uint32_t max_grid = (M + teams_per_wg - 1) / teams_per_wg;
   const unsigned grid = std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * c.wgs_per_cu);
+  const unsigned lds = x_lds_bytes(K) + (xp.mode ? (2 * K + 16) * 4 : 64);
+  if (lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
   std::string name = std::string(family) + "_t" + std::to_string(c.tpr) + "_g" +
                      std::to_string(c.gpl) + "_d" + std::to_string(c.depth);
-  return ctx->launch(name, dim3(grid), dim3(256), x_lds_bytes(K), args);
+  XPro xpc = xp;
+  void* args[] = {fmt_args, &xpc, &M, &K};
+  return ctx->launch(name, dim3(grid), dim3(256), lds, args);
+}
+
+unsigned stream_grid(const gh_context* ctx, uint32_t M, uint32_t K) {
+  GemvCfg c = pick_gemv(ctx, M, K);
+  const uint32_t teams_per_wg = 256 / c.tpr;
+  const uint32_t max_grid = (M + teams_per_wg - 1) / teams_per_wg;
+  return std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * c.wgs_per_cu);
+}
+
+gh_status check_pro(const gh_context* ctx, const XPro& p, uint32_t K, const char* who) {
+  if (p.mode > 2) return fail(GH_ERR_INVALID, std::string(who) + ": prologue mode must be 0..2");
+  if (!p.x || (reinterpret_cast<uintptr_t>(p.x) & 15))
+    return fail(GH_ERR_INVALID, std::string(who) + ": x null or not 16-byte aligned");
+  if (p.mode >= 1 && (!p.w || (reinterpret_cast<uintptr_t>(p.w) & 15)))
+    return fail(GH_ERR_INVALID, std::string(who) + ": norm weight null or misaligned");
+  if (p.mode == 2 && (!p.r || !p.xout || (reinterpret_cast<uintptr_t>(p.r) & 15)))
+    return fail(GH_ERR_INVALID, std::string(who) + ": residual input/output null or misaligned");
+  (void)ctx;
+  (void)K;
+  return GH_OK;
+}
+
+}  // namespace gh
+
+namespace {
+using gh::launch_stream;
+
+XPro plain_x(const float* X) {
+  XPro p{};
+  p.x = X;
+  p.mode = 0;
+  return p;
+}
+
+XPro from_abi(const gh_xprologue* q) {
+  XPro p{};
+  p.x = q->x;
+  p.r = q->r;
+  p.wr = q->r_norm;
+  p.w = q->norm;
+  p.xout = q->x_out;
+  p.s = q->scalar;
+  p.eps = q->eps;
+  p.mode = q->mode;
+  return p;
 }
 
 }  // namespace
@@ -88,16 +146,16 @@ gh_status gh_gemv_q4(gh_context* ctx, const void* W, const float* X, float* Y, u
                      uint32_t K) {
   gh_status st = check_gemv(ctx, W, X, Y, M, K, "gh_gemv_q4");
   if (st != GH_OK) return st;
-  void* args[] = {const_cast<void**>(&W), const_cast<float**>(&X), &Y, &M, &K};
-  return launch_gemv(ctx, "gh_gemv_q4", args, M, K);
+  Q4Args a{static_cast<const uint8_t*>(W), Y};
+  return launch_stream(ctx, "gh_gemv_q4", &a, plain_x(X), M, K);
 }
 
 gh_status gh_gemv_q8(gh_context* ctx, const void* W, const float* X, float* Y, uint32_t M,
                      uint32_t K) {
   gh_status st = check_gemv(ctx, W, X, Y, M, K, "gh_gemv_q8");
   if (st != GH_OK) return st;
-  void* args[] = {const_cast<void**>(&W), const_cast<float**>(&X), &Y, &M, &K};
-  return launch_gemv(ctx, "gh_gemv_q8", args, M, K);
+  Q4Args a{static_cast<const uint8_t*>(W), Y};
+  return launch_stream(ctx, "gh_gemv_q8", &a, plain_x(X), M, K);
 }
 
 gh_status gh_gate_up_geglu_q4(gh_context* ctx, const void* Wg, const void* Wu, const float* X,
@@ -106,9 +164,54 @@ gh_status gh_gate_up_geglu_q4(gh_context* ctx, const void* Wg, const void* Wu, c
   if (st != GH_OK) return st;
   if (!Wu || (reinterpret_cast<uintptr_t>(Wu) & 15))
     return fail(GH_ERR_INVALID, "gh_gate_up_geglu_q4: Wu null or misaligned");
-  void* args[] = {const_cast<void**>(&Wg), const_cast<void**>(&Wu), const_cast<float**>(&X), &Y,
-                  &M, &K};
-  return launch_gemv(ctx, "gh_gateup_q4", args, M, K);
+  GateUpArgs a{static_cast<const uint8_t*>(Wg), static_cast<const uint8_t*>(Wu), Y};
+  return launch_stream(ctx, "gh_gateup_q4", &a, plain_x(X), M, K);
+}
+
+gh_status gh_norm_gemv(gh_context* ctx, gh_quant_mode mode, const void* W, float* Y, uint32_t M,
+                       uint32_t K, const gh_xprologue* pro) {
+  if (!pro) return fail(GH_ERR_INVALID, "gh_norm_gemv: prologue is null");
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
+    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gemv: mode must be Q4 or Q8");
+  gh_status st = check_gemv(ctx, W, pro->x, Y, M, K, "gh_norm_gemv");
+  if (st != GH_OK) return st;
+  XPro p = from_abi(pro);
+  if ((st = gh::check_pro(ctx, p, K, "gh_norm_gemv")) != GH_OK) return st;
+  Q4Args a{static_cast<const uint8_t*>(W), Y};
+  return launch_stream(ctx, mode == GH_QUANT_Q4 ? "gh_gemv_q4" : "gh_gemv_q8", &a, p, M, K);
+}
+
+gh_status gh_norm_gate_up_geglu(gh_context* ctx, gh_quant_mode mode, const void* Wg,
+                                const void* Wu, float* Y, uint32_t M, uint32_t K,
+                                const gh_xprologue* pro) {
+  if (!pro) return fail(GH_ERR_INVALID, "gh_norm_gate_up_geglu: prologue is null");
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
+    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gate_up_geglu: mode must be Q4 or Q8");
+  gh_status st = check_gemv(ctx, Wg, pro->x, Y, M, K, "gh_norm_gate_up_geglu");
+  if (st != GH_OK) return st;
+  if (!Wu || (reinterpret_cast<uintptr_t>(Wu) & 15))
+    return fail(GH_ERR_INVALID, "gh_norm_gate_up_geglu: Wu null or misaligned");
+  XPro p = from_abi(pro);
+  if ((st = gh::check_pro(ctx, p, K, "gh_norm_gate_up_geglu")) != GH_OK) return st;
+  GateUpArgs a{static_cast<const uint8_t*>(Wg), static_cast<const uint8_t*>(Wu), Y};
+  return launch_stream(ctx, mode == GH_QUANT_Q4 ? "gh_gateup_q4" : "gh_gateup_q8", &a, p, M, K);
+}
+
+gh_status gh_norm_gemv_argmax_q8(gh_context* ctx, const void* W, float* logits,
+                                 uint32_t* token, uint32_t M, uint32_t K,
+                                 const gh_xprologue* pro) {
+  if (!pro || !token) return fail(GH_ERR_INVALID, "gh_norm_gemv_argmax_q8: null argument");
+  gh_status st = check_gemv(ctx, W, pro->x, token, M, K, "gh_norm_gemv_argmax_q8");
+  if (st != GH_OK) return st;
+  XPro p = from_abi(pro);
+  if ((st = gh::check_pro(ctx, p, K, "gh_norm_gemv_argmax_q8")) != GH_OK) return st;
+  st = ctx->ensure_zeroed(&ctx->argmax_scratch, &ctx->argmax_scratch_bytes, kArgmaxScratchBytes);
+  if (st != GH_OK) return st;
+  uint32_t* base = static_cast<uint32_t*>(ctx->argmax_scratch);
+  ArgmaxArgs a{static_cast<const uint8_t*>(W), logits, base + 64, base, token};
+  if (gh::stream_grid(ctx, M, K) > kArgmaxMaxBlocks)
+    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gemv_argmax_q8: grid too large");
+  return launch_stream(ctx, "gh_argmax_q8", &a, p, M, K);
 }
 
 gh_status gh_rmsnorm(gh_context* ctx, const float* X, const float* W, float* Y, uint32_t dim,
@@ -218,10 +321,10 @@ gh_status gh_argmax(gh_context* ctx, const float* logits, uint32_t* out_token, u
     return fail(GH_ERR_INVALID, "gh_argmax: bad argument");
   const uint32_t grid = std::min<uint32_t>(256u, (vocab + 1023) / 1024);
   gh_status st = ctx->ensure_zeroed(&ctx->argmax_scratch, &ctx->argmax_scratch_bytes,
-                                    (2 * 256 + 64) * 4);
+                                    kArgmaxScratchBytes);
   if (st != GH_OK) return st;
-  uint32_t* partial = static_cast<uint32_t*>(ctx->argmax_scratch);
-  uint32_t* counter = partial + 2 * 256;
+  uint32_t* counter = static_cast<uint32_t*>(ctx->argmax_scratch);
+  uint32_t* partial = counter + 64;
   void* args[] = {const_cast<float**>(&logits), &vocab, &out_token, &partial, &counter};
   return ctx->launch("gh_argmax_k", dim3(grid), dim3(256), 0, args);
 }

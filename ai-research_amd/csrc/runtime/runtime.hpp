@@ -35,6 +35,7 @@ struct gh_context {
 };
 
 #include "../common/attn_args.h"
+#include "../common/stream_args.h"
 
 namespace gh {
 using Context = gh_context;
@@ -42,6 +43,12 @@ struct AttnLaunch {
   AttnArgs args;
 };
 gh_status launch_attention(gh_context* ctx, const AttnLaunch& L);
+// Row-stream GEMV launch (gemv.hip); family = gh_gemv_q4, gh_gemv_q8,
+// gh_gateup_q4, gh_gateup_q8 or gh_argmax_q8; fmt_args points at the
+// family's argument block.
+gh_status launch_stream(gh_context* ctx, const char* family, void* fmt_args, const XPro& xp,
+                        uint32_t M, uint32_t K);
+unsigned stream_grid(const gh_context* ctx, uint32_t M, uint32_t K);
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);

@@ -69,6 +69,18 @@ _SIGS = {
     "gh_argmax": (_i, [_vp, _vp, _vp, _u32]),
 }
 
+class XPrologue(C.Structure):
+    """gh_xprologue: the x prologue of the fused GEMV entry points."""
+    _fields_ = [("x", _vp), ("r", _vp), ("r_norm", _vp), ("norm", _vp), ("x_out", _vp),
+                ("scalar", _f32), ("eps", _f32), ("mode", _u32)]
+
+
+_SIGS.update({
+    "gh_norm_gemv": (_i, [_vp, _i, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
+    "gh_norm_gate_up_geglu": (_i, [_vp, _i, _vp, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
+    "gh_norm_gemv_argmax_q8": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
+})
+
 _lib = None
 
 
@@ -260,6 +272,24 @@ class Context:
     def gate_up_geglu_q4(self, Wg, Wu, X, Y, M, K):
         _check(lib().gh_gate_up_geglu_q4(self.h, _addr(Wg), _addr(Wu), _addr(X), _addr(Y), M, K),
                "gh_gate_up_geglu_q4")
+
+    @staticmethod
+    def prologue(x, mode=0, norm=None, r=None, r_norm=None, x_out=None, scalar=1.0, eps=1e-6):
+        a = lambda b: _addr(b) if b is not None else None  # noqa: E731
+        return XPrologue(a(x), a(r), a(r_norm), a(norm), a(x_out), scalar, eps, mode)
+
+    def norm_gemv(self, quant, W, Y, M, K, pro):
+        _check(lib().gh_norm_gemv(self.h, quant, _addr(W), _addr(Y), M, K, C.byref(pro)),
+               "gh_norm_gemv")
+
+    def norm_gate_up_geglu(self, quant, Wg, Wu, Y, M, K, pro):
+        _check(lib().gh_norm_gate_up_geglu(self.h, quant, _addr(Wg), _addr(Wu), _addr(Y), M, K,
+                                           C.byref(pro)), "gh_norm_gate_up_geglu")
+
+    def norm_gemv_argmax_q8(self, W, logits, token, M, K, pro):
+        _check(lib().gh_norm_gemv_argmax_q8(self.h, _addr(W), _addr(logits) if logits else None,
+                                            _addr(token), M, K, C.byref(pro)),
+               "gh_norm_gemv_argmax_q8")
 
     def rmsnorm(self, X, W, Y, dim, eps=1e-6):
         _check(lib().gh_rmsnorm(self.h, _addr(X), _addr(W), _addr(Y), dim, eps), "gh_rmsnorm")

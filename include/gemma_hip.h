@@ -130,6 +130,37 @@ gh_status gh_gemv_q8(gh_context *ctx, const void *W, const float *X, float *Y,
 gh_status gh_gate_up_geglu_q4(gh_context *ctx, const void *Wg, const void *Wu,
                               const float *X, float *Y, uint32_t M, uint32_t K);
 
+/* ---- fused decode building blocks (no single reference counterpart: each
+ * fuses a norm dispatch into the GEMV that consumes it) ---------------------
+ * The x prologue every workgroup applies before the GEMV:
+ *   mode 0: x as given
+ *   mode 1: RMSNorm(x) * norm                               (recordRmsNorm)
+ *   mode 2: xn = (x + r') * scalar, r' = RMSNorm(r) * r_norm (r as given when
+ *           r_norm is null), xn written to x_out, then RMSNorm(xn) * norm
+ *           (recordRmsNorm of the post norm + recordAddRmsNorm,
+ *            src/gpu/model_dispatch.zig:32-34,39-41)
+ * All vectors have K floats, 16-byte aligned; x_out must not alias x or r. */
+typedef struct gh_xprologue {
+  const float *x, *r, *r_norm, *norm;
+  float *x_out;
+  float scalar, eps;
+  uint32_t mode;
+} gh_xprologue;
+/* Y = W . prologue(x) with Q4_0 or Q8_0 rows (recordRmsNorm + recordGemv). */
+gh_status gh_norm_gemv(gh_context *ctx, gh_quant_mode mode, const void *W, float *Y, uint32_t M,
+                       uint32_t K, const gh_xprologue *pro);
+/* Y = gelu_tanh(Wg . x) * (Wu . x), x = prologue (recordAddRmsNorm +
+ * recordGateUpSwiGlu). */
+gh_status gh_norm_gate_up_geglu(gh_context *ctx, gh_quant_mode mode, const void *Wg,
+                                const void *Wu, float *Y, uint32_t M, uint32_t K,
+                                const gh_xprologue *pro);
+/* Q8_0 vocab projection of prologue(x) with the greedy argmax fused in
+ * (recordRmsNorm + recordGemvLogits + recordArgmax, model_dispatch.zig:121-127);
+ * *token (device u32) gets the lowest index of the largest logit; logits
+ * (device, M floats) are written when non-null. */
+gh_status gh_norm_gemv_argmax_q8(gh_context *ctx, const void *W, float *logits, uint32_t *token,
+                                 uint32_t M, uint32_t K, const gh_xprologue *pro);
+
 /* recordRmsNorm (kernels.zig:108-111), shaders/rmsnorm.wgsl:
  * Y = X * (mean(X^2) + eps)^-1/2 * W.  Y may alias X. */
 gh_status gh_rmsnorm(gh_context *ctx, const float *X, const float *W, float *Y, uint32_t dim,

@@ -152,3 +152,73 @@ def test_gate_up_geglu_q4_parity(gpu, M, K):
     Wg, Wu, X, Y = gpu.upload(wg), gpu.upload(wu), gpu.upload(x), gpu.alloc(M * 4)
     gpu.gate_up_geglu_q4(Wg, Wu, X, Y, M, K)
     assert_close(Y.read(np.float32, M), ref, what="gate_up %dx%d" % (M, K))
+
+
+# ------------------------------------------------ fused prologue / epilogue --
+def _bf16r(a):
+    return nr.bf16_to_f32(nr.bf16_rne(a))
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("with_rnorm", [True, False])
+def test_norm_gemv_prologues(gpu, mode, with_rnorm):
+    # mode 1: input RMSNorm fused in; mode 2: post-FFN norm of r, residual add
+    # with layer_scalar, then the next input norm (model_dispatch.zig:39-41, 21)
+    M, K = 2048, 3840
+    wq = q4_weights(M, K, 0, 4000)
+    x = gh.synth_normal(K, 0, 41, 0.0, 2.0)
+    r = gh.synth_normal(K, 0, 42, 0.0, 1.0)
+    wn = _bf16r(gh.synth_normal(K, 0, 43, 1.0, 0.1))
+    wr = _bf16r(gh.synth_normal(K, 0, 44, 1.0, 0.1))
+    s = np.float32(0.875)
+    X, R, WN, WR, XO, Y = (gpu.upload(x), gpu.upload(r), gpu.upload(wn), gpu.upload(wr),
+                           gpu.alloc(K * 4), gpu.alloc(M * 4))
+    if mode == 1:
+        pro = gpu.prologue(X, 1, norm=WN)
+        xin = orc.rmsnorm(x, wn)
+    else:
+        pro = gpu.prologue(X, 2, norm=WN, r=R, r_norm=WR if with_rnorm else None, x_out=XO,
+                           scalar=float(s))
+        rr = orc.rmsnorm(r, wr) if with_rnorm else r
+        xn = ((x + rr) * s).astype(np.float32)
+        xin = orc.rmsnorm(xn, wn)
+    gpu.norm_gemv(gh.QUANT_Q4, gpu.upload(wq), Y, M, K, pro)
+    assert_close(Y.read(np.float32, M), orc.gemv_q4(wq, xin, K, NT), what="norm_gemv mode %d" % mode)
+    if mode == 2:
+        assert_close(XO.read(np.float32, K), xn, what="residual stream")
+
+
+def test_norm_gate_up_matches_oracle(gpu):
+    M, K = 15360, 3840
+    wg, wu = q4_weights(M, K, 0, 4100), q4_weights(M, K, 0, 4101)
+    x = gh.synth_normal(K, 0, 45, 0.0, 1.0)
+    r = gh.synth_normal(K, 0, 46, 0.0, 1.0)
+    wn = _bf16r(gh.synth_normal(K, 0, 47, 1.0, 0.1))
+    wr = _bf16r(gh.synth_normal(K, 0, 48, 1.0, 0.1))
+    X, R, WN, WR, XO, Y = (gpu.upload(x), gpu.upload(r), gpu.upload(wn), gpu.upload(wr),
+                           gpu.alloc(K * 4), gpu.alloc(M * 4))
+    pro = gpu.prologue(X, 2, norm=WN, r=R, r_norm=WR, x_out=XO, scalar=1.0)
+    gpu.norm_gate_up_geglu(gh.QUANT_Q4, gpu.upload(wg), gpu.upload(wu), Y, M, K, pro)
+    xn = (x + orc.rmsnorm(r, wr)).astype(np.float32)
+    ref = orc.gate_up_geglu_q4(orc.rmsnorm(xn, wn), wg, wu, NT)
+    assert_close(Y.read(np.float32, M), ref, what="norm gate_up")
+
+
+@pytest.mark.parametrize("V", [262144, 50000, 1000])
+def test_norm_gemv_argmax_q8(gpu, V):
+    H = 3840
+    w = gh.synth_normal(V * H, 0, 4200, 0.0, 0.02, bf16=True).reshape(V, H)
+    wq = orc.quantize_q8(w, NT)
+    x = gh.synth_normal(H, 0, 49, 0.0, 1.0)
+    wn = _bf16r(gh.synth_normal(H, 0, 50, 1.0, 0.1))
+    W, X, WN, L, T = gpu.upload(wq), gpu.upload(x), gpu.upload(wn), gpu.alloc(V * 4), gpu.alloc(4)
+    pro = gpu.prologue(X, 1, norm=WN)
+    gpu.norm_gemv_argmax_q8(W, L, T, V, H, pro)
+    logits = L.read(np.float32, V)
+    ref = orc.gemv_q8(wq, orc.rmsnorm(x, wn), H, NT)
+    assert_close(logits, ref, what="head logits")
+    tok = int(T.read(np.uint32, 1)[0])
+    assert tok == orc.argmax(logits)  # bit-exact pick over the logits it produced
+    assert tok == orc.argmax(ref) or ref[tok] >= np.max(ref) - 1e-5 * np.max(np.abs(ref))
+    gpu.norm_gemv_argmax_q8(W, None, T, V, H, pro)  # without materialised logits
+    assert int(T.read(np.uint32, 1)[0]) == tok

@@ -25,7 +25,7 @@ DEVICE_FLAGS = ["--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-
 
 KERNEL_FAMILIES = ["gemv", "util", "attn", "norm", "prefill"]
 
-HOST_SOURCES = ["runtime.cpp", "engine.cpp", "model.cpp"]
+HOST_SOURCES = ["runtime.cpp", "engine.cpp", "model.cpp", "ring.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-pthread", "-ffp-contract=off",
               "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
               "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),

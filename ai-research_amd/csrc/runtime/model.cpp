@@ -1,0 +1,693 @@
+// model.cpp -- the model-level C ABI: GpuModelContext.init/deinit and
+// gpuDispatchForwardToken (src/gpu/model_gpu.zig:35-197,
+// src/gpu/model_dispatch.zig:103-147) on one MI355X.
+//
+// HBM layout: one arena holding, per layer, the concatenated [q | k | v]
+// rows (one GEMV for the three projections), o, gate, up and down in the
+// reference's quant.zig blocks, the norms widened to f32, and the per-layer
+// K/V ring caches [max_slots][kv_dim]; then the Q8_0 LM head, the final
+// norm and the activations.  The per-token graph (5 kernels a layer + the LM
+// head) is captured once into a HIP graph with the small host->device copies
+// of x, the active list and the step parameters, and replayed per token.
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+#include <vector>
+
+#include "../common/attn_args.h"
+#include "../common/stream_args.h"
+#include "../common/synth.h"
+#include "runtime.hpp"
+
+using gh::fail;
+using gh::hip_fail;
+
+namespace {
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct Layer {
+  bool full;
+  uint32_t head_dim, rot, nkv, q_dim, kv_dim, qkv_rows;
+  bool k_eq_v;
+  float theta, scalar;
+  size_t qkv, o, gate, up, down;                   // arena offsets (bytes)
+  size_t input_norm, q_norm, k_norm, post_attn, pre_ffn, post_ffn;  // SIZE_MAX = absent
+  size_t k_cache, v_cache;
+};
+
+constexpr size_t kNone = ~(size_t)0;
+
+}  // namespace
+
+struct gh_model {
+  gh_context* ctx = nullptr;
+  gh_model_config cfg{};
+  gh_quant_mode mode = GH_QUANT_Q4;
+  std::vector<Layer> layers;
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
+  size_t lm_head = 0, final_norm = 0;
+  size_t x0 = 0, x1 = 0, qkv_out = 0, attn_out = 0, o_out = 0, act = 0, m_out = 0, logits = 0;
+  size_t token = 0, step = 0, active = 0, attn_part = 0, attn_cnt = 0, amax = 0;
+  uint32_t nsplit = 1, max_q = 0, max_kv = 0;
+  size_t hidden_final = 0;       // which x buffer holds the residual stream after a step
+  uint16_t* embed_dev = nullptr; // synthetic models only
+  // pinned host staging for the per-token copies
+  float* h_x = nullptr;
+  uint32_t* h_active = nullptr;
+  uint32_t* h_step = nullptr;
+  uint32_t* h_token = nullptr;
+  void* graph_decode = nullptr;
+  void* graph_prefill = nullptr;
+
+  template <typename T>
+  T* at(size_t off) const {
+    return reinterpret_cast<T*>(arena + off);
+  }
+  size_t row_bytes(uint32_t cols) const {
+    return (size_t)(cols / 32) * (mode == GH_QUANT_Q8 ? 36 : 20);
+  }
+  ~gh_model();
+};
+
+gh_model::~gh_model() {
+  if (ctx && ctx->stream) hipStreamSynchronize(ctx->stream);
+  if (graph_decode) gh_graph_destroy(graph_decode);
+  if (graph_prefill) gh_graph_destroy(graph_prefill);
+  if (arena) hipFree(arena);
+  if (embed_dev) hipFree(embed_dev);
+  if (h_x) hipHostFree(h_x);
+  if (h_active) hipHostFree(h_active);
+  if (h_step) hipHostFree(h_step);
+  if (h_token) hipHostFree(h_token);
+}
+
+namespace {
+
+gh_status validate(const gh_context* ctx, const gh_model_config& c, gh_quant_mode mode) {
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
+    return fail(GH_ERR_UNSUPPORTED, "model: mode must be Q4 or Q8 (the bf16 path is not built)");
+  if (c.num_hidden_layers == 0 || c.num_hidden_layers > 64)
+    return fail(GH_ERR_INVALID, "model: num_hidden_layers must be 1..64");
+  if (c.hidden_size == 0 || c.hidden_size % 128 || c.intermediate_size == 0 ||
+      c.intermediate_size % 128 || c.vocab_size == 0)
+    return fail(GH_ERR_UNSUPPORTED, "model: hidden and intermediate sizes must be multiples of 128");
+  if (c.num_attention_heads == 0 || c.num_key_value_heads == 0 || c.max_slots == 0)
+    return fail(GH_ERR_INVALID, "model: head counts and max_slots must be positive");
+  (void)ctx;
+  return GH_OK;
+}
+
+// src/model/loader.zig:36-42
+Layer layer_shape(const gh_model_config& c, uint32_t l) {
+  Layer L{};
+  L.full = c.layer_types[l] != 0;
+  L.head_dim = L.full ? c.global_head_dim : c.head_dim;
+  L.rot = L.full ? L.head_dim / 4 : L.head_dim;
+  L.nkv = L.full ? c.num_global_key_value_heads : c.num_key_value_heads;
+  L.q_dim = c.num_attention_heads * L.head_dim;
+  L.kv_dim = L.nkv * L.head_dim;
+  L.k_eq_v = L.full && c.attention_k_eq_v;
+  L.theta = L.full ? c.rope_theta_full : c.rope_theta;
+  L.scalar = 1.0f;
+  return L;
+}
+
+gh_status plan(gh_model* m) {
+  const gh_model_config& c = m->cfg;
+  const uint32_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off = align_up(off + bytes, 256);
+    return o;
+  };
+  m->layers.clear();
+  for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
+    Layer L = layer_shape(c, l);
+    if (L.nkv == 0 || c.num_attention_heads % L.nkv || c.num_attention_heads / L.nkv > 4)
+      return fail(GH_ERR_UNSUPPORTED, "model: query heads per kv head must be 1..4");
+    if (L.head_dim % 4 || L.head_dim > 512 || L.q_dim % 128 || L.rot % 2)
+      return fail(GH_ERR_UNSUPPORTED, "model: head_dim must be a multiple of 4 up to 512 with "
+                                      "num_heads * head_dim a multiple of 128");
+    L.qkv_rows = L.q_dim + L.kv_dim * (L.k_eq_v ? 1 : 2);
+    L.qkv = take((size_t)L.qkv_rows * m->row_bytes(H));
+    L.o = take((size_t)H * m->row_bytes(L.q_dim));
+    L.gate = take((size_t)I * m->row_bytes(H));
+    L.up = take((size_t)I * m->row_bytes(H));
+    L.down = take((size_t)H * m->row_bytes(I));
+    L.input_norm = take(H * 4);
+    L.q_norm = take(L.head_dim * 4);
+    L.k_norm = take(L.head_dim * 4);
+    L.post_attn = take(H * 4);
+    L.pre_ffn = take(H * 4);
+    L.post_ffn = take(H * 4);
+    L.k_cache = take((size_t)c.max_slots * L.kv_dim * 4);
+    L.v_cache = take((size_t)c.max_slots * L.kv_dim * 4);
+    m->max_q = std::max(m->max_q, L.q_dim);
+    m->max_kv = std::max(m->max_kv, L.kv_dim);
+    m->layers.push_back(L);
+  }
+  m->lm_head = take((size_t)V * (H / 32) * 36);
+  m->final_norm = take(H * 4);
+  m->x0 = take(H * 4);
+  m->x1 = take(H * 4);
+  uint32_t max_qkv = 0;
+  for (auto& L : m->layers) max_qkv = std::max(max_qkv, L.qkv_rows);
+  m->qkv_out = take((size_t)max_qkv * 4);
+  m->attn_out = take((size_t)m->max_q * 4);
+  m->o_out = take(H * 4);
+  m->act = take(I * 4);
+  m->m_out = take(H * 4);
+  m->logits = take((size_t)V * 4);
+  m->token = take(64);
+  m->step = take(64);
+  m->active = take((size_t)c.max_slots * 4);
+  uint32_t max_nkv = 0, max_g = 1, max_d = 0;
+  for (auto& L : m->layers) {
+    max_nkv = std::max(max_nkv, L.nkv);
+    max_g = std::max(max_g, c.num_attention_heads / L.nkv);
+    max_d = std::max(max_d, L.head_dim);
+  }
+  m->nsplit = gh::attention_splits(m->ctx, max_nkv, c.max_slots);
+  m->attn_cnt = take(256 * 4);
+  m->attn_part = take((size_t)max_nkv * m->nsplit * max_g * (max_d + 2) * 4);
+  m->amax = take((64 + 2 * 4096) * 4);
+  m->arena_bytes = off;
+  return GH_OK;
+}
+
+gh_status alloc_all(gh_model* m) {
+  hipError_t e = hipMalloc(&m->arena, m->arena_bytes);
+  if (e != hipSuccess)
+    return fail(GH_ERR_ALLOC, "model arena (" + std::to_string(m->arena_bytes >> 20) +
+                                  " MiB): " + hipGetErrorString(e));
+  e = hipHostMalloc(&m->h_x, m->cfg.hidden_size * 4);
+  if (e == hipSuccess) e = hipHostMalloc(&m->h_active, (size_t)m->cfg.max_slots * 4);
+  if (e == hipSuccess) e = hipHostMalloc(&m->h_step, 64);
+  if (e == hipSuccess) e = hipHostMalloc(&m->h_token, 64);
+  if (e != hipSuccess) return fail(GH_ERR_ALLOC, std::string("pinned staging: ") + hipGetErrorString(e));
+  memset(m->h_step, 0, 64);
+  memset(m->h_token, 0, 64);
+  // caches, activations and scratch start at zero (counters must)
+  uint64_t words = m->arena_bytes / 4;
+  uint32_t zero = 0;
+  void* p = m->arena;
+  void* args[] = {&p, &zero, &words};
+  gh_status st = m->ctx->launch("gh_fill_u32_k", dim3(8192), dim3(256), 0, args);
+  if (st != GH_OK) return st;
+  e = hipStreamSynchronize(m->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "arena zero-fill");
+  return GH_OK;
+}
+
+// Quantize [rows][cols] bf16 into dst, with the bf16 rows provided chunk by
+// chunk by fill(staging, row0, nrows) (an upload or the device generator).
+template <typename Fill>
+gh_status quantize_rows(gh_model* m, uint8_t* dst, uint32_t rows, uint32_t cols, gh_quant_mode q,
+                        uint16_t* staging, size_t staging_elems, Fill fill) {
+  const uint32_t chunk = (uint32_t)std::max<size_t>(1, staging_elems / cols);
+  const size_t rb = (size_t)(cols / 32) * (q == GH_QUANT_Q8 ? 36 : 20);
+  for (uint32_t r0 = 0; r0 < rows; r0 += chunk) {
+    const uint32_t n = std::min(chunk, rows - r0);
+    gh_status st = fill(staging, r0, n);
+    if (st != GH_OK) return st;
+    st = gh_quantize_matrix_dev(m->ctx, dst + (size_t)r0 * rb, staging, n, cols, q);
+    if (st != GH_OK) return st;
+  }
+  return GH_OK;
+}
+
+gh_status upload_norm(gh_model* m, size_t off, const uint16_t* bf16, uint32_t n) {
+  std::vector<float> f(n, 1.0f);  // absent weight = ones (model_gpu.zig:64-73)
+  if (bf16)
+    for (uint32_t i = 0; i < n; i++) {
+      uint32_t u = (uint32_t)bf16[i] << 16;
+      memcpy(&f[i], &u, 4);
+    }
+  return gh_buffer_write(m->ctx, m->arena + off, f.data(), (size_t)n * 4);
+}
+
+XPro pro_plain(const float* x) {
+  XPro p{};
+  p.x = x;
+  p.mode = 0;
+  return p;
+}
+
+// Records one forward pass (all layers; with the LM head when logits).
+gh_status record_forward(gh_model* m, bool logits) {
+  gh_context* ctx = m->ctx;
+  const gh_model_config& c = m->cfg;
+  const uint32_t H = c.hidden_size, I = c.intermediate_size;
+  const char* gemv = m->mode == GH_QUANT_Q8 ? "gh_gemv_q8" : "gh_gemv_q4";
+  const char* gateup = m->mode == GH_QUANT_Q8 ? "gh_gateup_q8" : "gh_gateup_q4";
+  hipError_t e;
+  // host -> device: x, active list, step params (pinned staging)
+  e = hipMemcpyAsync(m->at<float>(m->x0), m->h_x, H * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(m->at<uint32_t>(m->active), m->h_active, (size_t)c.max_slots * 4,
+                       hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(m->at<uint32_t>(m->step), m->h_step, 16, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "record: input copies");
+
+  size_t xcur = m->x0, xoth = m->x1;
+  gh_status st;
+  for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
+    const Layer& L = m->layers[l];
+    // 1. [q|k|v] = W_qkv . norm(x)  (layer 0: RMSNorm; later: post-FFN add + norm)
+    XPro p{};
+    p.eps = c.rms_norm_eps;
+    p.w = m->at<float>(L.input_norm);
+    if (l == 0) {
+      p.x = m->at<float>(xcur);
+      p.mode = 1;
+    } else {
+      const Layer& P = m->layers[l - 1];
+      p.x = m->at<float>(xcur);
+      p.r = m->at<float>(m->m_out);
+      p.wr = P.post_ffn == kNone ? nullptr : m->at<float>(P.post_ffn);
+      p.s = P.scalar;
+      p.xout = m->at<float>(xoth);
+      p.mode = 2;
+      std::swap(xcur, xoth);
+    }
+    Q4Args qa{m->at<uint8_t>(L.qkv), m->at<float>(m->qkv_out)};
+    if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H)) != GH_OK) return st;
+    // 2. q/k norm + RoPE + cache write + split-K attention
+    gh::AttnLaunch A{};
+    AttnArgs& a = A.args;
+    const float* qkv = m->at<float>(m->qkv_out);
+    a.q = qkv;
+    a.k_in = qkv + L.q_dim;
+    a.v_in = L.k_eq_v ? qkv + L.q_dim : qkv + L.q_dim + L.kv_dim;
+    a.q_norm = m->at<float>(L.q_norm);
+    a.k_norm = m->at<float>(L.k_norm);
+    a.k_cache = m->at<float>(L.k_cache);
+    a.v_cache = m->at<float>(L.v_cache);
+    a.active = m->at<uint32_t>(m->active);
+    a.step = m->at<uint32_t>(m->step);
+    a.part = m->at<float>(m->attn_part);
+    a.counters = m->at<uint32_t>(m->attn_cnt);
+    a.out = m->at<float>(m->attn_out);
+    a.nq = c.num_attention_heads;
+    a.nkv = L.nkv;
+    a.D = L.head_dim;
+    a.rot = L.rot;
+    a.k_eq_v = L.k_eq_v ? 1 : 0;
+    a.nsplit = m->nsplit;
+    a.fuse = 1;
+    a.theta = L.theta;
+    a.eps = c.rms_norm_eps;
+    a.scale = 1.0f;  // inv_sqrt_dim = 1.0 (src/model/forward.zig:80)
+    if ((st = gh::launch_attention(ctx, A)) != GH_OK) return st;
+    // 3. o = W_o . attn
+    Q4Args oa{m->at<uint8_t>(L.o), m->at<float>(m->o_out)};
+    if ((st = gh::launch_stream(ctx, gemv, &oa, pro_plain(m->at<float>(m->attn_out)), H,
+                                L.q_dim)) != GH_OK)
+      return st;
+    // 4. x += post_attn_norm(o); act = geglu(W_gate, W_up . pre_ffn_norm(x))
+    XPro g{};
+    g.x = m->at<float>(xcur);
+    g.r = m->at<float>(m->o_out);
+    g.wr = L.post_attn == kNone ? nullptr : m->at<float>(L.post_attn);
+    g.w = m->at<float>(L.pre_ffn);
+    g.xout = m->at<float>(xoth);
+    g.s = 1.0f;
+    g.eps = c.rms_norm_eps;
+    g.mode = 2;
+    std::swap(xcur, xoth);
+    GateUpArgs ga{m->at<uint8_t>(L.gate), m->at<uint8_t>(L.up), m->at<float>(m->act)};
+    if ((st = gh::launch_stream(ctx, gateup, &ga, g, I, H)) != GH_OK) return st;
+    // 5. m = W_down . act
+    Q4Args da{m->at<uint8_t>(L.down), m->at<float>(m->m_out)};
+    if ((st = gh::launch_stream(ctx, gemv, &da, pro_plain(m->at<float>(m->act)), H, I)) != GH_OK)
+      return st;
+  }
+  if (logits) {
+    // x = (x + post_ffn_norm(m)) * layer_scalar; token = argmax(head . final_norm(x))
+    const Layer& P = m->layers.back();
+    XPro p{};
+    p.x = m->at<float>(xcur);
+    p.r = m->at<float>(m->m_out);
+    p.wr = P.post_ffn == kNone ? nullptr : m->at<float>(P.post_ffn);
+    p.w = m->at<float>(m->final_norm);
+    p.xout = m->at<float>(xoth);
+    p.s = P.scalar;
+    p.eps = c.rms_norm_eps;
+    p.mode = 2;
+    m->hidden_final = xoth;
+    uint32_t* amax = m->at<uint32_t>(m->amax);
+    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), amax + 64, amax,
+                  m->at<uint32_t>(m->token)};
+    if (gh::stream_grid(ctx, c.vocab_size, H) > 4096)
+      return fail(GH_ERR_UNSUPPORTED, "model: LM head grid too large");
+    if ((st = gh::launch_stream(ctx, "gh_argmax_q8", &aa, p, c.vocab_size, H)) != GH_OK) return st;
+    e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost,
+                       ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "record: token copy");
+  }
+  return GH_OK;
+}
+
+gh_status record_graphs(gh_model* m) {
+  for (int pass = 0; pass < 2; pass++) {
+    gh_status st = gh_graph_begin(m->ctx);
+    if (st != GH_OK) return st;
+    gh_status rs = record_forward(m, pass == 0);
+    void* g = nullptr;
+    st = gh_graph_end(m->ctx, &g);
+    if (rs != GH_OK) {
+      if (g) gh_graph_destroy(g);
+      return rs;
+    }
+    if (st != GH_OK) return st;
+    (pass == 0 ? m->graph_decode : m->graph_prefill) = g;
+  }
+  return GH_OK;
+}
+
+gh_status finish_init(gh_model* m, gh_model** out) {
+  gh_status st = record_graphs(m);
+  if (st != GH_OK) {
+    delete m;
+    return st;
+  }
+  hipError_t e = hipStreamSynchronize(m->ctx->stream);
+  if (e != hipSuccess) {
+    delete m;
+    return hip_fail(e, "model init");
+  }
+  *out = m;
+  return GH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+gh_status gh_model_init(gh_context* ctx, const gh_model_config* cfg,
+                        const gh_layer_weights* layers, const uint16_t* embed_tokens,
+                        const uint16_t* final_norm, gh_quant_mode mode, float quiescence_thresh,
+                        gh_model** out) {
+  if (!ctx || !cfg || !layers || !embed_tokens || !out)
+    return fail(GH_ERR_INVALID, "gh_model_init: null argument");
+  *out = nullptr;
+  if (quiescence_thresh != 0.0f)
+    return fail(GH_ERR_UNSUPPORTED, "gh_model_init: quiescence gating is not part of this backend");
+  gh_status st = validate(ctx, *cfg, mode);
+  if (st != GH_OK) return st;
+  gh_model* m = new gh_model();
+  m->ctx = ctx;
+  m->cfg = *cfg;
+  m->mode = mode;
+  if ((st = plan(m)) != GH_OK || (st = alloc_all(m)) != GH_OK) {
+    delete m;
+    return st;
+  }
+  const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size;
+  const size_t staging_elems = 32u << 20;  // 64 MiB of bf16 per chunk
+  uint16_t* staging = nullptr;
+  if (hipMalloc(&staging, staging_elems * 2) != hipSuccess) {
+    delete m;
+    return fail(GH_ERR_ALLOC, "gh_model_init: staging");
+  }
+  auto upload_from = [&](const uint16_t* src, uint32_t cols) {
+    return [=](uint16_t* stg, uint32_t r0, uint32_t n) {
+      return gh_buffer_write(ctx, stg, src + (size_t)r0 * cols, (size_t)n * cols * 2);
+    };
+  };
+  for (uint32_t l = 0; l < cfg->num_hidden_layers && st == GH_OK; l++) {
+    Layer& L = m->layers[l];
+    const gh_layer_weights& w = layers[l];
+    if (!w.q_proj || !w.k_proj || !w.o_proj || !w.gate_proj || !w.up_proj || !w.down_proj ||
+        !w.input_layernorm || !w.q_norm || !w.pre_feedforward_layernorm) {
+      st = fail(GH_ERR_INVALID, "gh_model_init: layer " + std::to_string(l) + " misses a tensor");
+      break;
+    }
+    if (!w.v_proj && !L.k_eq_v) {  // v_proj absent: the key projection serves as value
+      L.k_eq_v = true;
+      L.qkv_rows = L.q_dim + L.kv_dim;
+    }
+    L.scalar = w.layer_scalar;
+    const size_t rb = m->row_bytes(H);
+    uint8_t* qkv = m->at<uint8_t>(L.qkv);
+    st = quantize_rows(m, qkv, L.q_dim, H, mode, staging, staging_elems, upload_from(w.q_proj, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, qkv + (size_t)L.q_dim * rb, L.kv_dim, H, mode, staging, staging_elems,
+                         upload_from(w.k_proj, H));
+    if (st == GH_OK && !L.k_eq_v)
+      st = quantize_rows(m, qkv + (size_t)(L.q_dim + L.kv_dim) * rb, L.kv_dim, H, mode, staging,
+                         staging_elems, upload_from(w.v_proj, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.o), H, L.q_dim, mode, staging, staging_elems,
+                         upload_from(w.o_proj, L.q_dim));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.gate), I, H, mode, staging, staging_elems,
+                         upload_from(w.gate_proj, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.up), I, H, mode, staging, staging_elems,
+                         upload_from(w.up_proj, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.down), H, I, mode, staging, staging_elems,
+                         upload_from(w.down_proj, I));
+    if (st == GH_OK) st = upload_norm(m, L.input_norm, w.input_layernorm, H);
+    if (st == GH_OK) st = upload_norm(m, L.q_norm, w.q_norm, L.head_dim);
+    if (st == GH_OK) st = upload_norm(m, L.k_norm, w.k_norm, L.head_dim);
+    if (st == GH_OK) st = upload_norm(m, L.pre_ffn, w.pre_feedforward_layernorm, H);
+    if (w.post_attention_layernorm) {
+      if (st == GH_OK) st = upload_norm(m, L.post_attn, w.post_attention_layernorm, H);
+    } else {
+      L.post_attn = kNone;
+    }
+    if (w.post_feedforward_layernorm) {
+      if (st == GH_OK) st = upload_norm(m, L.post_ffn, w.post_feedforward_layernorm, H);
+    } else {
+      L.post_ffn = kNone;
+    }
+  }
+  if (st == GH_OK)
+    st = quantize_rows(m, m->at<uint8_t>(m->lm_head), cfg->vocab_size, H, GH_QUANT_Q8, staging,
+                       staging_elems, upload_from(embed_tokens, H));
+  if (st == GH_OK) st = upload_norm(m, m->final_norm, final_norm, H);
+  hipStreamSynchronize(ctx->stream);
+  hipFree(staging);
+  if (st != GH_OK) {
+    delete m;
+    return st;
+  }
+  return finish_init(m, out);
+}
+
+gh_status gh_model_init_synthetic(gh_context* ctx, const gh_model_config* cfg, gh_quant_mode mode,
+                                  uint64_t seed, gh_model** out) {
+  if (!ctx || !cfg || !out) return fail(GH_ERR_INVALID, "gh_model_init_synthetic: null argument");
+  *out = nullptr;
+  gh_status st = validate(ctx, *cfg, mode);
+  if (st != GH_OK) return st;
+  gh_model* m = new gh_model();
+  m->ctx = ctx;
+  m->cfg = *cfg;
+  m->mode = mode;
+  if ((st = plan(m)) != GH_OK || (st = alloc_all(m)) != GH_OK) {
+    delete m;
+    return st;
+  }
+  const uint32_t H = cfg->hidden_size, I = cfg->intermediate_size, V = cfg->vocab_size;
+  const size_t staging_elems = 32u << 20;
+  uint16_t* staging = nullptr;
+  if (hipMalloc(&staging, staging_elems * 2) != hipSuccess ||
+      hipMalloc(&m->embed_dev, (size_t)V * H * 2) != hipSuccess) {
+    if (staging) hipFree(staging);
+    delete m;
+    return fail(GH_ERR_ALLOC, "gh_model_init_synthetic: staging / embedding");
+  }
+  // tensor t of layer l draws from stream 1000 + 16 l + t
+  auto gen = [&](uint64_t stream, uint32_t cols) {
+    return [=](uint16_t* stg, uint32_t r0, uint32_t n) {
+      return gh_synth_normal_bf16_dev(ctx, stg, (size_t)n * cols, seed, stream, 0.0, 0.02,
+                                      (uint64_t)r0 * cols);
+    };
+  };
+  auto norm = [&](size_t off, uint32_t n, uint64_t stream) {
+    std::vector<uint16_t> b(n);
+    gh_synth_normal_bf16(b.data(), n, seed, stream, 1.0, 0.1, 0);
+    return upload_norm(m, off, b.data(), n);
+  };
+  for (uint32_t l = 0; l < cfg->num_hidden_layers && st == GH_OK; l++) {
+    Layer& L = m->layers[l];
+    const uint64_t s0 = 1000 + 16ull * l;
+    const size_t rb = m->row_bytes(H);
+    uint8_t* qkv = m->at<uint8_t>(L.qkv);
+    st = quantize_rows(m, qkv, L.q_dim, H, mode, staging, staging_elems, gen(s0 + 0, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, qkv + (size_t)L.q_dim * rb, L.kv_dim, H, mode, staging, staging_elems,
+                         gen(s0 + 1, H));
+    if (st == GH_OK && !L.k_eq_v)
+      st = quantize_rows(m, qkv + (size_t)(L.q_dim + L.kv_dim) * rb, L.kv_dim, H, mode, staging,
+                         staging_elems, gen(s0 + 2, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.o), H, L.q_dim, mode, staging, staging_elems,
+                         gen(s0 + 3, L.q_dim));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.gate), I, H, mode, staging, staging_elems,
+                         gen(s0 + 4, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.up), I, H, mode, staging, staging_elems,
+                         gen(s0 + 5, H));
+    if (st == GH_OK)
+      st = quantize_rows(m, m->at<uint8_t>(L.down), H, I, mode, staging, staging_elems,
+                         gen(s0 + 6, I));
+    if (st == GH_OK) st = norm(L.input_norm, H, s0 + 7);
+    if (st == GH_OK) st = norm(L.q_norm, L.head_dim, s0 + 8);
+    if (st == GH_OK) st = norm(L.k_norm, L.head_dim, s0 + 9);
+    if (st == GH_OK) st = norm(L.post_attn, H, s0 + 10);
+    if (st == GH_OK) st = norm(L.pre_ffn, H, s0 + 11);
+    if (st == GH_OK) st = norm(L.post_ffn, H, s0 + 12);
+  }
+  // tied embedding / LM head: stream 999
+  if (st == GH_OK) st = gh_synth_normal_bf16_dev(ctx, m->embed_dev, (size_t)V * H, seed, 999, 0.0,
+                                                  0.02, 0);
+  if (st == GH_OK) {
+    const uint32_t chunk = (uint32_t)std::max<size_t>(1, staging_elems / H);
+    for (uint32_t r0 = 0; r0 < V && st == GH_OK; r0 += chunk) {
+      const uint32_t n = std::min(chunk, V - r0);
+      st = gh_quantize_matrix_dev(ctx, m->at<uint8_t>(m->lm_head) + (size_t)r0 * (H / 32) * 36,
+                                  m->embed_dev + (size_t)r0 * H, n, H, GH_QUANT_Q8);
+    }
+  }
+  if (st == GH_OK) st = norm(m->final_norm, H, 998);
+  hipStreamSynchronize(ctx->stream);
+  hipFree(staging);
+  if (st != GH_OK) {
+    delete m;
+    return st;
+  }
+  return finish_init(m, out);
+}
+
+void gh_model_deinit(gh_model* m) { delete m; }
+
+gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
+                                    uint32_t slot_idx, const uint32_t* active_slots,
+                                    uint32_t n_active, uint32_t* out_token) {
+  if (!m || !x || !active_slots || !out_token)
+    return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: null argument");
+  *out_token = 0;
+  const gh_model_config& c = m->cfg;
+  if (n_active == 0 || n_active > c.max_slots || slot_idx >= c.max_slots)
+    return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: active list / slot out of range");
+  for (uint32_t i = 0; i < n_active; i++)
+    if (active_slots[i] >= c.max_slots)
+      return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: active slot out of range");
+  if (clock > 0xFFFFFFFFull) return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: clock > 2^32");
+  memcpy(m->h_x, x, (size_t)c.hidden_size * 4);
+  memcpy(m->h_active, active_slots, (size_t)n_active * 4);
+  m->h_step[0] = (uint32_t)clock;
+  m->h_step[1] = slot_idx;
+  m->h_step[2] = n_active;
+  m->h_step[3] = 0;
+  gh_status st = gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
+  if (st != GH_OK) return st;
+  hipError_t e = hipStreamSynchronize(m->ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "gh_dispatch_forward_token");
+  if (want_logits) *out_token = m->h_token[0];
+  return GH_OK;
+}
+
+gh_status gh_model_embed(gh_model* m, uint32_t token, float* x_host) {
+  if (!m || !x_host) return fail(GH_ERR_INVALID, "gh_model_embed: null argument");
+  if (!m->embed_dev) return fail(GH_ERR_UNSUPPORTED, "gh_model_embed: model has no device embedding");
+  const uint32_t H = m->cfg.hidden_size;
+  if (token >= m->cfg.vocab_size) return fail(GH_ERR_INVALID, "gh_model_embed: token out of range");
+  std::vector<uint16_t> row(H);
+  gh_status st = gh_buffer_read(m->ctx, row.data(), m->embed_dev + (size_t)token * H, (size_t)H * 2);
+  if (st != GH_OK) return st;
+  const float scale = sqrtf((float)H);  // @sqrt(f32(H)), src/model/forward.zig:33
+  for (uint32_t i = 0; i < H; i++) {
+    uint32_t u = (uint32_t)row[i] << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    x_host[i] = f * scale;
+  }
+  return GH_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// (device pointer, bytes) of a tensor; nullptr when absent.
+std::pair<uint8_t*, size_t> tensor_ref(const gh_model* m, int layer, gh_tensor t) {
+  const gh_model_config& c = m->cfg;
+  const uint32_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
+  switch (t) {
+    case GH_T_LM_HEAD:
+      return {m->arena + m->lm_head, (size_t)V * (H / 32) * 36};
+    case GH_T_FINAL_NORM:
+      return {m->arena + m->final_norm, (size_t)H * 4};
+    case GH_T_EMBED:
+      return {reinterpret_cast<uint8_t*>(m->embed_dev), m->embed_dev ? (size_t)V * H * 2 : 0};
+    case GH_T_LOGITS:
+      return {m->arena + m->logits, (size_t)V * 4};
+    case GH_T_HIDDEN:
+      return {m->arena + (m->hidden_final ? m->hidden_final : m->x1), (size_t)H * 4};
+    default:
+      break;
+  }
+  if (layer < 0 || layer >= (int)m->layers.size()) return {nullptr, 0};
+  const Layer& L = m->layers[layer];
+  auto vec = [&](size_t off, size_t n) -> std::pair<uint8_t*, size_t> {
+    if (off == kNone) return {nullptr, 0};
+    return {m->arena + off, n * 4};
+  };
+  switch (t) {
+    case GH_T_QKV: return {m->arena + L.qkv, (size_t)L.qkv_rows * m->row_bytes(H)};
+    case GH_T_O_PROJ: return {m->arena + L.o, (size_t)H * m->row_bytes(L.q_dim)};
+    case GH_T_GATE: return {m->arena + L.gate, (size_t)I * m->row_bytes(H)};
+    case GH_T_UP: return {m->arena + L.up, (size_t)I * m->row_bytes(H)};
+    case GH_T_DOWN: return {m->arena + L.down, (size_t)H * m->row_bytes(I)};
+    case GH_T_INPUT_NORM: return vec(L.input_norm, H);
+    case GH_T_Q_NORM: return vec(L.q_norm, L.head_dim);
+    case GH_T_K_NORM: return vec(L.k_norm, L.head_dim);
+    case GH_T_POST_ATTN_NORM: return vec(L.post_attn, H);
+    case GH_T_PRE_FFN_NORM: return vec(L.pre_ffn, H);
+    case GH_T_POST_FFN_NORM: return vec(L.post_ffn, H);
+    case GH_T_K_CACHE: return vec(L.k_cache, (size_t)c.max_slots * L.kv_dim);
+    case GH_T_V_CACHE: return vec(L.v_cache, (size_t)c.max_slots * L.kv_dim);
+    default: return {nullptr, 0};
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t gh_model_tensor_bytes(const gh_model* m, int layer, gh_tensor t) {
+  if (!m) return 0;
+  auto r = tensor_ref(m, layer, t);
+  return r.first ? r.second : 0;
+}
+
+gh_status gh_model_read_tensor(gh_model* m, int layer, gh_tensor t, void* host, size_t bytes) {
+  if (!m || !host) return fail(GH_ERR_INVALID, "gh_model_read_tensor: null argument");
+  auto r = tensor_ref(m, layer, t);
+  if (!r.first) return fail(GH_ERR_INVALID, "gh_model_read_tensor: no such tensor");
+  if (bytes > r.second) return fail(GH_ERR_INVALID, "gh_model_read_tensor: size exceeds tensor");
+  return gh_buffer_read(m->ctx, host, r.first, bytes);
+}
+
+gh_status gh_model_write_tensor(gh_model* m, int layer, gh_tensor t, const void* host,
+                                size_t bytes) {
+  if (!m || !host) return fail(GH_ERR_INVALID, "gh_model_write_tensor: null argument");
+  auto r = tensor_ref(m, layer, t);
+  if (!r.first) return fail(GH_ERR_INVALID, "gh_model_write_tensor: no such tensor");
+  if (bytes > r.second) return fail(GH_ERR_INVALID, "gh_model_write_tensor: size exceeds tensor");
+  return gh_buffer_write(m->ctx, r.first, host, bytes);
+}
+
+}  // extern "C"

@@ -81,6 +81,50 @@ _SIGS.update({
     "gh_norm_gemv_argmax_q8": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
 })
 
+class ModelConfig(C.Structure):
+    """gh_model_config (ModelConfig, src/model/types.zig:43-61)."""
+    _fields_ = [("vocab_size", _u32), ("hidden_size", _u32), ("intermediate_size", _u32),
+                ("num_hidden_layers", _u32), ("num_attention_heads", _u32),
+                ("num_key_value_heads", _u32), ("num_global_key_value_heads", _u32),
+                ("head_dim", _u32), ("global_head_dim", _u32), ("attention_k_eq_v", _u32),
+                ("max_slots", _u32), ("rms_norm_eps", _f32), ("rope_theta", _f32),
+                ("rope_theta_full", _f32), ("layer_types", C.c_uint8 * 64)]
+
+
+class LayerWeights(C.Structure):
+    """gh_layer_weights (LayerWeights, src/model/types.zig:13-41)."""
+    _fields_ = [(n, _vp) for n in ("input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj",
+                                   "q_norm", "k_norm", "post_attention_layernorm",
+                                   "pre_feedforward_layernorm", "gate_proj", "up_proj",
+                                   "down_proj", "post_feedforward_layernorm")] + \
+        [("layer_scalar", _f32)]
+
+
+_SIGS.update({
+    "gh_ring_create": (_i, [_u32, _u32, _u32, _u32, C.POINTER(_vp)]),
+    "gh_ring_destroy": (None, [_vp]),
+    "gh_ring_total_slots": (_u32, [_vp]),
+    "gh_ring_slot_index": (_u32, [_vp, _u64]),
+    "gh_ring_activate_slot": (_u32, [_vp, _u32, _u64]),
+    "gh_ring_clear_recall": (None, [_vp]),
+    "gh_ring_activate_recall": (_u32, [_vp, _u32, _u32, _u64]),
+    "gh_ring_active_slots": (_u32, [_vp, _u32, _u64, _vp, _u32]),
+    "gh_model_init": (_i, [_vp, C.POINTER(ModelConfig), C.POINTER(LayerWeights), _vp, _vp, _i,
+                           _f32, C.POINTER(_vp)]),
+    "gh_model_init_synthetic": (_i, [_vp, C.POINTER(ModelConfig), _i, _u64, C.POINTER(_vp)]),
+    "gh_model_deinit": (None, [_vp]),
+    "gh_dispatch_forward_token": (_i, [_vp, _vp, _i, _u64, _u32, _vp, _u32, C.POINTER(_u32)]),
+    "gh_model_embed": (_i, [_vp, _u32, _vp]),
+    "gh_model_tensor_bytes": (_sz, [_vp, _i, _i]),
+    "gh_model_read_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
+    "gh_model_write_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
+})
+
+# gh_tensor
+(T_QKV, T_O_PROJ, T_GATE, T_UP, T_DOWN, T_INPUT_NORM, T_Q_NORM, T_K_NORM, T_POST_ATTN_NORM,
+ T_PRE_FFN_NORM, T_POST_FFN_NORM, T_K_CACHE, T_V_CACHE) = range(13)
+T_LM_HEAD, T_FINAL_NORM, T_EMBED, T_LOGITS, T_HIDDEN = 20, 21, 22, 23, 24
+
 _lib = None
 
 
@@ -319,3 +363,121 @@ def _addr(b):
     if isinstance(b, Buffer):
         return b.ptr
     return int(b)
+
+
+class Ring:
+    """DynamicRingBuffer slot bookkeeping (src/ring_buffer.zig:7-147)."""
+
+    def __init__(self, num_layers, num_anchors, window_size, num_recall):
+        h = _vp()
+        _check(lib().gh_ring_create(num_layers, num_anchors, window_size, num_recall,
+                                    C.byref(h)), "gh_ring_create")
+        self.h = h.value
+        self.total_slots = lib().gh_ring_total_slots(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.gh_ring_destroy(self.h)
+            self.h = None
+
+    def slot_index(self, clock):
+        return lib().gh_ring_slot_index(self.h, clock)
+
+    def activate_slot(self, layer, clock):
+        return lib().gh_ring_activate_slot(self.h, layer, clock)
+
+    def clear_recall(self):
+        lib().gh_ring_clear_recall(self.h)
+
+    def activate_recall(self, layer, rank, clock):
+        return lib().gh_ring_activate_recall(self.h, layer, rank, clock)
+
+    def active_slots(self, layer, clock):
+        out = np.zeros(self.total_slots, np.uint32)
+        n = lib().gh_ring_active_slots(self.h, layer, clock, _ptr(out), self.total_slots)
+        return out[:n].copy()
+
+
+def model_config(vocab, hidden, intermediate, layers, heads, kv_heads, head_dim, max_slots,
+                 global_kv_heads=None, global_head_dim=None, k_eq_v=False, eps=1e-6,
+                 theta=10000.0, theta_full=1e6, full_layers=()):
+    c = ModelConfig()
+    c.vocab_size, c.hidden_size, c.intermediate_size = vocab, hidden, intermediate
+    c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads = layers, heads, kv_heads
+    c.num_global_key_value_heads = kv_heads if global_kv_heads is None else global_kv_heads
+    c.head_dim = head_dim
+    c.global_head_dim = head_dim if global_head_dim is None else global_head_dim
+    c.attention_k_eq_v = int(k_eq_v)
+    c.max_slots = max_slots
+    c.rms_norm_eps, c.rope_theta, c.rope_theta_full = eps, theta, theta_full
+    for l in full_layers:
+        c.layer_types[l] = 1
+    return c
+
+
+class Model:
+    """GpuModelContext: weights, K/V ring caches and the recorded graphs."""
+
+    def __init__(self, ctx, cfg, mode=QUANT_Q4, seed=None, layers=None, embed=None,
+                 final_norm=None):
+        self.ctx, self.cfg = ctx, cfg
+        h = _vp()
+        if seed is not None:
+            _check(lib().gh_model_init_synthetic(ctx.h, C.byref(cfg), mode, seed, C.byref(h)),
+                   "gh_model_init_synthetic")
+        else:
+            self._keep = []
+            arr = (LayerWeights * cfg.num_hidden_layers)()
+            for i, d in enumerate(layers):
+                for name, _ in LayerWeights._fields_[:-1]:
+                    a = d.get(name)
+                    if a is None:
+                        setattr(arr[i], name, None)
+                    else:
+                        a = np.ascontiguousarray(a, np.uint16)
+                        self._keep.append(a)
+                        setattr(arr[i], name, a.ctypes.data)
+                arr[i].layer_scalar = float(d.get("layer_scalar", 1.0))
+            e = np.ascontiguousarray(embed, np.uint16)
+            fn = None if final_norm is None else np.ascontiguousarray(final_norm, np.uint16)
+            self._keep += [e, fn]
+            _check(lib().gh_model_init(ctx.h, C.byref(cfg), arr, _ptr(e),
+                                       _ptr(fn) if fn is not None else None, mode, 0.0,
+                                       C.byref(h)), "gh_model_init")
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().gh_model_deinit(self.h)
+            self.h = None
+
+    def forward(self, x, clock, slot_idx, active, want_logits=True):
+        x = np.ascontiguousarray(x, np.float32)
+        act = np.ascontiguousarray(active, np.uint32)
+        tok = _u32()
+        _check(lib().gh_dispatch_forward_token(self.h, _ptr(x), int(want_logits), clock, slot_idx,
+                                               _ptr(act), act.size, C.byref(tok)),
+               "gh_dispatch_forward_token")
+        return tok.value
+
+    def embed(self, token):
+        x = np.empty(self.cfg.hidden_size, np.float32)
+        _check(lib().gh_model_embed(self.h, token, _ptr(x)), "gh_model_embed")
+        return x
+
+    def tensor_bytes(self, layer, t):
+        return lib().gh_model_tensor_bytes(self.h, layer, t)
+
+    def read(self, layer, t, dtype):
+        n = self.tensor_bytes(layer, t)
+        if n == 0:
+            return None
+        out = np.empty(n // np.dtype(dtype).itemsize, dtype)
+        _check(lib().gh_model_read_tensor(self.h, layer, t, _ptr(out), out.nbytes),
+               "gh_model_read_tensor")
+        return out
+
+    def write(self, layer, t, arr):
+        a = np.ascontiguousarray(arr)
+        _check(lib().gh_model_write_tensor(self.h, layer, t, _ptr(a), a.nbytes),
+               "gh_model_write_tensor")

@@ -196,6 +196,119 @@ gh_status gh_decode_attn(gh_context *ctx, const float *Q, const float *K_cache,
  * of the largest value.  out_token is a device u32. */
 gh_status gh_argmax(gh_context *ctx, const float *logits, uint32_t *out_token, uint32_t vocab);
 
+/* ---- ring bookkeeping: DynamicRingBuffer (src/ring_buffer.zig:7-147) -------
+ * The host side of the [anchors | window | recall] ring: which slot a clock
+ * maps to and which slots a token attends over.  The K/V values live in the
+ * model's device caches; these calls produce the slot_idx / active list that
+ * gh_dispatch_forward_token takes. */
+typedef struct gh_ring gh_ring;
+/* DynamicRingBuffer.init (ring_buffer.zig:19-36); total = A + W + R slots. */
+gh_status gh_ring_create(uint32_t num_layers, uint32_t num_anchors, uint32_t window_size,
+                         uint32_t num_recall, gh_ring **out);
+void gh_ring_destroy(gh_ring *r);
+uint32_t gh_ring_total_slots(const gh_ring *r);
+/* getSlotIndex (ring_buffer.zig:56-59). */
+uint32_t gh_ring_slot_index(const gh_ring *r, uint64_t clock);
+/* activateSlot (ring_buffer.zig:61-68). */
+uint32_t gh_ring_activate_slot(gh_ring *r, uint32_t layer, uint64_t clock);
+/* clearRecall (ring_buffer.zig:82-88). */
+void gh_ring_clear_recall(gh_ring *r);
+/* writeRecallKV's slot bookkeeping (ring_buffer.zig:90-99); returns the slot. */
+uint32_t gh_ring_activate_recall(gh_ring *r, uint32_t layer, uint32_t rank, uint64_t clock);
+/* getActiveSlots (ring_buffer.zig:101-136): writes up to cap slots, returns
+ * the full count. */
+uint32_t gh_ring_active_slots(const gh_ring *r, uint32_t layer, uint64_t clock, uint32_t *out,
+                              uint32_t cap);
+
+/* ---- model: GpuModelContext + gpuDispatchForwardToken ---------------------
+ * (src/gpu/model_gpu.zig:35-197, src/gpu/model_dispatch.zig:103-147) */
+typedef struct gh_model gh_model;
+
+/* ModelConfig (src/model/types.zig:43-61) fields the device path uses.
+ * Per-layer shapes follow src/model/loader.zig:36-42: full-attention layers
+ * use global_head_dim, rotary_dim = head_dim / 4, num_global_key_value_heads,
+ * rope_theta_full and k_eq_v = attention_k_eq_v; sliding layers use head_dim,
+ * rotary_dim = head_dim, num_key_value_heads, rope_theta.  max_slots is the
+ * ring size (anchors + window + recall) of the per-layer K/V caches. */
+typedef struct gh_model_config {
+  uint32_t vocab_size, hidden_size, intermediate_size, num_hidden_layers;
+  uint32_t num_attention_heads, num_key_value_heads, num_global_key_value_heads;
+  uint32_t head_dim, global_head_dim, attention_k_eq_v, max_slots;
+  float rms_norm_eps, rope_theta, rope_theta_full;
+  uint8_t layer_types[64]; /* 1 = full_attention, 0 = sliding_attention */
+} gh_model_config;
+
+/* LayerWeights (src/model/types.zig:13-41): borrowed bf16 host pointers,
+ * row-major [out][in]; v_proj, post_* and k_norm may be null (k_norm null =
+ * ones, v_proj null = the key projection is used as value, as
+ * src/gpu/model_gpu.zig:267-278 does). */
+typedef struct gh_layer_weights {
+  const uint16_t *input_layernorm, *q_proj, *k_proj, *v_proj, *o_proj, *q_norm, *k_norm;
+  const uint16_t *post_attention_layernorm, *pre_feedforward_layernorm;
+  const uint16_t *gate_proj, *up_proj, *down_proj, *post_feedforward_layernorm;
+  float layer_scalar; /* 1.0 when the checkpoint has none */
+} gh_layer_weights;
+
+/* GpuModelContext.init (model_gpu.zig:75): quantizes every layer matrix with
+ * quantizeMatrix's bytes (Q4_0 or Q8_0 per mode; the tied LM head is always
+ * Q8_0, model_gpu.zig:160-161), widens norms to f32, allocates the K/V ring
+ * caches and records the decode and prefill graphs.  embed_tokens is
+ * [vocab][hidden] bf16.  quiescence_thresh must be 0 (layer gating is not
+ * part of this backend). */
+gh_status gh_model_init(gh_context *ctx, const gh_model_config *cfg,
+                        const gh_layer_weights *layers, const uint16_t *embed_tokens,
+                        const uint16_t *final_norm, gh_quant_mode mode,
+                        float quiescence_thresh, gh_model **out);
+/* Random-init model of the same architecture (no reference counterpart):
+ * every matrix N(0, 0.02) and every norm 1 + N(0, 0.1), drawn on the device
+ * with the synthetic generator, rounded to bf16 and quantized exactly as
+ * gh_model_init would; layer_scalar 1.  The bf16 embedding stays on the device
+ * for gh_model_embed. */
+gh_status gh_model_init_synthetic(gh_context *ctx, const gh_model_config *cfg,
+                                  gh_quant_mode mode, uint64_t seed, gh_model **out);
+/* GpuModelContext.deinit (model_gpu.zig:187). */
+void gh_model_deinit(gh_model *m);
+
+/* gpuDispatchForwardToken (model_dispatch.zig:131-147): x = the token's
+ * embedding [hidden] (host), clock, slot_idx = ring.activateSlot(0, clock)
+ * and the active slots from ring.getActiveSlots (u32, host).  When want_logits
+ * the decode graph runs and *out_token receives the greedy token; otherwise
+ * the prefill graph (no LM head) runs and *out_token is 0.  Every layer writes
+ * this token's K/V into its cache at slot_idx. */
+gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits, uint64_t clock,
+                                    uint32_t slot_idx, const uint32_t *active_slots,
+                                    uint32_t n_active, uint32_t *out_token);
+/* x = bf16(E[token]) * sqrt(hidden) (src/model/forward.zig:33-37) for a
+ * synthetic model, whose bf16 embedding lives on the device. */
+gh_status gh_model_embed(gh_model *m, uint32_t token, float *x_host);
+
+/* Tensor access for checking and cache set-up (no reference counterpart). */
+typedef enum gh_tensor {
+  GH_T_QKV = 0,        /* layer: [q_dim + kv_dim (+ kv_dim)] quantized rows */
+  GH_T_O_PROJ = 1,     /* layer: [hidden] rows over q_dim */
+  GH_T_GATE = 2,       /* layer: [intermediate] rows over hidden */
+  GH_T_UP = 3,
+  GH_T_DOWN = 4,       /* layer: [hidden] rows over intermediate */
+  GH_T_INPUT_NORM = 5, /* layer: f32 vectors ... */
+  GH_T_Q_NORM = 6,
+  GH_T_K_NORM = 7,
+  GH_T_POST_ATTN_NORM = 8,
+  GH_T_PRE_FFN_NORM = 9,
+  GH_T_POST_FFN_NORM = 10,
+  GH_T_K_CACHE = 11,   /* layer: f32 [max_slots][kv_dim] */
+  GH_T_V_CACHE = 12,
+  GH_T_LM_HEAD = 20,   /* global (layer ignored): Q8_0 [vocab] rows over hidden */
+  GH_T_FINAL_NORM = 21,
+  GH_T_EMBED = 22,     /* synthetic models: bf16 [vocab][hidden] */
+  GH_T_LOGITS = 23,    /* f32 [vocab] of the last decode step */
+  GH_T_HIDDEN = 24     /* f32 [hidden]: the residual stream after the last step */
+} gh_tensor;
+/* Byte size of a tensor (0 when it does not exist). */
+size_t gh_model_tensor_bytes(const gh_model *m, int layer, gh_tensor t);
+gh_status gh_model_read_tensor(gh_model *m, int layer, gh_tensor t, void *host, size_t bytes);
+gh_status gh_model_write_tensor(gh_model *m, int layer, gh_tensor t, const void *host,
+                                size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,7 +23,7 @@ DEVICE_FLAGS = ["--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-
                 "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                 "-I", CSRC, "-I", os.path.join(ROOT, "include")]
 
-KERNEL_FAMILIES = ["gemv", "util", "attn", "norm", "prefill"]
+KERNEL_FAMILIES = ["gemv", "gemv_norm", "util", "attn", "norm", "prefill"]
 
 HOST_SOURCES = ["runtime.cpp", "engine.cpp", "model.cpp", "ring.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-pthread", "-ffp-contract=off",

@@ -26,6 +26,7 @@
 #define ATT_WAVES (ATT_NT / 64)
 #define MAX_D 512
 #define MAX_G 4
+#define MAX_SPLIT 256
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -216,16 +217,20 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
     }
   };
 
-  // two slots in flight per wave
+  // four slots in flight per wave
   uint32_t si = s0 + wave;
-  for (; si + ATT_WAVES < s1; si += 2 * ATT_WAVES) {
-    float k0[DPL], v0[DPL], k1[DPL], v1[DPL];
+  for (; si + 3 * ATT_WAVES < s1; si += 4 * ATT_WAVES) {
+    float k0[DPL], v0[DPL], k1[DPL], v1[DPL], k2[DPL], v2[DPL], k3[DPL], v3[DPL];
     fetch(si, k0, v0);
     fetch(si + ATT_WAVES, k1, v1);
+    fetch(si + 2 * ATT_WAVES, k2, v2);
+    fetch(si + 3 * ATT_WAVES, k3, v3);
     consume(k0, v0);
     consume(k1, v1);
+    consume(k2, v2);
+    consume(k3, v3);
   }
-  if (si < s1) {
+  for (; si < s1; si += ATT_WAVES) {
     float k0[DPL], v0[DPL];
     fetch(si, k0, v0);
     consume(k0, v0);
@@ -245,7 +250,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
     }
   }
   __syncthreads();
-  const uint32_t PS = D + 2;  // partial record: o[D], m, l
+  const uint32_t PS = D + 4;  // partial record: o[D], m, l (+2 pad: float4 rows)
   float* part = a.part + ((size_t)kvh * a.nsplit + split) * G * PS;
   for (uint32_t i = tid; i < G * D; i += ATT_NT) {
     const uint32_t g = i / D, d = i % D;
@@ -274,21 +279,60 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
   __syncthreads();
   if (!last_flag) return;
   __threadfence();
+  __shared__ float sm[MAX_G][MAX_SPLIT], sc[MAX_G][MAX_SPLIT], sL[MAX_G];
   const float* allp = a.part + (size_t)kvh * a.nsplit * G * PS;
-  for (uint32_t i = tid; i < G * D; i += ATT_NT) {
-    const uint32_t g = i / D, d = i % D;
+  for (uint32_t i = tid; i < G * a.nsplit; i += ATT_NT) {
+    const uint32_t g = i / a.nsplit, sp = i % a.nsplit;
+    sm[g][sp] = allp[(sp * G + g) * PS + D];
+    sc[g][sp] = allp[(sp * G + g) * PS + D + 1];  // l for now
+  }
+  __syncthreads();
+  if (tid < G) {  // per query head: running max, weights c_s, and L
     float M = -INFINITY;
-    for (uint32_t s = 0; s < a.nsplit; s++)
-      M = fmaxf(M, __builtin_nontemporal_load(&allp[(s * G + g) * PS + D]));
-    float L = 0.f, O = 0.f;
-    for (uint32_t s = 0; s < a.nsplit; s++) {
-      const float* r = allp + (s * G + g) * PS;
-      const float ms = __builtin_nontemporal_load(&r[D]);
-      const float c = ms == -INFINITY ? 0.f : __expf(ms - M);
-      L += __builtin_nontemporal_load(&r[D + 1]) * c;
-      O += __builtin_nontemporal_load(&r[d]) * c;
+    for (uint32_t sp = 0; sp < a.nsplit; sp++) M = fmaxf(M, sm[tid][sp]);
+    float L = 0.f;
+    for (uint32_t sp = 0; sp < a.nsplit; sp++) {
+      const float c = sm[tid][sp] == -INFINITY ? 0.f : __expf(sm[tid][sp] - M);
+      L += sc[tid][sp] * c;
+      sc[tid][sp] = c;
     }
-    a.out[(size_t)(kvh * G + g) * D + d] = L > 0.f ? O / L : 0.f;
+    sL[tid] = L;
+  }
+  __syncthreads();
+  const uint32_t D4 = D / 4;
+  for (uint32_t i = tid; i < G * D4; i += ATT_NT) {
+    const uint32_t g = i / D4, d = (i % D4) * 4;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    uint32_t sp = 0;
+    for (; sp + 8 <= a.nsplit; sp += 8) {
+      float4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        t[u] = *reinterpret_cast<const float4*>(allp + ((sp + u) * G + g) * PS + d);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const float c = sc[g][sp + u];
+        O.x += t[u].x * c;
+        O.y += t[u].y * c;
+        O.z += t[u].z * c;
+        O.w += t[u].w * c;
+      }
+    }
+    for (; sp < a.nsplit; sp++) {
+      const float4 t = *reinterpret_cast<const float4*>(allp + (sp * G + g) * PS + d);
+      const float c = sc[g][sp];
+      O.x += t.x * c;
+      O.y += t.y * c;
+      O.z += t.z * c;
+      O.w += t.w * c;
+    }
+    const float L = sL[g];
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float* o = a.out + (size_t)(kvh * G + g) * D + d;
+    o[0] = O.x * inv;
+    o[1] = O.y * inv;
+    o[2] = O.z * inv;
+    o[3] = O.w * inv;
   }
   if (tid == 0) a.counters[kvh] = 0;  // ready for the next launch
 }

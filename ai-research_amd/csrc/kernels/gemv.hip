@@ -200,70 +200,87 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // Extra LDS (floats) the prologue needs beyond the padded x and block sums.
-__host__ __device__ constexpr uint32_t pro_extra_floats(uint32_t K) { return 2 * K + 16; }
+__host__ __device__ constexpr uint32_t pro_extra_floats(uint32_t) { return 16; }
 
-template <int NT>
+// Largest K of a normed prologue: each thread holds its float4 slices of x,
+// r and the two norm weights in registers (PRO_U per vector).
+#define PRO_U 4
+
+template <int NT, bool NORMED>
 __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs, float* bsum,
                                             float* ext) {
-  if (p.mode == 0) {
+  if (!NORMED || p.mode == 0) {
     stage_x<NT>(p.x, K, xs, bsum);
     return;
   }
-  float* xr = ext;          // [K] raw / combined x
-  float* rr = ext + K;      // [K] raw r
-  float* red = ext + 2 * K; // [16]
+  float* red = ext;  // [16]
   const uint32_t n4 = K >> 2;
-  constexpr uint32_t U = 4;
-  float ssx = 0.f, ssr = 0.f;
-  for (uint32_t base = 0; base < n4; base += NT * U) {
-    float4 vx[U], vr[U];
+  const bool add = p.mode == 2;
+  // one round trip: every load of the prologue is issued before any is used
+  float4 vx[PRO_U], vr[PRO_U], vwr[PRO_U], vw[PRO_U];
 #pragma unroll
-    for (uint32_t u = 0; u < U; u++) {
-      const uint32_t i = base + u * NT + threadIdx.x;
-      if (i < n4) {
-        vx[u] = reinterpret_cast<const float4*>(p.x)[i];
-        if (p.mode == 2) vr[u] = reinterpret_cast<const float4*>(p.r)[i];
-      }
-    }
-#pragma unroll
-    for (uint32_t u = 0; u < U; u++) {
-      const uint32_t i = base + u * NT + threadIdx.x;
-      if (i < n4) {
-        reinterpret_cast<float4*>(xr)[i] = vx[u];
-        ssx += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
-        if (p.mode == 2) {
-          reinterpret_cast<float4*>(rr)[i] = vr[u];
-          ssr += vr[u].x * vr[u].x + vr[u].y * vr[u].y + vr[u].z * vr[u].z + vr[u].w * vr[u].w;
-        }
+  for (uint32_t u = 0; u < PRO_U; u++) {
+    const uint32_t i = u * NT + threadIdx.x;
+    if (i < n4) {
+      vx[u] = reinterpret_cast<const float4*>(p.x)[i];
+      vw[u] = reinterpret_cast<const float4*>(p.w)[i];
+      if (add) {
+        vr[u] = reinterpret_cast<const float4*>(p.r)[i];
+        if (p.wr) vwr[u] = reinterpret_cast<const float4*>(p.wr)[i];
       }
     }
   }
-  if (p.mode == 2) {
+  if (add) {
+    float ssr = 0.f;
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++)
+      if (u * NT + threadIdx.x < n4)
+        ssr += vr[u].x * vr[u].x + vr[u].y * vr[u].y + vr[u].z * vr[u].z + vr[u].w * vr[u].w;
     const float inv_r = 1.0f / sqrtf(block_sum<NT>(ssr, red) / (float)K + p.eps);
-    ssx = 0.f;
-    for (uint32_t i = threadIdx.x; i < K; i += NT) {
-      const float rv = p.wr ? rr[i] * inv_r * p.wr[i] : rr[i];
-      const float xn = (xr[i] + rv) * p.s;
-      xr[i] = xn;
-      ssx += xn * xn;
-      if (blockIdx.x == 0) p.xout[i] = xn;
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++) {
+      const uint32_t i = u * NT + threadIdx.x;
+      if (i < n4) {
+        float4 rv = vr[u];
+        if (p.wr) {
+          rv.x = rv.x * inv_r * vwr[u].x;
+          rv.y = rv.y * inv_r * vwr[u].y;
+          rv.z = rv.z * inv_r * vwr[u].z;
+          rv.w = rv.w * inv_r * vwr[u].w;
+        }
+        vx[u].x = (vx[u].x + rv.x) * p.s;
+        vx[u].y = (vx[u].y + rv.y) * p.s;
+        vx[u].z = (vx[u].z + rv.z) * p.s;
+        vx[u].w = (vx[u].w + rv.w) * p.s;
+        if (blockIdx.x == 0) reinterpret_cast<float4*>(p.xout)[i] = vx[u];
+      }
     }
   }
+  float ssx = 0.f;
+#pragma unroll
+  for (uint32_t u = 0; u < PRO_U; u++)
+    if (u * NT + threadIdx.x < n4)
+      ssx += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
   const float inv = 1.0f / sqrtf(block_sum<NT>(ssx, red) / (float)K + p.eps);
-  for (uint32_t i = threadIdx.x; i < n4; i += NT) {
-    const uint32_t e = i << 2, g = e >> 7, o = e & 127;
-    const float4 wv = reinterpret_cast<const float4*>(p.w)[i];
-    float4 v;
-    v.x = xr[e] * inv * wv.x;
-    v.y = xr[e + 1] * inv * wv.y;
-    v.z = xr[e + 2] * inv * wv.z;
-    v.w = xr[e + 3] * inv * wv.w;
-    *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v;
-    float s = (v.x + v.y) + (v.z + v.w);
+#pragma unroll
+  for (uint32_t u = 0; u < PRO_U; u++) {
+    const uint32_t i = u * NT + threadIdx.x;
+    float s = 0.f;
+    if (i < n4) {
+      const uint32_t e = i << 2, g = e >> 7, o = e & 127;
+      float4 v;
+      v.x = vx[u].x * inv * vw[u].x;
+      v.y = vx[u].y * inv * vw[u].y;
+      v.z = vx[u].z * inv * vw[u].z;
+      v.w = vx[u].w * inv * vw[u].w;
+      *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v;
+      s = (v.x + v.y) + (v.z + v.w);
+    }
+    // block sums: 8 consecutive lanes hold one block (NT and n4 are multiples of 8)
     s += __shfl_xor(s, 1, 8);
     s += __shfl_xor(s, 2, 8);
     s += __shfl_xor(s, 4, 8);
-    if ((i & 7) == 0) bsum[i >> 3] = s;
+    if (i < n4 && (i & 7) == 0) bsum[i >> 3] = s;
   }
   __syncthreads();
 }
@@ -546,7 +563,7 @@ struct Q8ArgmaxFmt {
 // duplicate and contribute zero.  Teams with no rows skip the stream but
 // still take part in the block-wide prologue and epilogue.
 // ------------------------------------------------------------------------
-template <class F, int TPR, int GPL, int D, int NT>
+template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
                                             uint32_t K) {
   extern __shared__ float lds[];
@@ -582,7 +599,7 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 #pragma unroll
     for (int d = 0; d < D; d++) F::load(buf[d], a, offset_of(d), d % F::kSub);
   }
-  stage_x_pro<NT>(xp, K, xs, bsum, ext);
+  stage_x_pro<NT, NORMED>(xp, K, xs, bsum, ext);
   typename F::Acc acc;
   F::init(acc);
   for (uint32_t base = 0; base < n_items; base += D) {
@@ -605,40 +622,46 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
   F::template block_end<NT>(acc, a, ext);
 }
 
-#define GH_GEMV_INST(T, G, D)                                                                  \
-  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q4_t##T##_g##G##_d##D(              \
-      Q4Fmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                        \
-    stream_rows<Q4Fmt, T, G, D, 256>(a, xp, M, K);                                             \
-  }                                                                                            \
-  extern "C" __global__ __launch_bounds__(256) void gh_gateup_q4_t##T##_g##G##_d##D(            \
-      GateUpFmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                    \
-    stream_rows<GateUpFmt, T, G, D, 256>(a, xp, M, K);                                         \
-  }                                                                                            \
-  extern "C" __global__ __launch_bounds__(256) void gh_gemv_q8_t##T##_g##G##_d##D(              \
-      Q8Fmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                        \
-    stream_rows<Q8Fmt, T, G, D, 256>(a, xp, M, K);                                             \
-  }                                                                                            \
-  extern "C" __global__ __launch_bounds__(256) void gh_gateup_q8_t##T##_g##G##_d##D(            \
-      GateUpQ8Fmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                  \
-    stream_rows<GateUpQ8Fmt, T, G, D, 256>(a, xp, M, K);                                       \
-  }                                                                                            \
-  extern "C" __global__ __launch_bounds__(256) void gh_argmax_q8_t##T##_g##G##_d##D(            \
-      Q8ArgmaxFmt::Args a, XPro xp, uint32_t M, uint32_t K) {                                  \
-    stream_rows<Q8ArgmaxFmt, T, G, D, 256>(a, xp, M, K);                                       \
+// Kernel names: gh_<family>[n]_t<TPR>_g<GPL>_d<D>; the "n" variants carry the
+// normed x prologue (modes 1 and 2), the others stage x as given (mode 0)
+// and keep the prologue's registers out of the stream.  Weight and output
+// pointers are separate kernel parameters: loaded out of a by-value struct
+// parameter they lose the kernel-argument address-space and alignment facts,
+// and the stream then needs ~100 more VGPRs (220 vs 126 for the Q4 d3 form).
+#define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED)                       \
+  extern "C" __global__ __launch_bounds__(256) void NAME##_t##T##_g##G##_d##D(          \
+      GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                             \
+    stream_rows<FMT, T, G, D, 256, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);       \
   }
+#define GH_UNPAREN(...) __VA_ARGS__
 
-#define GH_GEMV_INST_D(T, G) \
-  GH_GEMV_INST(T, G, 2)      \
-  GH_GEMV_INST(T, G, 3)
+#define GH_P_W (const uint8_t* W, float* Y)
+#define GH_A_W (W, Y)
+#define GH_P_GU (const uint8_t* Wg, const uint8_t* Wu, float* Y)
+#define GH_A_GU (Wg, Wu, Y)
+#define GH_P_AM (const uint8_t* W, float* Y, uint32_t* partial, uint32_t* counter, uint32_t* token)
+#define GH_A_AM (W, Y, partial, counter, token)
 
-GH_GEMV_INST_D(8, 1)
-GH_GEMV_INST_D(8, 2)
-GH_GEMV_INST_D(16, 1)
-GH_GEMV_INST_D(16, 2)
-GH_GEMV_INST_D(16, 4)
-GH_GEMV_INST_D(32, 1)
-GH_GEMV_INST_D(32, 2)
-GH_GEMV_INST_D(32, 4)
-GH_GEMV_INST_D(64, 1)
-GH_GEMV_INST_D(64, 2)
-GH_GEMV_INST_D(64, 4)
+#define GH_PLAIN(T, G, D)                                                        \
+  GH_STREAM_KERNEL(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false)            \
+  GH_STREAM_KERNEL(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false)            \
+  GH_STREAM_KERNEL(gh_gateup_q4, GateUpFmt, GH_P_GU, GH_A_GU, T, G, D, false)    \
+  GH_STREAM_KERNEL(gh_gateup_q8, GateUpQ8Fmt, GH_P_GU, GH_A_GU, T, G, D, false)  \
+  GH_STREAM_KERNEL(gh_argmax_q8, Q8ArgmaxFmt, GH_P_AM, GH_A_AM, T, G, D, false)
+
+#define GH_NORMED(T, G, D)                                                       \
+  GH_STREAM_KERNEL(gh_gemv_q4n, Q4Fmt, GH_P_W, GH_A_W, T, G, D, true)            \
+  GH_STREAM_KERNEL(gh_gemv_q8n, Q8Fmt, GH_P_W, GH_A_W, T, G, D, true)            \
+  GH_STREAM_KERNEL(gh_gateup_q4n, GateUpFmt, GH_P_GU, GH_A_GU, T, G, D, true)    \
+  GH_STREAM_KERNEL(gh_gateup_q8n, GateUpQ8Fmt, GH_P_GU, GH_A_GU, T, G, D, true)  \
+  GH_STREAM_KERNEL(gh_argmax_q8n, Q8ArgmaxFmt, GH_P_AM, GH_A_AM, T, G, D, true)
+
+#define GH_SHAPES(X, D) X(16, 1, D) X(32, 1, D) X(64, 1, D) X(32, 2, D) X(64, 2, D) X(32, 4, D) X(64, 4, D)
+
+#if defined(GH_GEMV_NORMED)
+GH_SHAPES(GH_NORMED, 2)
+GH_SHAPES(GH_NORMED, 3)
+#else
+GH_SHAPES(GH_PLAIN, 2)
+GH_SHAPES(GH_PLAIN, 3)
+#endif

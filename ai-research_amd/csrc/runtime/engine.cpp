@@ -26,13 +26,13 @@ unsigned x_lds_bytes(uint32_t K);
 // persistent grid of wgs_per_cu workgroups per CU (bounded by LDS).
 GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K) {
   const uint32_t ng = K / 128;
-  static const int kT[] = {8, 16, 32, 64};
+  static const int kT[] = {16, 32, 64};
   int best_t = 64, best_g = 4;
   uint32_t best_waste = ~0u;
   for (int g : {1, 2, 4}) {
     for (int t : kT) {
       if ((uint32_t)(t * g) < ng) continue;
-      if (t == 8 && g == 4) continue;
+      if (t == 16 && g > 1) continue;  // shapes built: 16x1, 32x{1,2,4}, 64x{1,2,4}
       const uint32_t waste = t * g - ng;
       if (waste < best_waste || (waste == best_waste && t > best_t)) {
         best_waste = waste;
@@ -45,9 +45,9 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K) {
   GemvCfg c{best_t, best_g, 4, 3};
   if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning override "tpr,gpl,wgs_per_cu,depth"
     int t = 0, g = 0, w = 0, d = 0;
-    if (sscanf(env, "%d,%d,%d,%d", &t, &g, &w, &d) == 4 && (t == 8 || t == 16 || t == 32 || t == 64) &&
-        (g == 1 || g == 2 || g == 4) && !(t == 8 && g == 4) && w >= 1 && w <= 32 &&
-        (uint32_t)(t * g) >= ng && d >= 2 && d <= 4) {
+    if (sscanf(env, "%d,%d,%d,%d", &t, &g, &w, &d) == 4 && (t == 16 || t == 32 || t == 64) &&
+        (g == 1 || g == 2 || g == 4) && !(t == 16 && g > 1) && w >= 1 && w <= 32 &&
+        (uint32_t)(t * g) >= ng && d >= 2 && d <= 3) {
       c = {t, g, w, d};
     }
   }
@@ -78,26 +78,34 @@ gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const
 
 namespace gh {
 
-gh_status launch_stream(gh_context* ctx, const char* family, void* fmt_args, const XPro& xp,
-                        uint32_t M, uint32_t K) {
+gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
+                       StreamShape* out) {
   GemvCfg c = pick_gemv(ctx, M, K);
+  out->lds = x_lds_bytes(K) + 64;
+  if (out->lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
+  out->name = std::string(family) + (normed ? "n" : "") + "_t" + std::to_string(c.tpr) + "_g" +
+              std::to_string(c.gpl) + "_d" + std::to_string(c.depth);
+  // A persistent grid larger than what the CUs hold at once would run its
+  // last workgroups as a second, mostly idle wave.
+  const int occ = ctx->occupancy(out->name, 256, out->lds);
+  if (occ <= 0) return fail(GH_ERR_CODE_OBJECT, "kernel not found in the code objects: " + out->name);
   const uint32_t teams_per_wg = 256 / c.tpr;
   const uint32_t max_grid = (M + teams_per_wg - 1) / teams_per_wg;
-  const unsigned grid = std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * c.wgs_per_cu);
-  const unsigned lds = x_lds_bytes(K) + (xp.mode ? (2 * K + 16) * 4 : 64);
-  if (lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
-  std::string name = std::string(family) + "_t" + std::to_string(c.tpr) + "_g" +
-                     std::to_string(c.gpl) + "_d" + std::to_string(c.depth);
-  XPro xpc = xp;
-  void* args[] = {fmt_args, &xpc, &M, &K};
-  return ctx->launch(name, dim3(grid), dim3(256), lds, args);
+  out->grid = std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * std::min(c.wgs_per_cu, occ));
+  return GH_OK;
 }
 
-unsigned stream_grid(const gh_context* ctx, uint32_t M, uint32_t K) {
-  GemvCfg c = pick_gemv(ctx, M, K);
-  const uint32_t teams_per_wg = 256 / c.tpr;
-  const uint32_t max_grid = (M + teams_per_wg - 1) / teams_per_wg;
-  return std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * c.wgs_per_cu);
+gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> fmt_params,
+                        const XPro& xp, uint32_t M, uint32_t K) {
+  if (xp.mode != 0 && K > 4u * 4u * 256u)  // PRO_U float4 per thread of 256
+    return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": normed prologue needs K <= 4096");
+  StreamShape sh;
+  gh_status st = stream_shape(ctx, family, xp.mode != 0, M, K, &sh);
+  if (st != GH_OK) return st;
+  XPro xpc = xp;
+  std::vector<void*> args = std::move(fmt_params);
+  args.insert(args.end(), {&xpc, &M, &K});
+  return ctx->launch(sh.name, dim3(sh.grid), dim3(256), sh.lds, args.data());
 }
 
 gh_status check_pro(const gh_context* ctx, const XPro& p, uint32_t K, const char* who) {
@@ -209,7 +217,9 @@ gh_status gh_norm_gemv_argmax_q8(gh_context* ctx, const void* W, float* logits,
   if (st != GH_OK) return st;
   uint32_t* base = static_cast<uint32_t*>(ctx->argmax_scratch);
   ArgmaxArgs a{static_cast<const uint8_t*>(W), logits, base + 64, base, token};
-  if (gh::stream_grid(ctx, M, K) > kArgmaxMaxBlocks)
+  gh::StreamShape sh;
+  if ((st = gh::stream_shape(ctx, "gh_argmax_q8", p.mode != 0, M, K, &sh)) != GH_OK) return st;
+  if (sh.grid > kArgmaxMaxBlocks)
     return fail(GH_ERR_UNSUPPORTED, "gh_norm_gemv_argmax_q8: grid too large");
   return launch_stream(ctx, "gh_argmax_q8", &a, p, M, K);
 }
@@ -267,8 +277,10 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {
-  uint32_t ns = (2u * (uint32_t)ctx->num_cus + nkv - 1) / nkv;  // about two workgroups per CU
-  ns = std::min<uint32_t>(ns, std::max<uint32_t>(1u, (max_slots + 7) / 8));  // >= 8 slots a split
+  // about 32 slots per split (8 per wave, 4 in flight), at most ~one
+  // workgroup per CU in total
+  uint32_t ns = std::max<uint32_t>(1u, (max_slots + 31) / 32);
+  ns = std::min<uint32_t>(ns, std::max<uint32_t>(1u, (uint32_t)ctx->num_cus / std::max(1u, nkv)));
   if (const char* env = getenv("GH_ATTN_SPLITS")) {
     int v = atoi(env);
     if (v >= 1 && v <= 256) ns = (uint32_t)v;
@@ -304,7 +316,7 @@ gh_status gh_decode_attn(gh_context* ctx, const float* Q, const float* K_cache,
   a.fuse = 0;
   a.scale = inv_sqrt_dim;
   a.nsplit = gh::attention_splits(ctx, a.nkv, 1024);
-  const size_t part_bytes = (size_t)a.nkv * a.nsplit * gqa_ratio * (head_dim + 2) * 4;
+  const size_t part_bytes = (size_t)a.nkv * a.nsplit * gqa_ratio * (head_dim + 4) * 4;
   if (a.nkv > 256) return fail(GH_ERR_UNSUPPORTED, "gh_decode_attn: more than 256 kv heads");
   // counters first, at a fixed offset, so a later call with a different
   // partial size still finds them at zero

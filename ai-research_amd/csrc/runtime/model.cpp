@@ -174,7 +174,7 @@ gh_status plan(gh_model* m) {
   }
   m->nsplit = gh::attention_splits(m->ctx, max_nkv, c.max_slots);
   m->attn_cnt = take(256 * 4);
-  m->attn_part = take((size_t)max_nkv * m->nsplit * max_g * (max_d + 2) * 4);
+  m->attn_part = take((size_t)max_nkv * m->nsplit * max_g * (max_d + 4) * 4);
   m->amax = take((64 + 2 * 4096) * 4);
   m->arena_bytes = off;
   return GH_OK;
@@ -344,8 +344,10 @@ gh_status record_forward(gh_model* m, bool logits) {
     uint32_t* amax = m->at<uint32_t>(m->amax);
     ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), amax + 64, amax,
                   m->at<uint32_t>(m->token)};
-    if (gh::stream_grid(ctx, c.vocab_size, H) > 4096)
-      return fail(GH_ERR_UNSUPPORTED, "model: LM head grid too large");
+    gh::StreamShape sh;
+    if ((st = gh::stream_shape(ctx, "gh_argmax_q8", true, c.vocab_size, H, &sh)) != GH_OK)
+      return st;
+    if (sh.grid > 4096) return fail(GH_ERR_UNSUPPORTED, "model: LM head grid too large");
     if ((st = gh::launch_stream(ctx, "gh_argmax_q8", &aa, p, c.vocab_size, H)) != GH_OK) return st;
     e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost,
                        ctx->stream);

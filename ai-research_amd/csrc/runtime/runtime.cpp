@@ -42,8 +42,8 @@ static std::string library_dir() {
 }
 
 // Code objects built by ai-research_amd/build.py next to libgemma_hip.so.
-static const char* kCodeObjects[] = {"gh_gemv.hsaco", "gh_util.hsaco", "gh_attn.hsaco",
-                                     "gh_norm.hsaco", "gh_prefill.hsaco"};
+static const char* kCodeObjects[] = {"gh_gemv.hsaco", "gh_gemv_norm.hsaco", "gh_util.hsaco",
+                                     "gh_attn.hsaco", "gh_norm.hsaco", "gh_prefill.hsaco"};
 
 }  // namespace gh
 
@@ -89,6 +89,22 @@ gh_status gh_context::launch(const std::string& name, dim3 grid, dim3 block, uns
                                        lds, stream, args, nullptr);
   if (e != hipSuccess) return hip_fail(e, ("launch " + name).c_str());
   return GH_OK;
+}
+
+int gh_context::occupancy(const std::string& name, int block, unsigned lds) {
+  const std::string key = name + "/" + std::to_string(block) + "/" + std::to_string(lds);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = occ.find(key);
+    if (it != occ.end()) return it->second;
+  }
+  hipFunction_t f = fn(name);
+  if (!f) return 0;
+  int n = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, block, lds) != hipSuccess) n = 1;
+  std::lock_guard<std::mutex> lk(mu);
+  occ[key] = n;
+  return n;
 }
 
 gh_status gh_context::ensure_zeroed(void** buf, size_t* have, size_t need) {

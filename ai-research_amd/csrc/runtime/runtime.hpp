@@ -31,6 +31,10 @@ struct gh_context {
   gh_status load(const char* dir);
   hipFunction_t fn(const std::string& name);
   gh_status launch(const std::string& name, dim3 grid, dim3 block, unsigned lds, void** args);
+  // Workgroups of `block` threads one CU holds at once (registers and LDS);
+  // 0 when the kernel is missing.
+  int occupancy(const std::string& name, int block, unsigned lds);
+  std::unordered_map<std::string, int> occ;
   ~gh_context();
 };
 
@@ -44,11 +48,30 @@ struct AttnLaunch {
 };
 gh_status launch_attention(gh_context* ctx, const AttnLaunch& L);
 // Row-stream GEMV launch (gemv.hip); family = gh_gemv_q4, gh_gemv_q8,
-// gh_gateup_q4, gh_gateup_q8 or gh_argmax_q8; fmt_args points at the
-// family's argument block.
-gh_status launch_stream(gh_context* ctx, const char* family, void* fmt_args, const XPro& xp,
-                        uint32_t M, uint32_t K);
-unsigned stream_grid(const gh_context* ctx, uint32_t M, uint32_t K);
+// gh_gateup_q4, gh_gateup_q8 or gh_argmax_q8.  The kernels take the
+// argument block's members as separate parameters, in member order.
+gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> fmt_params,
+                        const XPro& xp, uint32_t M, uint32_t K);
+inline gh_status launch_stream(gh_context* ctx, const char* family, Q4Args* a, const XPro& xp,
+                               uint32_t M, uint32_t K) {
+  return launch_stream(ctx, family, {&a->W, &a->Y}, xp, M, K);
+}
+inline gh_status launch_stream(gh_context* ctx, const char* family, GateUpArgs* a,
+                               const XPro& xp, uint32_t M, uint32_t K) {
+  return launch_stream(ctx, family, {&a->Wg, &a->Wu, &a->Y}, xp, M, K);
+}
+inline gh_status launch_stream(gh_context* ctx, const char* family, ArgmaxArgs* a,
+                               const XPro& xp, uint32_t M, uint32_t K) {
+  return launch_stream(ctx, family, {&a->W, &a->Y, &a->partial, &a->counter, &a->token}, xp, M,
+                       K);
+}
+// Kernel name and persistent grid of one row-stream launch.
+struct StreamShape {
+  std::string name;
+  unsigned grid = 0, lds = 0;
+};
+gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
+                       StreamShape* out);
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);

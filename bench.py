@@ -134,6 +134,53 @@ def bench_gemv(ctx, reps=256):
     return nbytes / (ms * 1e-3) / 1e9, ms * 1e3
 
 
+def bench_decode(ctx, n_prompt=512, n_decode=128):
+    """12B-shaped decode: 48 layers (global iff (l+1) % 6 == 0), hidden 3840,
+    16/8 heads of 256, intermediate 15360, vocab 262144, Q4_0 layers and Q8_0
+    tied head, 640-slot ring (32 anchors, 512 window, 96 recall).  A prompt of
+    512 token ids uniform over the vocabulary (seed 1) is prefilled, then 128
+    greedy steps run, each one host round trip like gpuDispatchForwardToken:
+    embedding on the host, slot bookkeeping, graph replay, token read back."""
+    cfg = gh.model_config(vocab=262144, hidden=H, intermediate=I, layers=48, heads=16,
+                          kv_heads=8, head_dim=256, max_slots=640,
+                          full_layers=[l for l in range(48) if (l + 1) % 6 == 0])
+    t0 = time.perf_counter()
+    m = gh.Model(ctx, cfg, mode=gh.QUANT_Q4, seed=0)
+    init_s = time.perf_counter() - t0
+    embed = m.read(-1, gh.T_EMBED, np.uint16).reshape(cfg.vocab_size, H)
+    scale = np.sqrt(np.float32(H))
+
+    def emb(t):  # src/model/forward.zig:33-37
+        return (embed[t].astype(np.uint32) << 16).view(np.float32) * scale
+
+    ring = gh.Ring(48, 32, 512, 96)
+    prompt = gh.synth_uniform_u32(n_prompt, 1, 0, cfg.vocab_size)
+    t0 = time.perf_counter()
+    tok = 0
+    for c, t in enumerate(prompt):
+        slot = ring.activate_slot(0, c)
+        tok = m.forward(emb(int(t)), c, slot, ring.active_slots(0, c), c == n_prompt - 1)
+    prefill_s = time.perf_counter() - t0
+    toks = []
+    t0 = time.perf_counter()
+    for i in range(n_decode):
+        c = n_prompt + i
+        slot = ring.activate_slot(0, c)
+        tok = m.forward(emb(tok), c, slot, ring.active_slots(0, c), True)
+        toks.append(tok)
+    decode_s = time.perf_counter() - t0
+    m.close()
+    step_bytes = (48 * (8192 * Q4_ROW(H) + H * Q4_ROW(4096) + 2 * I * Q4_ROW(H) + H * Q4_ROW(I))
+                  + 262144 * (H // 32) * 36)
+    return {"decode_tok_s": round(n_decode / decode_s, 2),
+            "decode_ms_per_token": round(decode_s / n_decode * 1e3, 3),
+            "decode_weight_gbs": round(step_bytes * n_decode / decode_s / 1e9, 1),
+            "prefill_tok_s": round(n_prompt / prefill_s, 2),
+            "prefill_path": "per-token graph replay",
+            "model_init_s": round(init_s, 2),
+            "decode_tokens_head": [int(t) for t in toks[:8]]}
+
+
 def cpu_baseline(x, host_w, budget_s=10.0):
     """The oracle's restatement of the reference CPU path (src/test_q4_exec.zig
     dequant loop inside gatedMlp's 16-job row split, src/kernels.zig:100-129)
@@ -158,6 +205,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the 12B decode leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: the decode backend has no multi-GPU path "
@@ -173,6 +221,10 @@ def main():
     value = step_bytes * args.steps / wall / 1e9
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
     gemv_gbs, gemv_us = bench_gemv(ctx)
+    dec = bench_decode(ctx) if not args.no_decode else None
+    if dec:
+        log("decode %.1f tok/s (%.3f ms/token), prefill %.1f tok/s"
+            % (dec["decode_tok_s"], dec["decode_ms_per_token"], dec["prefill_tok_s"]))
     log("mlp %.1f GB/s, gate_up %.2f us, down %.2f us, gemv8192x2048 %.2f us"
         % (value, gu_ms * 1e3, dn_ms * 1e3, gemv_us))
 
@@ -216,7 +268,8 @@ def main():
                   "down_proj_us": round(dn_ms * 1e3, 3),
                   "down_proj_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
                   "gemv_q4_8192x2048_gbs": round(gemv_gbs, 1),
-                  "gemv_q4_8192x2048_us": round(gemv_us, 3)},
+                  "gemv_q4_8192x2048_us": round(gemv_us, 3),
+                  "decode_12b": dec},
     }
     ctx.close()
     print(json.dumps(line), flush=True)

@@ -47,31 +47,32 @@ __device__ __forceinline__ u32x4 ldw(const void* p) {
 
 // Stage x[K] into LDS (padded by group) and write the per-block sums.
 // K % 128 == 0.  All NT threads of the block must call it.  The loads of a
-// chunk of up to 8 float4 per thread are all issued before any is consumed,
-// so staging costs one L2 round trip per chunk rather than one per float4.
+// chunk of U float4 per thread are all issued before any is consumed, so
+// staging costs one L2 round trip per chunk.  The loads are unconditional
+// (indices clamped into range) and every loaded value is consumed within its
+// chunk: a load left pending across the loop's back edge, or one issued
+// under a branch, makes the compiler wait for every earlier load -- the
+// weight loads in flight included -- before issuing the next.
 template <int NT>
 __device__ __forceinline__ void stage_x(const float* __restrict__ X, uint32_t K,
                                         float* xs, float* bsum) {
   constexpr uint32_t U = 8;
   const uint32_t n4 = K >> 2;
+  const float4* X4 = reinterpret_cast<const float4*>(X);
   for (uint32_t base = 0; base < n4; base += NT * U) {
     float4 v[U];
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) {
       const uint32_t i = base + u * NT + threadIdx.x;
-      if (i < n4) v[u] = reinterpret_cast<const float4*>(X)[i];
+      v[u] = X4[i < n4 ? i : n4 - 1];
     }
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) {
       const uint32_t i = base + u * NT + threadIdx.x;
-      if (base + u * NT >= n4) break;  // uniform: no thread has work from here on
-      float s = 0.f;
-      if (i < n4) {
-        const uint32_t e = i << 2;       // element index
-        const uint32_t g = e >> 7, o = e & 127;  // group, offset in group
-        *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v[u];
-        s = (v[u].x + v[u].y) + (v[u].z + v[u].w);
-      }
+      const uint32_t e = i << 2;               // element index
+      const uint32_t g = e >> 7, o = e & 127;  // group, offset in group
+      float s = (v[u].x + v[u].y) + (v[u].z + v[u].w);
+      if (i < n4) *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v[u];
       // a block is 8 consecutive float4s = 8 consecutive lanes (n4 % 8 == 0,
       // so a lane group of 8 is either fully in range or fully out)
       s += __shfl_xor(s, 1, 8);
@@ -292,7 +293,7 @@ __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs
 // after the stream (all threads).
 // ------------------------------------------------------------------------
 struct Q4Fmt {  // shaders/gemv_q4.wgsl
-  static constexpr uint32_t kGroupBytes = 80, kBlockBytes = 20, kSub = 1;
+  static constexpr uint32_t kGroupBytes = 80, kBlockBytes = 20;
   struct Item {
     Q4G w;
   };
@@ -303,13 +304,12 @@ struct Q4Fmt {  // shaders/gemv_q4.wgsl
     const uint8_t* W;
     float* Y;
   };
-  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
+  __device__ static void load(Item& it, const Args& a, size_t off) {
     it.w = load_q4g(a.W + off);
   }
   __device__ static void init(Acc& c) { c.s = 0.f; }
   __device__ static void zero(Acc& c) { c.s = 0.f; }
-  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
-                             uint32_t) {
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid) {
     c.s += valid * q4_group_dot(it.w, xg, bs);
   }
   template <int TPR>
@@ -321,13 +321,63 @@ struct Q4Fmt {  // shaders/gemv_q4.wgsl
   __device__ static void block_end(const Acc&, const Args&, float*) {}
 };
 
+// Gate and up rows of the same (row, group) travel as one item, so every x
+// value read from LDS feeds both matrices.
+__device__ __forceinline__ void q4_group_dot2(const Q4G& a, const Q4G& b, const float* __restrict__ xg,
+                                              const float* __restrict__ bs, float& ra, float& rb) {
+  const uint32_t A[20] = {a.a0.x, a.a0.y, a.a0.z, a.a0.w, a.a1.x, a.a1.y, a.a1.z, a.a1.w,
+                          a.a2.x, a.a2.y, a.a2.z, a.a2.w, a.a3.x, a.a3.y, a.a3.z, a.a3.w,
+                          a.a4.x, a.a4.y, a.a4.z, a.a4.w};
+  const uint32_t B[20] = {b.a0.x, b.a0.y, b.a0.z, b.a0.w, b.a1.x, b.a1.y, b.a1.z, b.a1.w,
+                          b.a2.x, b.a2.y, b.a2.z, b.a2.w, b.a3.x, b.a3.y, b.a3.z, b.a3.w,
+                          b.a4.x, b.a4.y, b.a4.z, b.a4.w};
+  ra = 0.f;
+  rb = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t* wa = &A[5 * j + 1];
+    const uint32_t* wb = &B[5 * j + 1];
+    const float* xb = xg + 32 * j;
+    float al = 0.f, ah = 0.f, bl = 0.f, bh = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t alo = opaque_and(wa[k], 0x0F0F0F0Fu), ahi = opaque_and(wa[k], 0xF0F0F0F0u);
+      const uint32_t blo = opaque_and(wb[k], 0x0F0F0F0Fu), bhi = opaque_and(wb[k], 0xF0F0F0F0u);
+      const float4 xa = *reinterpret_cast<const float4*>(xb + 8 * k);
+      const float4 xc = *reinterpret_cast<const float4*>(xb + 8 * k + 4);
+      al += ub0(alo) * xa.x;
+      ah += ub0(ahi) * xa.y;
+      al += ub1(alo) * xa.z;
+      ah += ub1(ahi) * xa.w;
+      al += ub2(alo) * xc.x;
+      ah += ub2(ahi) * xc.y;
+      al += ub3(alo) * xc.z;
+      ah += ub3(ahi) * xc.w;
+      bl += ub0(blo) * xa.x;
+      bh += ub0(bhi) * xa.y;
+      bl += ub1(blo) * xa.z;
+      bh += ub1(bhi) * xa.w;
+      bl += ub2(blo) * xc.x;
+      bh += ub2(bhi) * xc.y;
+      bl += ub3(blo) * xc.z;
+      bh += ub3(bhi) * xc.w;
+    }
+    // same operation order as q4_group_dot for each matrix
+    const float sa = al + ah * 0.0625f, sb = bl + bh * 0.0625f;
+    if (j == 0) {
+      ra = u2f(A[0]) * (sa - 8.0f * bs[0]);
+      rb = u2f(B[0]) * (sb - 8.0f * bs[0]);
+    } else {
+      ra += u2f(A[5 * j]) * (sa - 8.0f * bs[j]);
+      rb += u2f(B[5 * j]) * (sb - 8.0f * bs[j]);
+    }
+  }
+}
+
 struct GateUpFmt {  // shaders/fused_mlp_q4.wgsl: act = gelu_tanh(Wg x) * (Wu x)
   static constexpr uint32_t kGroupBytes = 80, kBlockBytes = 20;
-  // Sub-items: each (row, group) is walked twice, gate then up, so a lane
-  // holds one 80-B group per look-ahead slot instead of two.
-  static constexpr uint32_t kSub = 2;
   struct Item {
-    Q4G w;
+    Q4G g, u;
   };
   struct Acc {
     float g, u;
@@ -337,15 +387,17 @@ struct GateUpFmt {  // shaders/fused_mlp_q4.wgsl: act = gelu_tanh(Wg x) * (Wu x)
     const uint8_t* Wu;
     float* Y;
   };
-  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t sub) {
-    it.w = load_q4g((sub ? a.Wu : a.Wg) + off);
+  __device__ static void load(Item& it, const Args& a, size_t off) {
+    it.g = load_q4g(a.Wg + off);
+    it.u = load_q4g(a.Wu + off);
   }
   __device__ static void init(Acc& c) { c.g = c.u = 0.f; }
   __device__ static void zero(Acc& c) { c.g = c.u = 0.f; }
-  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
-                             uint32_t sub) {
-    const float d = valid * q4_group_dot(it.w, xg, bs);
-    if (sub) c.u += d; else c.g += d;
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid) {
+    float g, u;
+    q4_group_dot2(it.g, it.u, xg, bs, g, u);
+    c.g += valid * g;
+    c.u += valid * u;
   }
   template <int TPR>
   __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
@@ -382,7 +434,7 @@ __device__ __forceinline__ float q8_group_dot(const Q8G& g, const float* xg, con
 }
 
 struct Q8Fmt {  // shaders/gemv_q8.wgsl
-  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 1;
+  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36;
   struct Item {
     Q8G w;
   };
@@ -393,13 +445,12 @@ struct Q8Fmt {  // shaders/gemv_q8.wgsl
     const uint8_t* W;
     float* Y;
   };
-  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
+  __device__ static void load(Item& it, const Args& a, size_t off) {
     load_q8g(it.w, a.W + off);
   }
   __device__ static void init(Acc& c) { c.s = 0.f; }
   __device__ static void zero(Acc& c) { c.s = 0.f; }
-  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
-                             uint32_t) {
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid) {
     c.s += valid * q8_group_dot(it.w, xg, bs);
   }
   template <int TPR>
@@ -411,22 +462,63 @@ struct Q8Fmt {  // shaders/gemv_q8.wgsl
   __device__ static void block_end(const Acc&, const Args&, float*) {}
 };
 
+__device__ __forceinline__ void q8_group_dot2(const Q8G& a, const Q8G& b, const float* xg,
+                                              const float* bs, float& ra, float& rb) {
+  uint32_t A[36], B[36];
+#pragma unroll
+  for (int k = 0; k < 9; k++) {
+    A[4 * k + 0] = a.v[k].x;
+    A[4 * k + 1] = a.v[k].y;
+    A[4 * k + 2] = a.v[k].z;
+    A[4 * k + 3] = a.v[k].w;
+    B[4 * k + 0] = b.v[k].x;
+    B[4 * k + 1] = b.v[k].y;
+    B[4 * k + 2] = b.v[k].z;
+    B[4 * k + 3] = b.v[k].w;
+  }
+  ra = 0.f;
+  rb = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float* xb = xg + 32 * j;
+    float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t ua = opaque_and(A[9 * j + 1 + k] ^ 0x80808080u, 0xFFFFFFFFu);
+      const uint32_t ub = opaque_and(B[9 * j + 1 + k] ^ 0x80808080u, 0xFFFFFFFFu);
+      const float4 xa = *reinterpret_cast<const float4*>(xb + 4 * k);
+      a0 += ub0(ua) * xa.x;
+      a1 += ub1(ua) * xa.y;
+      a0 += ub2(ua) * xa.z;
+      a1 += ub3(ua) * xa.w;
+      b0 += ub0(ub) * xa.x;
+      b1 += ub1(ub) * xa.y;
+      b0 += ub2(ub) * xa.z;
+      b1 += ub3(ub) * xa.w;
+    }
+    ra += u2f(A[9 * j]) * ((a0 + a1) - 128.0f * bs[j]);
+    rb += u2f(B[9 * j]) * ((b0 + b1) - 128.0f * bs[j]);
+  }
+}
+
 struct GateUpQ8Fmt {  // shaders/fused_mlp_q8.wgsl (--q8 layers)
-  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 2;
+  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36;
   struct Item {
-    Q8G w;
+    Q8G g, u;
   };
   using Acc = GateUpFmt::Acc;
   using Args = GateUpFmt::Args;
-  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t sub) {
-    load_q8g(it.w, (sub ? a.Wu : a.Wg) + off);
+  __device__ static void load(Item& it, const Args& a, size_t off) {
+    load_q8g(it.g, a.Wg + off);
+    load_q8g(it.u, a.Wu + off);
   }
   __device__ static void init(Acc& c) { c.g = c.u = 0.f; }
   __device__ static void zero(Acc& c) { c.g = c.u = 0.f; }
-  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
-                             uint32_t sub) {
-    const float d = valid * q8_group_dot(it.w, xg, bs);
-    if (sub) c.u += d; else c.g += d;
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid) {
+    float g, u;
+    q8_group_dot2(it.g, it.u, xg, bs, g, u);
+    c.g += valid * g;
+    c.u += valid * u;
   }
   template <int TPR>
   __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
@@ -448,7 +540,7 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 // writes one partial, and the last block to finish reduces the partials in
 // block order and writes the token.  Logits are stored only when Y != null.
 struct Q8ArgmaxFmt {
-  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36, kSub = 1;
+  static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36;
   using Item = Q8Fmt::Item;
   struct Acc {
     float s, bv;
@@ -461,7 +553,7 @@ struct Q8ArgmaxFmt {
     uint32_t* counter;  // zero between launches
     uint32_t* token;
   };
-  __device__ static void load(Item& it, const Args& a, size_t off, uint32_t) {
+  __device__ static void load(Item& it, const Args& a, size_t off) {
     load_q8g(it.w, a.W + off);
   }
   __device__ static void init(Acc& c) {
@@ -470,8 +562,7 @@ struct Q8ArgmaxFmt {
     c.bi = 0xFFFFFFFFu;
   }
   __device__ static void zero(Acc& c) { c.s = 0.f; }
-  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid,
-                             uint32_t) {
+  __device__ static void fma(Acc& c, const Item& it, const float* xg, const float* bs, float valid) {
     c.s += valid * q8_group_dot(it.w, xg, bs);
   }
   template <int TPR>
@@ -556,12 +647,15 @@ struct Q8ArgmaxFmt {
 // t + 2T, ... (T = teams in the grid); lane l of a team owns groups
 // l, l + TPR, ..., l + (GPL-1) TPR of each of its rows.  A lane walks its
 // items in order through a ring of D item buffers: while item i is reduced,
-// items i+1 .. i+D-1 are in flight, so each wave keeps D-1 groups of HBM
-// traffic outstanding through its compute.  The ring is unrolled so no
-// register copies (which would force an early wait) are needed.  Items past
-// the end (group >= ng, or look-ahead beyond the last row) load an in-range
-// duplicate and contribute zero.  Teams with no rows skip the stream but
-// still take part in the block-wide prologue and epilogue.
+// items i+1 .. i+D-1 are in flight.  D = 1 keeps one item per lane in flight
+// and relies on the other waves of the CU to cover the latency; on MI355X
+// that reads faster than deeper per-lane look-ahead at these sizes (more
+// outstanding requests per CU than the memory system serves well).  The
+// ring is unrolled so no register copies (which would force an early wait)
+// are needed.  Items past the end of a row (group >= ng) load an in-range
+// duplicate and contribute zero; nothing is loaded beyond a team's last
+// item.  Teams with no rows skip the stream but still take part in the
+// block-wide prologue and epilogue.
 // ------------------------------------------------------------------------
 template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
@@ -577,15 +671,13 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
   const uint32_t team = blockIdx.x * TEAMS + threadIdx.x / TPR;
   const uint32_t nteams = gridDim.x * TEAMS;
   const bool active = team < M;
-  constexpr uint32_t PER_ROW = GPL * F::kSub;  // items per row for one lane
+  constexpr uint32_t PER_ROW = GPL;  // items per row for one lane
   const uint32_t n_items = active ? ((M - 1 - team) / nteams + 1) * PER_ROW : 0;
   const size_t row_bytes = (size_t)nb * F::kBlockBytes;
 
-  // item i -> row (i / PER_ROW), lane group slot ((i % PER_ROW) / kSub),
-  // sub-matrix (i % kSub)
-  auto group_of = [&](uint32_t i) -> uint32_t { return lr + ((i % PER_ROW) / F::kSub) * TPR; };
+  // item i -> row (i / PER_ROW), lane group slot (i % PER_ROW)
+  auto group_of = [&](uint32_t i) -> uint32_t { return lr + (i % PER_ROW) * TPR; };
   auto offset_of = [&](uint32_t i) -> size_t {
-    i = i < n_items ? i : n_items - 1;
     const uint32_t row = team + (i / PER_ROW) * nteams;
     uint32_t g = group_of(i);
     g = g < ng ? g : ng - 1;
@@ -595,13 +687,13 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
   // The first D items' weight loads go out before x is staged, so the x
   // round trip through L2 overlaps the weight latency.
   typename F::Item buf[D];
-  if (active) {
 #pragma unroll
-    for (int d = 0; d < D; d++) F::load(buf[d], a, offset_of(d), d % F::kSub);
-  }
+  for (int d = 0; d < D; d++)
+    if (d < n_items) F::load(buf[d], a, offset_of(d));
   stage_x_pro<NT, NORMED>(xp, K, xs, bsum, ext);
   typename F::Acc acc;
   F::init(acc);
+#pragma unroll 1
   for (uint32_t base = 0; base < n_items; base += D) {
 #pragma unroll
     for (int d = 0; d < D; d++) {
@@ -609,14 +701,13 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
       if (i < n_items) {  // uniform within a team
         const uint32_t g = group_of(i);
         const uint32_t gc = g < ng ? g : ng - 1;
-        F::fma(acc, buf[d], xs + gc * GROUP_STRIDE, bsum + gc * 4, g < ng ? 1.0f : 0.0f,
-               i % F::kSub);
+        F::fma(acc, buf[d], xs + gc * GROUP_STRIDE, bsum + gc * 4, g < ng ? 1.0f : 0.0f);
         if (i % PER_ROW == PER_ROW - 1) {
           F::template finish<TPR>(acc, a, team + (i / PER_ROW) * nteams, lr == 0);
           F::zero(acc);
         }
       }
-      F::load(buf[d], a, offset_of(i + D), (i + D) % F::kSub);
+      if (i + D < n_items) F::load(buf[d], a, offset_of(i + D));
     }
   }
   F::template block_end<NT>(acc, a, ext);
@@ -659,9 +750,11 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 #define GH_SHAPES(X, D) X(16, 1, D) X(32, 1, D) X(64, 1, D) X(32, 2, D) X(64, 2, D) X(32, 4, D) X(64, 4, D)
 
 #if defined(GH_GEMV_NORMED)
+GH_SHAPES(GH_NORMED, 1)
 GH_SHAPES(GH_NORMED, 2)
 GH_SHAPES(GH_NORMED, 3)
 #else
+GH_SHAPES(GH_PLAIN, 1)
 GH_SHAPES(GH_PLAIN, 2)
 GH_SHAPES(GH_PLAIN, 3)
 #endif

@@ -2,6 +2,7 @@
 // record* helpers (src/gpu/kernels.zig:80-142): shape checks, launch-shape
 // selection, and the launch on the context stream.
 #include <stdlib.h>
+#include <string.h>
 
 #include <string>
 
@@ -24,7 +25,7 @@ unsigned x_lds_bytes(uint32_t K);
 // Lanes per row team (TPR) and 4-block groups per lane per row (GPL) with
 // TPR * GPL >= the row's group count and the least idle lanes; then a
 // persistent grid of wgs_per_cu workgroups per CU (bounded by LDS).
-GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K) {
+GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8) {
   const uint32_t ng = K / 128;
   static const int kT[] = {16, 32, 64};
   int best_t = 64, best_g = 4;
@@ -42,12 +43,14 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K) {
     }
     if (best_waste != ~0u) break;  // prefer one group per lane per row
   }
-  GemvCfg c{best_t, best_g, 4, 3};
+  // Measured on MI355X (graph replay, 12B decode shapes): one item in flight
+  // per lane and 3 (Q4) or 2 (Q8) workgroups per CU read fastest.
+  GemvCfg c{best_t, best_g, q8 ? 2 : 3, 1};
   if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning override "tpr,gpl,wgs_per_cu,depth"
     int t = 0, g = 0, w = 0, d = 0;
     if (sscanf(env, "%d,%d,%d,%d", &t, &g, &w, &d) == 4 && (t == 16 || t == 32 || t == 64) &&
         (g == 1 || g == 2 || g == 4) && !(t == 16 && g > 1) && w >= 1 && w <= 32 &&
-        (uint32_t)(t * g) >= ng && d >= 2 && d <= 3) {
+        (uint32_t)(t * g) >= ng && d >= 1 && d <= 3) {
       c = {t, g, w, d};
     }
   }
@@ -80,7 +83,7 @@ namespace gh {
 
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out) {
-  GemvCfg c = pick_gemv(ctx, M, K);
+  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr);
   out->lds = x_lds_bytes(K) + 64;
   if (out->lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
   out->name = std::string(family) + (normed ? "n" : "") + "_t" + std::to_string(c.tpr) + "_g" +
@@ -89,9 +92,18 @@ gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_
   // last workgroups as a second, mostly idle wave.
   const int occ = ctx->occupancy(out->name, 256, out->lds);
   if (occ <= 0) return fail(GH_ERR_CODE_OBJECT, "kernel not found in the code objects: " + out->name);
+  // The same number of workgroups on every CU (a multiple of the CU count)
+  // measured faster than fewer workgroups with an equal row count per team.
   const uint32_t teams_per_wg = 256 / c.tpr;
-  const uint32_t max_grid = (M + teams_per_wg - 1) / teams_per_wg;
-  out->grid = std::min<uint32_t>(max_grid, (uint32_t)ctx->num_cus * std::min(c.wgs_per_cu, occ));
+  const uint32_t cap = (uint32_t)ctx->num_cus * (uint32_t)std::min(c.wgs_per_cu, occ);
+  out->grid = std::min<uint32_t>(cap, (M + teams_per_wg - 1) / teams_per_wg);
+  if (const char* env = getenv("GH_GEMV_GRID")) {  // tuning: "bal" = balanced rows per team
+    if (env[0] == 'b') {
+      const uint32_t rows_per_team = (M + cap * teams_per_wg - 1) / (cap * teams_per_wg);
+      const uint32_t rows_per_wg = rows_per_team * teams_per_wg;
+      out->grid = (M + rows_per_wg - 1) / rows_per_wg;
+    }
+  }
   return GH_OK;
 }
 

@@ -7,9 +7,11 @@ Weights are rotated over several distinct copies so every step streams its
 110.6 MB from HBM rather than from the 256 MB Infinity Cache.
 
 Printed as one JSON line: value = MLP HBM GB/s (algorithmic bytes / wall time
-of the K timed steps), plus the dominant kernel's roofline, the CPU baseline
-(the oracle's restatement of the reference CPU path, timed on this host) and
-secondary figures (single Q4_0 GEMV 8192 x 2048).
+of the K timed steps, recorded once as a HIP graph and replayed, as the decode
+step runs), plus the dominant kernel's roofline (gate+up, its duration from
+HIP events around K back-to-back launches of it alone), the CPU baseline (the
+oracle's restatement of the reference CPU path, timed on this host) and
+secondary figures (single Q4_0 GEMV 8192 x 2048, the 12B-shaped decode).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -59,52 +61,56 @@ def bench_mlp(ctx, steps, warmup):
     x = (xr / np.sqrt(np.mean(xr * xr) + 1e-6) * w).astype(np.float32)
     X, ACT, OUT = ctx.upload(x), ctx.alloc(I * 4), ctx.alloc(H * 4)
 
-    def step(i, evs=None):
-        wg, wu, wd = copies[i % ncopy]
-        if evs is not None:
-            ctx.record(evs[0])
+    def gate_up(i):
+        wg, wu, _ = copies[i % ncopy]
         ctx.gate_up_geglu_q4(wg, wu, X, ACT, I, H)
-        if evs is not None:
-            ctx.record(evs[1])
-        ctx.gemv_q4(wd, ACT, OUT, H, I)
-        if evs is not None:
-            ctx.record(evs[2])
 
-    for i in range(warmup):
-        step(i)
-    ctx.sync()
-    # timed region: the K steps launched back to back on the context stream,
-    # an event on each side of every kernel (same stream) for the roofline.
-    evs = [[ctx.event() for _ in range(3)] for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(i, evs[i])
-    ctx.sync()
-    wall = time.perf_counter() - t0
-    gu_ms = [ctx.elapsed_ms(e[0], e[1]) for e in evs]
-    dn_ms = [ctx.elapsed_ms(e[1], e[2]) for e in evs]
-    gpu_ms = ctx.elapsed_ms(evs[0][0], evs[-1][2])
-    for e in evs:
-        for v in e:
-            ctx.destroy_event(v)
-    # the same K steps recorded once and replayed as one graph (how the decode
-    # step runs); reported beside the direct launches
-    ctx.graph_begin()
-    for i in range(steps):
-        step(i)
-    g = ctx.graph_end()
-    ctx.graph_launch(g)
+    def down(i):
+        ctx.gemv_q4(copies[i % ncopy][2], ACT, OUT, H, I)
+
+    def record(n, parts):
+        ctx.graph_begin()
+        for i in range(n):
+            for f in parts:
+                f(i)
+        return ctx.graph_end()
+
+    # The K steps are recorded once as a HIP graph (how the decode step runs
+    # them) and replayed; the warmup is a replay of W steps.
+    g_warm = record(max(1, warmup), (gate_up, down))
+    g_step = record(steps, (gate_up, down))
+    g_gu = record(steps, (gate_up,))
+    g_dn = record(steps, (down,))
+    ctx.graph_launch(g_warm)
     ctx.sync()
     e0, e1 = ctx.event(), ctx.event()
+    # timed region: K steps, synchronized on both sides
+    t0 = time.perf_counter()
     ctx.record(e0)
-    ctx.graph_launch(g)
+    ctx.graph_launch(g_step)
     ctx.record(e1)
-    graph_ms = ctx.elapsed_ms(e0, e1)
-    ctx.graph_destroy(g)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    step_ms = ctx.elapsed_ms(e0, e1)
+    # per-kernel durations for the roofline: the same K launches of one
+    # kernel alone, events on the context stream around the replay
+    per_kernel = []
+    for g in (g_gu, g_dn):
+        ctx.graph_launch(g)
+        ctx.sync()
+        ctx.record(e0)
+        ctx.graph_launch(g)
+        ctx.record(e1)
+        ctx.sync()
+        per_kernel.append(ctx.elapsed_ms(e0, e1) / steps)
+    for g in (g_warm, g_step, g_gu, g_dn):
+        ctx.graph_destroy(g)
+    ctx.destroy_event(e0)
+    ctx.destroy_event(e1)
     out = OUT.read(np.float32, H)
     assert np.all(np.isfinite(out))
     host_w = [b.read(np.uint32) for b in copies[0]]
-    return wall, float(np.mean(gu_ms)), float(np.mean(dn_ms)), gpu_ms, graph_ms, x, host_w
+    return wall, step_ms, per_kernel[0], per_kernel[1], x, host_w
 
 
 def bench_gemv(ctx, reps=256):
@@ -206,6 +212,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the 12B decode leg")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the 12B decode leg and print its figures (for profiling)")
+    ap.add_argument("--prompt", type=int, default=512, help="decode leg: prompt tokens")
+    ap.add_argument("--decode", type=int, default=128, help="decode leg: greedy steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: the decode backend has no multi-GPU path "
@@ -214,14 +224,18 @@ def main():
 
     ctx = gh.Context()
     log("device:", ctx.device_name)
-    wall, gu_ms, dn_ms, gpu_ms, graph_ms, x, host_w = bench_mlp(ctx, args.steps, args.warmup)
+    if args.decode_only:
+        print(json.dumps({"decode_12b": bench_decode(ctx, args.prompt, args.decode)}), flush=True)
+        ctx.close()
+        return
+    wall, step_ms, gu_ms, dn_ms, x, host_w = bench_mlp(ctx, args.steps, args.warmup)
     gu_bytes = 2 * I * Q4_ROW(H) + H * 4 + I * 4
     dn_bytes = H * Q4_ROW(I) + I * 4 + H * 4
     step_bytes = gu_bytes + dn_bytes
     value = step_bytes * args.steps / wall / 1e9
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
     gemv_gbs, gemv_us = bench_gemv(ctx)
-    dec = bench_decode(ctx) if not args.no_decode else None
+    dec = bench_decode(ctx, args.prompt, args.decode) if not args.no_decode else None
     if dec:
         log("decode %.1f tok/s (%.3f ms/token), prefill %.1f tok/s"
             % (dec["decode_tok_s"], dec["decode_ms_per_token"], dec["prefill_tok_s"]))
@@ -231,7 +245,8 @@ def main():
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("gh_gateup_q4", None)
+        rec = json.load(open(tpath)).get("gh_gateup_q4")
+        traffic = rec["hbm_bytes"] if rec else None
 
     cpu = None
     if not args.no_cpu:
@@ -263,8 +278,7 @@ def main():
                      "avg_launch_us": round(gu_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": {"mlp_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-                  "mlp_gbs_event_timed": round(step_bytes * args.steps / (gpu_ms * 1e-3) / 1e9, 1),
-                  "mlp_gbs_graph_replay": round(step_bytes * args.steps / (graph_ms * 1e-3) / 1e9, 1),
+                  "mlp_gbs_event_timed": round(step_bytes * args.steps / (step_ms * 1e-3) / 1e9, 1),
                   "down_proj_us": round(dn_ms * 1e3, 3),
                   "down_proj_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
                   "gemv_q4_8192x2048_gbs": round(gemv_gbs, 1),

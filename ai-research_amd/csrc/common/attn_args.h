@@ -13,9 +13,8 @@ struct AttnArgs {
   float* v_cache;
   const uint32_t* active;  // [S] slot numbers (src/ring_buffer.zig getActiveSlots)
   const uint32_t* step;    // {clock, slot_idx, S, 0}
-  float* part;             // [nkv][nsplit][G][D + 4] partial (o, m, l, pad)
-  uint32_t* counters;      // [nkv], zero between launches
-  float* out;              // [nq][D]
+  float* part;             // [nkv][nsplit][G][D + 4] split partials (o, m, l, pad)
+  float* out;              // [nq][D], written by the merge kernel
   uint32_t nq, nkv, D, rot, k_eq_v, nsplit, fuse;
   float theta, eps, scale;
 };

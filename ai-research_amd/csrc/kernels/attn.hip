@@ -10,15 +10,15 @@
 // slots), active slot list u32[S], step params u32 {clock, slot_idx, S, 0}
 // read on the device like the reference's Step_params buffer.
 //
-// Attention design: one workgroup per (kv head, split of the active list).
-// The G = nq / nkv query heads of a kv head share every K/V load (GQA bytes
-// are read once).  A wavefront owns 64 lanes x DPL = D dims of a slot (one
-// 16-byte load per lane per K or V row for D = 256); its waves take slots
-// round-robin with two slots in flight, keep an online softmax (running max,
-// running sum, rescaled output) per query head, and merge through LDS.  Each
-// split writes (m, l, o) partials; the last split of a kv head to finish
-// (device-scope counter, self-resetting) merges them in split order, so the
-// result does not depend on scheduling.
+// Attention design: one workgroup per (kv head, split of the active list),
+// then a small merge kernel.  The G = nq / nkv query heads of a kv head share
+// every K/V load (GQA bytes are read once).  A wavefront owns all D dims of a
+// slot (one 16-byte load per lane per K or V row for D = 256) and walks its
+// slots in tiles: a tile's loads go out together, its scores are reduced
+// together (DPP inside rows of 16 lanes), and the online softmax is updated
+// once per tile.  Waves merge through LDS; each split writes (o, m, l); the
+// merge kernel combines the splits in split order, so the result does not
+// depend on scheduling.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -102,11 +102,28 @@ extern "C" __global__ __launch_bounds__(64) void gh_qkv_rope_k(
 // ---------------------------------------------------------------------------
 #include "../common/attn_args.h"
 
+// Full-wavefront sum with every lane receiving the same, bit-identical total:
+// DPP butterflies inside each row of 16 lanes (xor 1, xor 2, half-row
+// mirror, row mirror), then two cross-row exchanges.  Each step adds a value
+// to its partner's in a commutative pair, so all lanes end with one value.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_allsum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 template <int DPL>
 __device__ __forceinline__ void load_row(const float* p, float* r) {
-  if constexpr (DPL == 4) {
-    const float4 t = *reinterpret_cast<const float4*>(p);
-    r[0] = t.x; r[1] = t.y; r[2] = t.z; r[3] = t.w;
+  if constexpr (DPL == 1) {
+    r[0] = p[0];
   } else if constexpr (DPL == 2) {
     const float2 t = *reinterpret_cast<const float2*>(p);
     r[0] = t.x; r[1] = t.y;
@@ -119,13 +136,80 @@ __device__ __forceinline__ void load_row(const float* p, float* r) {
   }
 }
 
+// Stage one head (D floats) normalised -- in * (mean(in^2) + eps)^-1/2 * w,
+// w == nullptr meaning ones -- into LDS, one wavefront, one global read.
 template <int DPL>
-__device__ __forceinline__ void attn_body(const AttnArgs& a) {
+__device__ __forceinline__ void norm_head_to_lds(const float* __restrict__ in,
+                                                 const float* __restrict__ w, float* out,
+                                                 uint32_t D, float eps, uint32_t lane) {
+  float v[DPL];
+  const uint32_t d0 = lane * DPL;
+  const bool dl = d0 < D;
+  if (dl) load_row<DPL>(in + d0, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < DPL; j++) ss += dl ? v[j] * v[j] : 0.f;
+  const float inv = 1.0f / sqrtf(wave_allsum(ss) / (float)D + eps);
+  if (dl) {
+#pragma unroll
+    for (int j = 0; j < DPL; j++) out[d0 + j] = v[j] * inv * (w ? w[d0 + j] : 1.0f);
+  }
+}
+
+// RoPE angles of the pairs a lane rotates: i = lane + 64 k < rot/2, freq =
+// theta^(-2i/rot).  Computed before the head loads return (they depend on
+// nothing loaded) so the transcendental work hides under the load latency.
+#define ROPE_K (MAX_D / 128)
+__device__ __forceinline__ void rope_angles(uint32_t rot, float theta, uint32_t clock,
+                                            uint32_t lane, float* c, float* s) {
+#pragma unroll
+  for (int k = 0; k < ROPE_K; k++) {
+    const uint32_t i = lane + 64 * k;
+    c[k] = 1.f;
+    s[k] = 0.f;
+    if (i < rot / 2) {
+      const float freq = 1.0f / powf(theta, (2.0f * (float)i) / (float)rot);
+      const float ang = (float)clock * freq;
+      c[k] = cosf(ang);
+      s[k] = sinf(ang);
+    }
+  }
+}
+
+// Partial RoPE in place on an LDS head, one wavefront: pairs (i, i + rot/2)
+// for i < rot/2 rotate by the angles of rope_angles.
+__device__ __forceinline__ void rope_lds(float* h, uint32_t rot, const float* c, const float* s,
+                                         uint32_t lane) {
+  const uint32_t half = rot / 2;
+#pragma unroll
+  for (int k = 0; k < ROPE_K; k++) {
+    const uint32_t i = lane + 64 * k;
+    if (i < half) {
+      const float v0 = h[i], v1 = h[i + half];
+      h[i] = v0 * c[k] - v1 * s[k];
+      h[i + half] = v0 * s[k] + v1 * c[k];
+    }
+  }
+}
+
+#define ATT_CHUNK ATT_NT  // active-list indices staged in LDS per round (one per thread)
+
+// One workgroup per (kv head, split of the active list).  Each wavefront
+// owns all D dims of a slot (DPL per lane) and walks the split's slots in
+// tiles of T: the 2T row loads of a tile are issued together, the T x G
+// scores are reduced together, and the online softmax (running max m,
+// running sum l, rescaled output o per query head) is updated once per tile.
+// The waves' states merge through LDS and the split writes its partial
+// (o[D], m, l); gh_attn_merge_k combines the splits.  No inter-workgroup
+// synchronisation inside the kernel: a device-scope fence per workgroup
+// costs more than the whole attention at these sizes.
+template <int DPL, int T>
+__device__ __forceinline__ void attn_split(const AttnArgs& a) {
   __shared__ float qs[MAX_G][MAX_D];
   __shared__ float knew[MAX_D], vnew[MAX_D];
+  __shared__ uint32_t sidx[ATT_CHUNK];
   __shared__ float wm[ATT_WAVES][MAX_G], wl[ATT_WAVES][MAX_G];
   __shared__ float wo[ATT_WAVES][MAX_G][MAX_D];
-  __shared__ uint32_t last_flag;
 
   const uint32_t D = a.D, G = a.nq / a.nkv;
   const uint32_t kvh = blockIdx.x / a.nsplit, split = blockIdx.x % a.nsplit;
@@ -133,25 +217,32 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
   const uint32_t clock = a.step[0], cur_slot = a.step[1], S = a.step[2];
   const size_t kv_dim = (size_t)a.nkv * D;
 
+  // this split's share of the active list, staged in rounds of ATT_CHUNK
+  // indices; the first round's load goes out before the prologue's
+  const uint32_t per = (S + a.nsplit - 1) / a.nsplit;
+  const uint32_t s0 = min(S, split * per), s1 = min(S, s0 + per);
+  const uint32_t n0 = min(s1 - s0, (uint32_t)ATT_CHUNK);
+  const uint32_t idx0 = tid < n0 ? a.active[s0 + tid] : 0u;  // ATT_CHUNK == ATT_NT
+
   // 1. query heads of this kv group (and, fused, this token's K/V) into LDS
   if (a.fuse) {
+    float rc[ROPE_K], rs[ROPE_K];
+    rope_angles(a.rot, a.theta, clock, lane, rc, rs);
     for (uint32_t g = wave; g < G + 2; g += ATT_WAVES) {
-      if (g < G) {
-        const float* in = a.q + (size_t)(kvh * G + g) * D;
-        const float inv = head_inv_rms(in, D, a.eps, lane);
-        norm_rope_head(in, a.q_norm, qs[g], D, a.rot, a.theta, inv, clock, lane);
-      } else if (g == G) {
-        const float* in = a.k_in + (size_t)kvh * D;
-        const float inv = head_inv_rms(in, D, a.eps, lane);
-        norm_rope_head(in, a.k_norm, knew, D, a.rot, a.theta, inv, clock, lane);
-      } else {
-        const float* in = (a.k_eq_v ? a.k_in : a.v_in) + (size_t)kvh * D;
-        const float inv = head_inv_rms(in, D, a.eps, lane);
-        for (uint32_t d = lane; d < D; d += 64) vnew[d] = in[d] * inv;
-      }
+      if (g < G)
+        norm_head_to_lds<DPL>(a.q + (size_t)(kvh * G + g) * D, a.q_norm, qs[g], D, a.eps, lane);
+      else if (g == G)
+        norm_head_to_lds<DPL>(a.k_in + (size_t)kvh * D, a.k_norm, knew, D, a.eps, lane);
+      else
+        norm_head_to_lds<DPL>((a.k_eq_v ? a.k_in : a.v_in) + (size_t)kvh * D, nullptr, vnew, D,
+                              a.eps, lane);
     }
+    if (tid < n0) sidx[tid] = idx0;
+    __syncthreads();
+    for (uint32_t g = wave; g < G + 1; g += ATT_WAVES) rope_lds(g < G ? qs[g] : knew, a.rot, rc, rs, lane);
   } else {
     for (uint32_t i = tid; i < G * D; i += ATT_NT) qs[i / D][i % D] = a.q[(size_t)kvh * G * D + i];
+    if (tid < n0) sidx[tid] = idx0;
   }
   __syncthreads();
   if (a.fuse && split == 0) {  // ring_buffer.writeKV for this layer
@@ -163,11 +254,8 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
     }
   }
 
-  // 2. this split's share of the active list
-  const uint32_t chunk = (S + a.nsplit - 1) / a.nsplit;
-  const uint32_t s0 = split * chunk;
-  const uint32_t s1 = min(S, s0 + chunk);
-  const uint32_t d0 = lane * DPL;  // this lane's dims
+  // 2. online softmax over the split's slots
+  const uint32_t d0 = lane * DPL;
   const bool dl = d0 < D;
   float q[MAX_G][DPL], o[MAX_G][DPL], m[MAX_G], l[MAX_G];
 #pragma unroll
@@ -183,60 +271,66 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
   const float* kbase = a.k_cache + (size_t)kvh * D + d0;
   const float* vbase = a.v_cache + (size_t)kvh * D + d0;
 
-  auto fetch = [&](uint32_t si, float* kr, float* vr) {
-    const uint32_t slot = a.active[si];
-    if (a.fuse && slot == cur_slot) {  // this token's K/V: from LDS, not the cache
+  for (uint32_t r0 = s0; r0 < s1; r0 += ATT_CHUNK) {
+    const uint32_t n = min(s1 - r0, (uint32_t)ATT_CHUNK);
+    if (r0 != s0) {     // the first round was staged with the prologue
+      __syncthreads();  // previous round's indices are no longer read
+      for (uint32_t t = tid; t < n; t += ATT_NT) sidx[t] = a.active[r0 + t];
+      __syncthreads();
+    }
+    for (uint32_t base = wave * T; base < n; base += ATT_WAVES * T) {
+      float kr[T][DPL], vr[T][DPL];
 #pragma unroll
-      for (int j = 0; j < DPL; j++) {
-        kr[j] = dl ? knew[d0 + j] : 0.f;
-        vr[j] = dl ? vnew[d0 + j] : 0.f;
+      for (int j = 0; j < T; j++) {
+        const uint32_t slot = sidx[min(base + j, n - 1)];
+        if (a.fuse && slot == cur_slot) {  // this token's K/V: from LDS, not the cache
+#pragma unroll
+          for (int e = 0; e < DPL; e++) {
+            kr[j][e] = dl ? knew[d0 + e] : 0.f;
+            vr[j][e] = dl ? vnew[d0 + e] : 0.f;
+          }
+        } else if (dl) {
+          load_row<DPL>(kbase + (size_t)slot * kv_dim, kr[j]);
+          load_row<DPL>(vbase + (size_t)slot * kv_dim, vr[j]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; e++) kr[j][e] = vr[j][e] = 0.f;
+        }
       }
-    } else if (dl) {
-      load_row<DPL>(kbase + (size_t)slot * kv_dim, kr);
-      load_row<DPL>(vbase + (size_t)slot * kv_dim, vr);
-    } else {
 #pragma unroll
-      for (int j = 0; j < DPL; j++) kr[j] = vr[j] = 0.f;
+      for (int g = 0; g < MAX_G; g++) {
+        if (g >= (int)G) break;
+        float s[T];
+#pragma unroll
+        for (int j = 0; j < T; j++) {
+          float p = 0.f;
+#pragma unroll
+          for (int e = 0; e < DPL; e++) p += q[g][e] * kr[j][e];
+          s[j] = p;
+        }
+#pragma unroll
+        for (int j = 0; j < T; j++) s[j] = wave_allsum(s[j]) * a.scale;
+        float mt = m[g];
+#pragma unroll
+        for (int j = 0; j < T; j++)
+          if (base + j < n) mt = fmaxf(mt, s[j]);
+        const float corr = __expf(m[g] - mt);  // m = -inf, mt finite: 0
+        l[g] *= corr;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) o[g][e] *= corr;
+#pragma unroll
+        for (int j = 0; j < T; j++) {
+          const float p = base + j < n ? __expf(s[j] - mt) : 0.f;
+          l[g] += p;
+#pragma unroll
+          for (int e = 0; e < DPL; e++) o[g][e] += p * vr[j][e];
+        }
+        m[g] = mt;
+      }
     }
-  };
-  auto consume = [&](const float* kr, const float* vr) {
-#pragma unroll
-    for (int g = 0; g < MAX_G; g++) {
-      if (g >= (int)G) break;
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < DPL; j++) s += q[g][j] * kr[j];
-      s = wave_sum(s) * a.scale;
-      const float mn = fmaxf(m[g], s);
-      const float corr = __expf(m[g] - mn);
-      const float p = __expf(s - mn);
-      l[g] = l[g] * corr + p;
-#pragma unroll
-      for (int j = 0; j < DPL; j++) o[g][j] = o[g][j] * corr + p * vr[j];
-      m[g] = mn;
-    }
-  };
-
-  // four slots in flight per wave
-  uint32_t si = s0 + wave;
-  for (; si + 3 * ATT_WAVES < s1; si += 4 * ATT_WAVES) {
-    float k0[DPL], v0[DPL], k1[DPL], v1[DPL], k2[DPL], v2[DPL], k3[DPL], v3[DPL];
-    fetch(si, k0, v0);
-    fetch(si + ATT_WAVES, k1, v1);
-    fetch(si + 2 * ATT_WAVES, k2, v2);
-    fetch(si + 3 * ATT_WAVES, k3, v3);
-    consume(k0, v0);
-    consume(k1, v1);
-    consume(k2, v2);
-    consume(k3, v3);
-  }
-  for (; si < s1; si += ATT_WAVES) {
-    float k0[DPL], v0[DPL];
-    fetch(si, k0, v0);
-    consume(k0, v0);
   }
 
-  // 3. merge the waves of this workgroup
+  // 3. merge the waves of this workgroup (wave order), write the split partial
 #pragma unroll
   for (int g = 0; g < MAX_G; g++) {
     if (g >= (int)G) break;
@@ -246,7 +340,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
     }
     if (dl) {
 #pragma unroll
-      for (int j = 0; j < DPL; j++) wo[wave][g][d0 + j] = o[g][j];
+      for (int e = 0; e < DPL; e++) wo[wave][g][d0 + e] = o[g][e];
     }
   }
   __syncthreads();
@@ -268,75 +362,77 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
       part[g * PS + D + 1] = L;
     }
   }
-
-  // 4. the last split of this kv head merges all partials in split order
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&a.counters[kvh], 1u);
-    last_flag = (prev == a.nsplit - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  __shared__ float sm[MAX_G][MAX_SPLIT], sc[MAX_G][MAX_SPLIT], sL[MAX_G];
-  const float* allp = a.part + (size_t)kvh * a.nsplit * G * PS;
-  for (uint32_t i = tid; i < G * a.nsplit; i += ATT_NT) {
-    const uint32_t g = i / a.nsplit, sp = i % a.nsplit;
-    sm[g][sp] = allp[(sp * G + g) * PS + D];
-    sc[g][sp] = allp[(sp * G + g) * PS + D + 1];  // l for now
-  }
-  __syncthreads();
-  if (tid < G) {  // per query head: running max, weights c_s, and L
-    float M = -INFINITY;
-    for (uint32_t sp = 0; sp < a.nsplit; sp++) M = fmaxf(M, sm[tid][sp]);
-    float L = 0.f;
-    for (uint32_t sp = 0; sp < a.nsplit; sp++) {
-      const float c = sm[tid][sp] == -INFINITY ? 0.f : __expf(sm[tid][sp] - M);
-      L += sc[tid][sp] * c;
-      sc[tid][sp] = c;
-    }
-    sL[tid] = L;
-  }
-  __syncthreads();
-  const uint32_t D4 = D / 4;
-  for (uint32_t i = tid; i < G * D4; i += ATT_NT) {
-    const uint32_t g = i / D4, d = (i % D4) * 4;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    uint32_t sp = 0;
-    for (; sp + 8 <= a.nsplit; sp += 8) {
-      float4 t[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++)
-        t[u] = *reinterpret_cast<const float4*>(allp + ((sp + u) * G + g) * PS + d);
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const float c = sc[g][sp + u];
-        O.x += t[u].x * c;
-        O.y += t[u].y * c;
-        O.z += t[u].z * c;
-        O.w += t[u].w * c;
-      }
-    }
-    for (; sp < a.nsplit; sp++) {
-      const float4 t = *reinterpret_cast<const float4*>(allp + (sp * G + g) * PS + d);
-      const float c = sc[g][sp];
-      O.x += t.x * c;
-      O.y += t.y * c;
-      O.z += t.z * c;
-      O.w += t.w * c;
-    }
-    const float L = sL[g];
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
-    float* o = a.out + (size_t)(kvh * G + g) * D + d;
-    o[0] = O.x * inv;
-    o[1] = O.y * inv;
-    o[2] = O.z * inv;
-    o[3] = O.w * inv;
-  }
-  if (tid == 0) a.counters[kvh] = 0;  // ready for the next launch
 }
 
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_body<4>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_body<2>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_body<8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { attn_split<1, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_split<2, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_split<4, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_split<8, 4>(a); }
+
+// Combine the split partials of one query head:
+// out = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s.  One workgroup of
+// 256 threads per query head; wave w takes splits w, w + 4, ... and issues
+// all its partial-row loads before consuming any (one L2 round trip for up
+// to 32 splits); the four waves' sums combine in wave order through LDS.
+#define MERGE_U 8
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) {
+  __shared__ float c[MAX_SPLIT];
+  __shared__ float red[ATT_WAVES];
+  __shared__ float4 acc[ATT_WAVES][MAX_D / 4];
+  const uint32_t D = a.D, G = a.nq / a.nkv, h = blockIdx.x, tid = threadIdx.x;
+  const uint32_t lane = tid & 63, wave = tid >> 6;
+  const uint32_t kvh = h / G, g = h % G, PS = D + 4, ns = a.nsplit;
+  const float* allp = a.part + (size_t)kvh * ns * G * PS + (size_t)g * PS;
+  const size_t stride = (size_t)G * PS;  // one split to the next
+  // running max and weights: thread t owns split t (ns <= 256)
+  const float ms = tid < ns ? allp[tid * stride + D] : -INFINITY;
+  const float ls = tid < ns ? allp[tid * stride + D + 1] : 0.f;
+  float M = ms;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float cs = ms == -INFINITY ? 0.f : __expf(ms - M);
+  if (tid < ns) c[tid] = cs;
+  float L = wave_allsum(cs * ls);
+  __syncthreads();  // red[] reads done
+  if (lane == 0) red[wave] = L;
+  __syncthreads();
+  L = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  // weighted column sums: lane -> float4 column, wave -> splits w, w+4, ...
+  const uint32_t D4 = D / 4;
+  for (uint32_t col = lane; col < D4; col += 64) {
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t sp0 = wave; sp0 < ns; sp0 += ATT_WAVES * MERGE_U) {
+      float4 t[MERGE_U];
+#pragma unroll
+      for (int u = 0; u < MERGE_U; u++) {
+        const uint32_t sp = sp0 + u * ATT_WAVES;
+        t[u] = sp < ns ? *reinterpret_cast<const float4*>(allp + sp * stride + col * 4)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < MERGE_U; u++) {
+        const uint32_t sp = sp0 + u * ATT_WAVES;
+        const float w = sp < ns ? c[sp] : 0.f;
+        O.x += t[u].x * w;
+        O.y += t[u].y * w;
+        O.z += t[u].z * w;
+        O.w += t[u].w * w;
+      }
+    }
+    acc[wave][col] = O;
+  }
+  __syncthreads();
+  for (uint32_t col = tid; col < D4; col += ATT_NT) {
+    const float4 a0 = acc[0][col], a1 = acc[1][col], a2 = acc[2][col], a3 = acc[3][col];
+    float4 r;
+    r.x = ((a0.x + a1.x) + (a2.x + a3.x)) * inv;
+    r.y = ((a0.y + a1.y) + (a2.y + a3.y)) * inv;
+    r.z = ((a0.z + a1.z) + (a2.z + a3.z)) * inv;
+    r.w = ((a0.w + a1.w) + (a2.w + a3.w)) * inv;
+    *reinterpret_cast<float4*>(a.out + (size_t)h * D + col * 4) = r;
+  }
+}

@@ -280,17 +280,22 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
   const uint32_t D = L.args.D;
   if (L.args.nkv == 0 || L.args.nq % L.args.nkv != 0 || G > 4)
     return fail(GH_ERR_UNSUPPORTED, "attention: query heads per kv head must be 1..4");
-  int dpl = D <= 128 ? 2 : (D <= 256 ? 4 : 8);
-  if (D > 512 || D % dpl != 0 || D % 4 != 0)
+  if (L.args.nsplit == 0 || L.args.nsplit > 256)
+    return fail(GH_ERR_UNSUPPORTED, "attention: 1..256 splits");
+  const int dpl = D <= 64 ? 1 : (D <= 128 ? 2 : (D <= 256 ? 4 : 8));
+  if (D > 512 || D % 4 != 0 || D % dpl != 0)
     return fail(GH_ERR_UNSUPPORTED, "attention: head_dim must be a multiple of 4 up to 512");
   void* args[] = {const_cast<AttnArgs*>(&L.args)};
-  const char* name = dpl == 2 ? "gh_attn_d2_k" : (dpl == 4 ? "gh_attn_d4_k" : "gh_attn_d8_k");
-  return ctx->launch(name, dim3(L.args.nkv * L.args.nsplit), dim3(256), 0, args);
+  const char* name = dpl == 1 ? "gh_attn_d1_k"
+                     : dpl == 2 ? "gh_attn_d2_k"
+                     : dpl == 4 ? "gh_attn_d4_k" : "gh_attn_d8_k";
+  gh_status st = ctx->launch(name, dim3(L.args.nkv * L.args.nsplit), dim3(256), 0, args);
+  if (st != GH_OK) return st;
+  return ctx->launch("gh_attn_merge_k", dim3(L.args.nq), dim3(256), 0, args);
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {
-  // about 32 slots per split (8 per wave, 4 in flight), at most ~one
-  // workgroup per CU in total
+  // about 32 slots per split (8 per wave), at most ~one workgroup per CU
   uint32_t ns = std::max<uint32_t>(1u, (max_slots + 31) / 32);
   ns = std::min<uint32_t>(ns, std::max<uint32_t>(1u, (uint32_t)ctx->num_cus / std::max(1u, nkv)));
   if (const char* env = getenv("GH_ATTN_SPLITS")) {
@@ -329,14 +334,9 @@ gh_status gh_decode_attn(gh_context* ctx, const float* Q, const float* K_cache,
   a.scale = inv_sqrt_dim;
   a.nsplit = gh::attention_splits(ctx, a.nkv, 1024);
   const size_t part_bytes = (size_t)a.nkv * a.nsplit * gqa_ratio * (head_dim + 4) * 4;
-  if (a.nkv > 256) return fail(GH_ERR_UNSUPPORTED, "gh_decode_attn: more than 256 kv heads");
-  // counters first, at a fixed offset, so a later call with a different
-  // partial size still finds them at zero
-  gh_status st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes,
-                                    256 * 4 + part_bytes);
+  gh_status st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes, part_bytes);
   if (st != GH_OK) return st;
-  a.counters = static_cast<uint32_t*>(ctx->attn_scratch);
-  a.part = reinterpret_cast<float*>(static_cast<char*>(ctx->attn_scratch) + 256 * 4);
+  a.part = static_cast<float*>(ctx->attn_scratch);
   return gh::launch_attention(ctx, L);
 }
 

@@ -51,7 +51,7 @@ struct gh_model {
   size_t arena_bytes = 0;
   size_t lm_head = 0, final_norm = 0;
   size_t x0 = 0, x1 = 0, qkv_out = 0, attn_out = 0, o_out = 0, act = 0, m_out = 0, logits = 0;
-  size_t token = 0, step = 0, active = 0, attn_part = 0, attn_cnt = 0, amax = 0;
+  size_t token = 0, step = 0, active = 0, attn_part = 0, amax = 0;
   uint32_t nsplit = 1, max_q = 0, max_kv = 0;
   size_t hidden_final = 0;       // which x buffer holds the residual stream after a step
   uint16_t* embed_dev = nullptr; // synthetic models only
@@ -173,7 +173,6 @@ gh_status plan(gh_model* m) {
     max_d = std::max(max_d, L.head_dim);
   }
   m->nsplit = gh::attention_splits(m->ctx, max_nkv, c.max_slots);
-  m->attn_cnt = take(256 * 4);
   m->attn_part = take((size_t)max_nkv * m->nsplit * max_g * (max_d + 4) * 4);
   m->amax = take((64 + 2 * 4096) * 4);
   m->arena_bytes = off;
@@ -292,7 +291,6 @@ gh_status record_forward(gh_model* m, bool logits) {
     a.active = m->at<uint32_t>(m->active);
     a.step = m->at<uint32_t>(m->step);
     a.part = m->at<float>(m->attn_part);
-    a.counters = m->at<uint32_t>(m->attn_cnt);
     a.out = m->at<float>(m->attn_out);
     a.nq = c.num_attention_heads;
     a.nkv = L.nkv;

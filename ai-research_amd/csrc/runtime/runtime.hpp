@@ -17,9 +17,9 @@ struct gh_context {
   int num_cus = 0;
   size_t max_lds = 0;
   std::vector<hipModule_t> modules;
-  // Scratch of the standalone split-K attention and argmax entry points:
-  // partial records plus last-block counters, zero-filled when (re)allocated
-  // and left at zero by every launch.
+  // Scratch of the standalone split-K attention (split partials) and argmax
+  // (partials plus a last-block counter that every launch leaves at zero)
+  // entry points, zero-filled when (re)allocated.
   void* attn_scratch = nullptr;
   size_t attn_scratch_bytes = 0;
   void* argmax_scratch = nullptr;

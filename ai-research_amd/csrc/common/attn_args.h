@@ -17,4 +17,10 @@ struct AttnArgs {
   float* out;              // [nq][D], written by the merge kernel
   uint32_t nq, nkv, D, rot, k_eq_v, nsplit, fuse;
   float theta, eps, scale;
+  // batched prefill (gh_pf_* kernels): token t of the batch reads its q at
+  // q + t * q_stride, its active list at active + t * active_stride (length
+  // n_active[t]), and writes its output at out_rows + t * out_stride.
+  const uint32_t* n_active;
+  float* out_rows;
+  uint32_t q_stride, active_stride, out_stride;
 };

@@ -203,7 +203,7 @@ __device__ __forceinline__ void rope_lds(float* h, uint32_t rot, const float* c,
 // (o[D], m, l); gh_attn_merge_k combines the splits.  No inter-workgroup
 // synchronisation inside the kernel: a device-scope fence per workgroup
 // costs more than the whole attention at these sizes.
-template <int DPL, int T>
+template <int DPL, int T, bool PF>
 __device__ __forceinline__ void attn_split(const AttnArgs& a) {
   __shared__ float qs[MAX_G][MAX_D];
   __shared__ float knew[MAX_D], vnew[MAX_D];
@@ -212,20 +212,28 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
   __shared__ float wo[ATT_WAVES][MAX_G][MAX_D];
 
   const uint32_t D = a.D, G = a.nq / a.nkv;
-  const uint32_t kvh = blockIdx.x / a.nsplit, split = blockIdx.x % a.nsplit;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t clock = a.step[0], cur_slot = a.step[1], S = a.step[2];
   const size_t kv_dim = (size_t)a.nkv * D;
+  // decode: one split of one token; prefill: all of token blockIdx.y's list
+  const uint32_t nsplit = PF ? 1u : a.nsplit;
+  const uint32_t kvh = PF ? blockIdx.x : blockIdx.x / nsplit;
+  const uint32_t split = PF ? 0u : blockIdx.x % nsplit;
+  const uint32_t tok = PF ? blockIdx.y : 0u;
+  const uint32_t clock = PF ? 0u : a.step[0], cur_slot = PF ? 0u : a.step[1];
+  const uint32_t S = PF ? a.n_active[tok] : a.step[2];
+  const uint32_t* active = PF ? a.active + (size_t)tok * a.active_stride : a.active;
+  const float* qsrc = PF ? a.q + (size_t)tok * a.q_stride : a.q;
+  const bool fuse = !PF && a.fuse;
 
   // this split's share of the active list, staged in rounds of ATT_CHUNK
   // indices; the first round's load goes out before the prologue's
-  const uint32_t per = (S + a.nsplit - 1) / a.nsplit;
+  const uint32_t per = (S + nsplit - 1) / nsplit;
   const uint32_t s0 = min(S, split * per), s1 = min(S, s0 + per);
   const uint32_t n0 = min(s1 - s0, (uint32_t)ATT_CHUNK);
-  const uint32_t idx0 = tid < n0 ? a.active[s0 + tid] : 0u;  // ATT_CHUNK == ATT_NT
+  const uint32_t idx0 = tid < n0 ? active[s0 + tid] : 0u;  // ATT_CHUNK == ATT_NT
 
   // 1. query heads of this kv group (and, fused, this token's K/V) into LDS
-  if (a.fuse) {
+  if (fuse) {
     float rc[ROPE_K], rs[ROPE_K];
     rope_angles(a.rot, a.theta, clock, lane, rc, rs);
     for (uint32_t g = wave; g < G + 2; g += ATT_WAVES) {
@@ -241,11 +249,11 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
     __syncthreads();
     for (uint32_t g = wave; g < G + 1; g += ATT_WAVES) rope_lds(g < G ? qs[g] : knew, a.rot, rc, rs, lane);
   } else {
-    for (uint32_t i = tid; i < G * D; i += ATT_NT) qs[i / D][i % D] = a.q[(size_t)kvh * G * D + i];
+    for (uint32_t i = tid; i < G * D; i += ATT_NT) qs[i / D][i % D] = qsrc[(size_t)kvh * G * D + i];
     if (tid < n0) sidx[tid] = idx0;
   }
   __syncthreads();
-  if (a.fuse && split == 0) {  // ring_buffer.writeKV for this layer
+  if (fuse && split == 0) {  // ring_buffer.writeKV for this layer
     float* kc = a.k_cache + (size_t)cur_slot * kv_dim + (size_t)kvh * D;
     float* vc = a.v_cache + (size_t)cur_slot * kv_dim + (size_t)kvh * D;
     for (uint32_t d = tid; d < D; d += ATT_NT) {
@@ -275,7 +283,7 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
     const uint32_t n = min(s1 - r0, (uint32_t)ATT_CHUNK);
     if (r0 != s0) {     // the first round was staged with the prologue
       __syncthreads();  // previous round's indices are no longer read
-      for (uint32_t t = tid; t < n; t += ATT_NT) sidx[t] = a.active[r0 + t];
+      for (uint32_t t = tid; t < n; t += ATT_NT) sidx[t] = active[r0 + t];
       __syncthreads();
     }
     for (uint32_t base = wave * T; base < n; base += ATT_WAVES * T) {
@@ -283,7 +291,7 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
 #pragma unroll
       for (int j = 0; j < T; j++) {
         const uint32_t slot = sidx[min(base + j, n - 1)];
-        if (a.fuse && slot == cur_slot) {  // this token's K/V: from LDS, not the cache
+        if (fuse && slot == cur_slot) {  // this token's K/V: from LDS, not the cache
 #pragma unroll
           for (int e = 0; e < DPL; e++) {
             kr[j][e] = dl ? knew[d0 + e] : 0.f;
@@ -345,7 +353,7 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
   }
   __syncthreads();
   const uint32_t PS = D + 4;  // partial record: o[D], m, l (+2 pad: float4 rows)
-  float* part = a.part + ((size_t)kvh * a.nsplit + split) * G * PS;
+  float* part = PF ? nullptr : a.part + ((size_t)kvh * nsplit + split) * G * PS;
   for (uint32_t i = tid; i < G * D; i += ATT_NT) {
     const uint32_t g = i / D, d = i % D;
     float M = -INFINITY;
@@ -356,18 +364,59 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
       L += wl[w][g] * c;
       O += wo[w][g][d] * c;
     }
-    part[g * PS + d] = O;
-    if (d == 0) {
-      part[g * PS + D] = M;
-      part[g * PS + D + 1] = L;
+    if constexpr (PF) {  // the whole list: the final output row of this token
+      a.out_rows[(size_t)tok * a.out_stride + (size_t)(kvh * G + g) * D + d] = L > 0.f ? O / L : 0.f;
+    } else {
+      part[g * PS + d] = O;
+      if (d == 0) {
+        part[g * PS + D] = M;
+        part[g * PS + D + 1] = L;
+      }
     }
   }
 }
 
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { attn_split<1, 8>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_split<2, 8>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_split<4, 8>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_split<8, 4>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { attn_split<1, 8, false>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_split<2, 8, false>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_split<4, 8, false>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_split<8, 4, false>(a); }
+
+// Batched prefill: grid (kv heads, tokens); each workgroup runs token
+// blockIdx.y's whole active list (q already normalised and roped by
+// gh_pf_qkv_rope_k, this batch's K/V already in the caches).
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d1_k(AttnArgs a) { attn_split<1, 8, true>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d2_k(AttnArgs a) { attn_split<2, 8, true>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d4_k(AttnArgs a) { attn_split<4, 8, true>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d8_k(AttnArgs a) { attn_split<8, 4, true>(a); }
+
+// Batched q/k norm + RoPE + cache write (qkv_rope.wgsl for T tokens): grid
+// (nq + nkv heads, tokens), one wavefront each.  Token t's q/k/v rows start
+// at a.q + t * q_stride (q, then k, then v unless k_eq_v); its position and
+// ring slot are clocks[t] and slots[t].
+extern "C" __global__ __launch_bounds__(64) void gh_pf_qkv_rope_k(AttnArgs a,
+                                                                 const uint32_t* clocks,
+                                                                 const uint32_t* slots) {
+  const uint32_t h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, D = a.D;
+  const uint32_t clock = clocks[t], slot = slots[t];
+  float* row = const_cast<float*>(a.q) + (size_t)t * a.q_stride;
+  const size_t q_dim = (size_t)a.nq * D, kv_dim = (size_t)a.nkv * D;
+  if (h < a.nq) {
+    float* q = row + (size_t)h * D;
+    const float inv = head_inv_rms(q, D, a.eps, lane);
+    norm_rope_head(q, a.q_norm, q, D, a.rot, a.theta, inv, clock, lane);
+    return;
+  }
+  const uint32_t kh = h - a.nq;
+  if (kh >= a.nkv) return;
+  const float* kin = row + q_dim + (size_t)kh * D;
+  const float* vin = (a.k_eq_v ? row + q_dim : row + q_dim + kv_dim) + (size_t)kh * D;
+  float* kc = a.k_cache + (size_t)slot * kv_dim + (size_t)kh * D;
+  float* vc = a.v_cache + (size_t)slot * kv_dim + (size_t)kh * D;
+  const float kinv = head_inv_rms(kin, D, a.eps, lane);
+  norm_rope_head(kin, a.k_norm, kc, D, a.rot, a.theta, kinv, clock, lane);
+  const float vinv = head_inv_rms(vin, D, a.eps, lane);
+  for (uint32_t d = lane; d < D; d += 64) vc[d] = vin[d] * vinv;
+}
 
 // Combine the split partials of one query head:
 // out = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s.  One workgroup of

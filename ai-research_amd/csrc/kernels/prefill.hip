@@ -1,0 +1,309 @@
+// prefill.hip -- batched prefill for gfx950: the MFMA Q4_0 / Q8_0 dequant GEMM
+// and the row-wise norm that feeds it.
+//
+// The reference has no batched prefill: it runs prompt tokens one at a time
+// through its decode graph without logits (src/interactive.zig:33-37,
+// src/gpu/model_dispatch.zig:144).  Here the T prompt tokens of a layer go
+// through each projection as one dense contraction
+//     C[T][N] = A[T][K] . deq(W)[N][K]^T
+// on the matrix cores (v_mfma_f32_32x32x16_f16), keeping the decode path's
+// accuracy:
+//  * weights enter exactly: the MFMA B operand is the integer n - 8 (Q4) or
+//    q (Q8), exact in fp16, and each 32-block's f32 scale d is applied to the
+//    block's fp32 partial sum (acc += d * block_sum), as the GEMV does;
+//  * activations are split a = hi + lo with hi = fp16(a), lo = fp16(a - hi),
+//    and both halves go through the MFMA (22+ significant bits of a);
+//  * accumulation is fp32.
+//
+// Tiling: a workgroup of 256 threads (2 x 2 wavefronts) owns a BM x BN tile
+// of C; each wavefront a (BM/2) x (BN/2) sub-tile of 32 x 32 MFMA blocks.  K
+// advances one quant block (32) per step: the A slice (as hi and lo) and the
+// integer W slice with its scales go to LDS (row stride padded to 40 halves
+// so the 16-byte operand reads of 32 consecutive rows spread over all
+// banks), while the next step's global loads are already in flight.
+//
+// MFMA 32x32x16 f16 operand layout (checked on the device): lane l holds
+// A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32], e = 0..7; result
+// register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define PF_NT 256
+#define LDS_STRIDE 40  // halves per LDS row of a 32-wide K slice (+8 pad)
+
+// Weight words through an explicit global-address-space pointer: the matrix
+// is picked at run time (gate or up), which would otherwise degrade to FLAT.
+typedef const uint32_t __attribute__((address_space(1)))* gword_ptr;
+
+struct Q4W {  // src/quant.zig:55-90: {f32 d, 4 words of nibbles}
+  static constexpr uint32_t kBlockBytes = 20;
+  static constexpr int kWords = 3;
+  // half h (elements 16h .. 16h+15) of a block: scale and its 16 values
+  __device__ static void load(const uint8_t* blk, uint32_t h, uint32_t* w) {
+    gword_ptr p = (gword_ptr)(blk);
+    w[0] = p[0];
+    w[1] = p[1 + 2 * h];
+    w[2] = p[2 + 2 * h];
+  }
+  __device__ static void ints(const uint32_t* w, _Float16* out) {  // n - 8
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+      for (int n = 0; n < 8; n++)
+        out[8 * k + n] = (_Float16)((int)((w[1 + k] >> (4 * n)) & 15u) - 8);
+  }
+};
+
+struct Q8W {  // src/quant.zig:20-51: {f32 d, 8 words of int8}
+  static constexpr uint32_t kBlockBytes = 36;
+  static constexpr int kWords = 5;
+  __device__ static void load(const uint8_t* blk, uint32_t h, uint32_t* w) {
+    gword_ptr p = (gword_ptr)(blk);
+    w[0] = p[0];
+#pragma unroll
+    for (int k = 0; k < 4; k++) w[1 + k] = p[1 + 4 * h + k];
+  }
+  __device__ static void ints(const uint32_t* w, _Float16* out) {  // q
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+      for (int n = 0; n < 4; n++) out[4 * k + n] = (_Float16)(int)(int8_t)((w[1 + k] >> (8 * n)) & 0xFFu);
+  }
+};
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // kernels.zig:94-97 / fused_mlp_q4.wgsl:15-18
+  const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// NMAT = 1: C = A W^T.  NMAT = 2: C = gelu_tanh(A Wg^T) * (A Wu^T).  A, C f32.
+template <class F, int BM, int BN, int NMAT>
+__device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
+                                          const uint8_t* __restrict__ W0,
+                                          const uint8_t* __restrict__ W1, float* __restrict__ C,
+                                          uint32_t T, uint32_t N, uint32_t K) {
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave in M and N
+  constexpr int A_PER = BM * 8 / PF_NT;      // 16-byte (4 f32) A chunks per thread per step
+  constexpr int B_ROWS = NMAT * BN;          // weight rows per step
+  constexpr int B_PER = (2 * B_ROWS + PF_NT - 1) / PF_NT;  // half-blocks per thread
+  __shared__ _Float16 Ah[BM * LDS_STRIDE], Al[BM * LDS_STRIDE];
+  __shared__ _Float16 Bs[B_ROWS * LDS_STRIDE];
+  __shared__ float Ds[B_ROWS];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const uint32_t wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const uint32_t nb = K / 32;
+  const size_t row_bytes = (size_t)nb * F::kBlockBytes;
+
+  // global -> register staging of one K step
+  float4 ra[A_PER];
+  uint32_t rb[B_PER][F::kWords];
+  auto load_step = [&](uint32_t kb) {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const uint32_t c = tid + i * PF_NT;  // chunk: row c / 8, 4 floats at 4 (c % 8)
+      uint32_t r = m0 + c / 8;
+      r = r < T ? r : T - 1;
+      ra[i] = *reinterpret_cast<const float4*>(A + (size_t)r * K + kb * 32 + 4 * (c % 8));
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      const uint32_t hb = tid + i * PF_NT;  // half-block: row hb / 2, half hb % 2
+      if (hb < 2 * B_ROWS) {
+        const uint32_t lr = hb / 2, mat = lr / BN;
+        uint32_t r = n0 + lr % BN;
+        r = r < N ? r : N - 1;
+        const uint8_t* W = mat ? W1 : W0;
+        F::load(W + (size_t)r * row_bytes + (size_t)kb * F::kBlockBytes, hb % 2, rb[i]);
+      }
+    }
+  };
+  auto store_step = [&]() {
+#pragma unroll
+    for (int i = 0; i < A_PER; i++) {
+      const uint32_t c = tid + i * PF_NT;
+      const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
+      _Float16 hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        hi[e] = (_Float16)v[e];
+        lo[e] = (_Float16)(v[e] - (float)hi[e]);
+      }
+      const uint32_t o = (c / 8) * LDS_STRIDE + 4 * (c % 8);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        Ah[o + e] = hi[e];
+        Al[o + e] = lo[e];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER; i++) {
+      const uint32_t hb = tid + i * PF_NT;
+      if (hb < 2 * B_ROWS) {
+        _Float16 v[16];
+        F::ints(rb[i], v);
+        _Float16* dst = &Bs[(hb / 2) * LDS_STRIDE + 16 * (hb % 2)];
+        *reinterpret_cast<half8*>(dst) = *reinterpret_cast<const half8*>(v);
+        *reinterpret_cast<half8*>(dst + 8) = *reinterpret_cast<const half8*>(v + 8);
+        if (hb % 2 == 0) Ds[hb / 2] = __uint_as_float(rb[i][0]);
+      }
+    }
+  };
+
+  f32x16 acc[NMAT][TM][TN];
+#pragma unroll
+  for (int q = 0; q < NMAT; q++)
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[q][i][j][r] = 0.f;
+
+  load_step(0);
+  for (uint32_t kb = 0; kb < nb; kb++) {
+    store_step();
+    __syncthreads();
+    if (kb + 1 < nb) load_step(kb + 1);  // in flight through this step's MFMAs
+    half8 ah[2][TM], al[2][TM];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const uint32_t o = (wm + 32 * i + lane % 32) * LDS_STRIDE + 16 * h + 8 * (lane / 32);
+        ah[h][i] = *reinterpret_cast<const half8*>(&Ah[o]);
+        al[h][i] = *reinterpret_cast<const half8*>(&Al[o]);
+      }
+#pragma unroll
+    for (int q = 0; q < NMAT; q++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const uint32_t brow = q * BN + wn + 32 * j + lane % 32;
+        const half8 b0 = *reinterpret_cast<const half8*>(&Bs[brow * LDS_STRIDE + 8 * (lane / 32)]);
+        const half8 b1 = *reinterpret_cast<const half8*>(&Bs[brow * LDS_STRIDE + 16 + 8 * (lane / 32)]);
+        const float d = Ds[brow];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          f32x16 blk = {};
+          blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[0][i], b0, blk, 0, 0, 0);
+          blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[0][i], b0, blk, 0, 0, 0);
+          blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[1][i], b1, blk, 0, 0, 0);
+          blk = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[1][i], b1, blk, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[q][i][j][r] += d * blk[r];
+        }
+      }
+    __syncthreads();  // LDS is rewritten by the next step
+  }
+
+  // epilogue: result register r of lane l -> row 8 (r/4) + 4 (l/32) + r%4, col l % 32
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const uint32_t col = n0 + wn + 32 * j + lane % 32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const uint32_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+        if (row < T && col < N) {
+          if constexpr (NMAT == 1)
+            C[(size_t)row * N + col] = acc[0][i][j][r];
+          else
+            C[(size_t)row * N + col] = gelu_tanh(acc[0][i][j][r]) * acc[1][i][j][r];
+        }
+      }
+    }
+}
+
+#define GH_GEMM(NAME, F, BM, BN)                                                          \
+  extern "C" __global__ __launch_bounds__(PF_NT) void NAME(                               \
+      const float* A, const uint8_t* W, float* C, uint32_t T, uint32_t N, uint32_t K) {   \
+    gemm_tile<F, BM, BN, 1>(A, W, W, C, T, N, K);                                         \
+  }
+#define GH_GEMM_PAIR(NAME, F, BM, BN)                                                     \
+  extern "C" __global__ __launch_bounds__(PF_NT) void NAME(                               \
+      const float* A, const uint8_t* Wg, const uint8_t* Wu, float* Act, uint32_t T,       \
+      uint32_t N, uint32_t K) {                                                           \
+    gemm_tile<F, BM, BN, 2>(A, Wg, Wu, Act, T, N, K);                                     \
+  }
+
+GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128)
+GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64)
+GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128)
+GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64)
+GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64)
+GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64)
+GH_GEMM_PAIR(gh_pf_gateup_q8_m128_n64, Q8W, 128, 64)
+GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64)
+
+// ---------------------------------------------------------------------------
+// Row-wise x prologue for T tokens (the batched form of the decode GEMVs'
+// fused norms, src/gpu/model_dispatch.zig:21,32-34,39-41):
+//   mode 1: xn = RMSNorm(x) * w
+//   mode 2: x <- (x + RMSNorm(r) * wr) * s  (r as given when wr is null),
+//           stored back as the residual stream; xn = RMSNorm(x) * w
+// One workgroup per token row.
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+#define PF_ROW_MAX 32  // elements per thread: hidden <= 8192
+
+extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_norm_k(
+    float* X, const float* R, const float* wr, const float* w, float* Xn, uint32_t H,
+    float s, float eps, uint32_t mode) {
+  __shared__ float red[PF_NT / 64];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  float* x = X + (size_t)t * H;
+  float v[PF_ROW_MAX];
+#pragma unroll
+  for (int u = 0; u < PF_ROW_MAX; u++) {
+    const uint32_t i = tid + u * PF_NT;
+    v[u] = i < H ? x[i] : 0.f;
+  }
+  if (mode == 2) {
+    const float* r = R + (size_t)t * H;
+    float rv[PF_ROW_MAX];
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < PF_ROW_MAX; u++) {
+      const uint32_t i = tid + u * PF_NT;
+      rv[u] = i < H ? r[i] : 0.f;
+      ss += rv[u] * rv[u];
+    }
+    const float inv_r = 1.0f / sqrtf(block_sum<PF_NT>(ss, red) / (float)H + eps);
+#pragma unroll
+    for (int u = 0; u < PF_ROW_MAX; u++) {
+      const uint32_t i = tid + u * PF_NT;
+      if (i < H) {
+        const float rr = wr ? rv[u] * inv_r * wr[i] : rv[u];
+        v[u] = (v[u] + rr) * s;
+        x[i] = v[u];
+      }
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < PF_ROW_MAX; u++) ss += v[u] * v[u];
+  const float inv = 1.0f / sqrtf(block_sum<PF_NT>(ss, red) / (float)H + eps);
+#pragma unroll
+  for (int u = 0; u < PF_ROW_MAX; u++) {
+    const uint32_t i = tid + u * PF_NT;
+    if (i < H) Xn[(size_t)t * H + i] = v[u] * inv * w[i];
+  }
+}

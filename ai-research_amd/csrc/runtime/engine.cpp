@@ -294,6 +294,34 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
   return ctx->launch("gh_attn_merge_k", dim3(L.args.nq), dim3(256), 0, args);
 }
 
+gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
+                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K) {
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
+    return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4 or Q8");
+  if (!W0 || !A || !C || T == 0 || N == 0 || K == 0)
+    return fail(GH_ERR_INVALID, "prefill GEMM: null pointer or zero size");
+  if (K % 32 != 0) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K must be a multiple of 32");
+  if ((reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(W0) & 3) ||
+      (W1 && (reinterpret_cast<uintptr_t>(W1) & 3)))
+    return fail(GH_ERR_INVALID, "prefill GEMM: A must be 16-byte and W 4-byte aligned");
+  const bool pair = W1 != nullptr;
+  const uint32_t cus = (uint32_t)ctx->num_cus;
+  // the large tile when it still gives every CU a workgroup
+  const uint32_t bn_big = pair ? 64 : 128;
+  const bool big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128) >= cus;
+  const uint32_t bm = big ? 128 : 64, bn = big ? bn_big : 64;
+  std::string name = std::string(pair ? "gh_pf_gateup_" : "gh_pf_gemm_") +
+                     (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
+                     std::to_string(bn);
+  dim3 grid((N + bn - 1) / bn, (T + bm - 1) / bm);
+  if (pair) {
+    void* args[] = {&A, const_cast<void**>(&W0), const_cast<void**>(&W1), &C, &T, &N, &K};
+    return ctx->launch(name, grid, dim3(256), 0, args);
+  }
+  void* args[] = {&A, const_cast<void**>(&W0), &C, &T, &N, &K};
+  return ctx->launch(name, grid, dim3(256), 0, args);
+}
+
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {
   // about 32 slots per split (8 per wave), at most ~one workgroup per CU
   uint32_t ns = std::max<uint32_t>(1u, (max_slots + 31) / 32);
@@ -338,6 +366,21 @@ gh_status gh_decode_attn(gh_context* ctx, const float* Q, const float* K_cache,
   if (st != GH_OK) return st;
   a.part = static_cast<float*>(ctx->attn_scratch);
   return gh::launch_attention(ctx, L);
+}
+
+gh_status gh_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W, const float* A,
+                          float* C, uint32_t T, uint32_t N, uint32_t K) {
+  if (!ctx) return fail(GH_ERR_INVALID, "gh_prefill_gemm: ctx is null");
+  if (!W) return fail(GH_ERR_INVALID, "gh_prefill_gemm: W is null");
+  return gh::launch_prefill_gemm(ctx, mode, W, nullptr, A, C, T, N, K);
+}
+
+gh_status gh_prefill_gate_up_geglu(gh_context* ctx, gh_quant_mode mode, const void* Wg,
+                                   const void* Wu, const float* A, float* act, uint32_t T,
+                                   uint32_t N, uint32_t K) {
+  if (!ctx) return fail(GH_ERR_INVALID, "gh_prefill_gate_up_geglu: ctx is null");
+  if (!Wg || !Wu) return fail(GH_ERR_INVALID, "gh_prefill_gate_up_geglu: null weights");
+  return gh::launch_prefill_gemm(ctx, mode, Wg, Wu, A, act, T, N, K);
 }
 
 gh_status gh_argmax(gh_context* ctx, const float* logits, uint32_t* out_token, uint32_t vocab) {

@@ -62,6 +62,12 @@ struct gh_model {
   uint32_t* h_token = nullptr;
   void* graph_decode = nullptr;
   void* graph_prefill = nullptr;
+  // batched prefill buffers (gh_model_prefill), sized for pf_cap tokens
+  uint32_t pf_cap = 0, pf_stride = 0;
+  uint8_t* pf_arena = nullptr;
+  float *pf_x = nullptr, *pf_qkv = nullptr, *pf_o = nullptr, *pf_m = nullptr;
+  float *pf_xn = nullptr, *pf_attn = nullptr, *pf_act = nullptr;
+  uint32_t *pf_meta = nullptr, *pf_active = nullptr;
 
   template <typename T>
   T* at(size_t off) const {
@@ -73,11 +79,17 @@ struct gh_model {
   ~gh_model();
 };
 
+namespace {
+gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride);
+gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits);
+}  // namespace
+
 gh_model::~gh_model() {
   if (ctx && ctx->stream) hipStreamSynchronize(ctx->stream);
   if (graph_decode) gh_graph_destroy(graph_decode);
   if (graph_prefill) gh_graph_destroy(graph_prefill);
   if (arena) hipFree(arena);
+  if (pf_arena) hipFree(pf_arena);
   if (embed_dev) hipFree(embed_dev);
   if (h_x) hipHostFree(h_x);
   if (h_active) hipHostFree(h_active);
@@ -599,6 +611,67 @@ gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits
   return GH_OK;
 }
 
+gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64_t* clocks,
+                           const uint32_t* slot_idx, const uint32_t* active,
+                           uint32_t active_stride, const uint32_t* n_active, int want_logits,
+                           uint32_t* out_token) {
+  if (!m || !x || !clocks || !slot_idx || !active || !n_active || !out_token)
+    return fail(GH_ERR_INVALID, "gh_model_prefill: null argument");
+  *out_token = 0;
+  const gh_model_config& c = m->cfg;
+  if (T == 0) return fail(GH_ERR_INVALID, "gh_model_prefill: T is zero");
+  if (c.hidden_size > 8192)
+    return fail(GH_ERR_UNSUPPORTED, "gh_model_prefill: hidden size above 8192");
+  uint32_t max_n = 1;
+  for (uint32_t t = 0; t < T; t++) max_n = std::max(max_n, n_active[t]);
+  if (active_stride < max_n) return fail(GH_ERR_INVALID, "gh_model_prefill: active_stride < n_active");
+  // slot writers of this batch; a token may read its own and earlier tokens' slots only
+  std::vector<int64_t> writer(c.max_slots, -1);
+  for (uint32_t t = 0; t < T; t++) {
+    if (slot_idx[t] >= c.max_slots || clocks[t] > 0xFFFFFFFFull)
+      return fail(GH_ERR_INVALID, "gh_model_prefill: slot or clock out of range");
+    if (writer[slot_idx[t]] >= 0)
+      return fail(GH_ERR_UNSUPPORTED, "gh_model_prefill: the batch writes one ring slot twice");
+    writer[slot_idx[t]] = t;
+  }
+  for (uint32_t t = 0; t < T; t++) {
+    if (n_active[t] == 0 || n_active[t] > c.max_slots)
+      return fail(GH_ERR_INVALID, "gh_model_prefill: active list length out of range");
+    const uint32_t* row = active + (size_t)t * active_stride;
+    for (uint32_t i = 0; i < n_active[t]; i++) {
+      if (row[i] >= c.max_slots) return fail(GH_ERR_INVALID, "gh_model_prefill: active slot out of range");
+      if (writer[row[i]] > (int64_t)t)
+        return fail(GH_ERR_UNSUPPORTED,
+                    "gh_model_prefill: a token attends to a slot a later token of the batch writes");
+    }
+  }
+  gh_status st = ensure_prefill(m, T, active_stride);
+  if (st != GH_OK) return st;
+  hipStream_t s = m->ctx->stream;
+  std::vector<uint32_t> meta(3 * (size_t)T);
+  for (uint32_t t = 0; t < T; t++) {
+    meta[t] = (uint32_t)clocks[t];
+    meta[T + t] = slot_idx[t];
+    meta[2 * T + t] = n_active[t];
+  }
+  std::vector<uint32_t> act((size_t)T * m->pf_stride, 0u);
+  for (uint32_t t = 0; t < T; t++)
+    memcpy(&act[(size_t)t * m->pf_stride], active + (size_t)t * active_stride, (size_t)n_active[t] * 4);
+  hipError_t e = hipMemcpyAsync(m->pf_x, x, (size_t)T * c.hidden_size * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(m->pf_meta, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(m->pf_active, act.data(), act.size() * 4, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: input copies");
+  if ((st = prefill_forward(m, T, want_logits != 0)) != GH_OK) return st;
+  if (want_logits) {
+    e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: token copy");
+  }
+  e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "gh_model_prefill");
+  if (want_logits) *out_token = m->h_token[0];
+  return GH_OK;
+}
+
 gh_status gh_model_embed(gh_model* m, uint32_t token, float* x_host) {
   if (!m || !x_host) return fail(GH_ERR_INVALID, "gh_model_embed: null argument");
   if (!m->embed_dev) return fail(GH_ERR_UNSUPPORTED, "gh_model_embed: model has no device embedding");
@@ -620,6 +693,158 @@ gh_status gh_model_embed(gh_model* m, uint32_t token, float* x_host) {
 }  // extern "C"
 
 namespace {
+
+// Prefill buffers for up to T tokens with active lists of up to stride slots.
+gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
+  if (m->pf_arena && m->pf_cap >= T && m->pf_stride >= stride) return GH_OK;
+  const gh_model_config& c = m->cfg;
+  const uint32_t H = c.hidden_size, I = c.intermediate_size;
+  T = std::max(T, m->pf_cap);
+  stride = std::max(stride, m->pf_stride);
+  uint32_t max_qkv = 0;
+  for (auto& L : m->layers) max_qkv = std::max(max_qkv, L.qkv_rows);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += (bytes + 255) & ~(size_t)255;
+    return o;
+  };
+  const size_t o_x = take((size_t)T * H * 4), o_qkv = take((size_t)T * max_qkv * 4);
+  const size_t o_o = take((size_t)T * H * 4), o_m = take((size_t)T * H * 4);
+  const size_t o_xn = take((size_t)T * H * 4), o_attn = take((size_t)T * m->max_q * 4);
+  const size_t o_act = take((size_t)T * I * 4), o_meta = take((size_t)3 * T * 4);
+  const size_t o_active = take((size_t)T * stride * 4);
+  if (m->pf_arena) {
+    hipStreamSynchronize(m->ctx->stream);
+    hipFree(m->pf_arena);
+    m->pf_arena = nullptr;
+    m->pf_cap = m->pf_stride = 0;
+  }
+  hipError_t e = hipMalloc(&m->pf_arena, off);
+  if (e != hipSuccess) return fail(GH_ERR_ALLOC, std::string("prefill buffers: ") + hipGetErrorString(e));
+  auto f32 = [&](size_t o) { return reinterpret_cast<float*>(m->pf_arena + o); };
+  auto u32 = [&](size_t o) { return reinterpret_cast<uint32_t*>(m->pf_arena + o); };
+  m->pf_x = f32(o_x);
+  m->pf_qkv = f32(o_qkv);
+  m->pf_o = f32(o_o);
+  m->pf_m = f32(o_m);
+  m->pf_xn = f32(o_xn);
+  m->pf_attn = f32(o_attn);
+  m->pf_act = f32(o_act);
+  m->pf_meta = u32(o_meta);
+  m->pf_active = u32(o_active);
+  m->pf_cap = T;
+  m->pf_stride = stride;
+  return GH_OK;
+}
+
+// gh_pf_norm_k over T rows (mode 1: RMSNorm; mode 2: residual add + RMSNorm).
+gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* wr,
+                         const float* w, float s, uint32_t mode) {
+  uint32_t H = m->cfg.hidden_size;
+  float eps = m->cfg.rms_norm_eps;
+  float* X = m->pf_x;
+  float* Xn = m->pf_xn;
+  void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
+                  &Xn, &H, &s, &eps, &mode};
+  return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(256), 0, args);
+}
+
+gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
+  gh_context* ctx = m->ctx;
+  const gh_model_config& c = m->cfg;
+  const uint32_t H = c.hidden_size, I = c.intermediate_size;
+  gh_status st;
+  uint32_t* clocks = m->pf_meta;
+  uint32_t* slots = m->pf_meta + T;
+  uint32_t* nact = m->pf_meta + 2 * T;
+  for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
+    const Layer& L = m->layers[l];
+    // 1. xn = norm(x) (layer 0: RMSNorm; later: post-FFN add + layer scalar + norm)
+    if (l == 0) {
+      st = launch_pf_norm(m, T, nullptr, nullptr, m->at<float>(L.input_norm), 1.0f, 1);
+    } else {
+      const Layer& P = m->layers[l - 1];
+      st = launch_pf_norm(m, T, m->pf_m, P.post_ffn == kNone ? nullptr : m->at<float>(P.post_ffn),
+                          m->at<float>(L.input_norm), P.scalar, 2);
+    }
+    if (st != GH_OK) return st;
+    // 2. [q|k|v] rows of every token
+    if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.qkv), nullptr, m->pf_xn,
+                                      m->pf_qkv, T, L.qkv_rows, H)) != GH_OK)
+      return st;
+    // 3. q/k norm + RoPE in place, K/V into the caches, then attention
+    AttnArgs a{};
+    a.q = m->pf_qkv;
+    a.q_norm = m->at<float>(L.q_norm);
+    a.k_norm = m->at<float>(L.k_norm);
+    a.k_cache = m->at<float>(L.k_cache);
+    a.v_cache = m->at<float>(L.v_cache);
+    a.active = m->pf_active;
+    a.n_active = nact;
+    a.out_rows = m->pf_attn;
+    a.nq = c.num_attention_heads;
+    a.nkv = L.nkv;
+    a.D = L.head_dim;
+    a.rot = L.rot;
+    a.k_eq_v = L.k_eq_v ? 1 : 0;
+    a.nsplit = 1;
+    a.theta = L.theta;
+    a.eps = c.rms_norm_eps;
+    a.scale = 1.0f;  // inv_sqrt_dim = 1.0 (src/model/forward.zig:80)
+    a.q_stride = L.qkv_rows;
+    a.active_stride = m->pf_stride;
+    a.out_stride = L.q_dim;
+    {
+      void* args[] = {&a, &clocks, &slots};
+      if ((st = ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args)) != GH_OK)
+        return st;
+    }
+    {
+      const uint32_t D = L.head_dim;
+      const char* name = D <= 64 ? "gh_pf_attn_d1_k"
+                         : D <= 128 ? "gh_pf_attn_d2_k"
+                         : D <= 256 ? "gh_pf_attn_d4_k" : "gh_pf_attn_d8_k";
+      void* args[] = {&a};
+      if ((st = ctx->launch(name, dim3(a.nkv, T), dim3(256), 0, args)) != GH_OK) return st;
+    }
+    // 4. o = W_o . attn
+    if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.o), nullptr, m->pf_attn,
+                                      m->pf_o, T, H, L.q_dim)) != GH_OK)
+      return st;
+    // 5. x += post_attn_norm(o); act = geglu(W_gate, W_up . pre_ffn_norm(x))
+    if ((st = launch_pf_norm(m, T, m->pf_o,
+                             L.post_attn == kNone ? nullptr : m->at<float>(L.post_attn),
+                             m->at<float>(L.pre_ffn), 1.0f, 2)) != GH_OK)
+      return st;
+    if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.gate), m->at<uint8_t>(L.up),
+                                      m->pf_xn, m->pf_act, T, I, H)) != GH_OK)
+      return st;
+    // 6. m = W_down . act
+    if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.down), nullptr, m->pf_act,
+                                      m->pf_m, T, H, I)) != GH_OK)
+      return st;
+  }
+  if (want_logits) {
+    // last token: x = (x + post_ffn_norm(m)) * layer_scalar; argmax(head . final_norm(x))
+    const Layer& P = m->layers.back();
+    XPro p{};
+    p.x = m->pf_x + (size_t)(T - 1) * H;
+    p.r = m->pf_m + (size_t)(T - 1) * H;
+    p.wr = P.post_ffn == kNone ? nullptr : m->at<float>(P.post_ffn);
+    p.w = m->at<float>(m->final_norm);
+    p.xout = m->at<float>(m->x1);
+    p.s = P.scalar;
+    p.eps = c.rms_norm_eps;
+    p.mode = 2;
+    m->hidden_final = m->x1;
+    uint32_t* amax = m->at<uint32_t>(m->amax);
+    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), amax + 64, amax,
+                  m->at<uint32_t>(m->token)};
+    if ((st = gh::launch_stream(ctx, "gh_argmax_q8", &aa, p, c.vocab_size, H)) != GH_OK) return st;
+  }
+  return GH_OK;
+}
 
 // (device pointer, bytes) of a tensor; nullptr when absent.
 std::pair<uint8_t*, size_t> tensor_ref(const gh_model* m, int layer, gh_tensor t) {

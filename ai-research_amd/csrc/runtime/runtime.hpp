@@ -73,6 +73,10 @@ struct StreamShape {
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out);
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
+// Prefill MFMA GEMM (prefill.hip): C [T][N] = A [T][K] . deq(W0)^T, or with
+// W1, C = gelu_tanh(A . deq(W0)^T) * (A . deq(W1)^T); A and C f32.
+gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
+                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);
 }  // namespace gh

@@ -67,6 +67,8 @@ _SIGS = {
                          _u32, _f32, _f32]),
     "gh_decode_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _u32]),
     "gh_argmax": (_i, [_vp, _vp, _vp, _u32]),
+    "gh_prefill_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _u32, _u32, _u32]),
+    "gh_prefill_gate_up_geglu": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
 }
 
 class XPrologue(C.Structure):
@@ -114,6 +116,7 @@ _SIGS.update({
     "gh_model_init_synthetic": (_i, [_vp, C.POINTER(ModelConfig), _i, _u64, C.POINTER(_vp)]),
     "gh_model_deinit": (None, [_vp]),
     "gh_dispatch_forward_token": (_i, [_vp, _vp, _i, _u64, _u32, _vp, _u32, C.POINTER(_u32)]),
+    "gh_model_prefill": (_i, [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _i, C.POINTER(_u32)]),
     "gh_model_embed": (_i, [_vp, _u32, _vp]),
     "gh_model_tensor_bytes": (_sz, [_vp, _i, _i]),
     "gh_model_read_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
@@ -358,6 +361,15 @@ class Context:
     def argmax(self, logits, out_token, vocab):
         _check(lib().gh_argmax(self.h, _addr(logits), _addr(out_token), vocab), "gh_argmax")
 
+    def prefill_gemm(self, mode, W, A, C, T, N, K):
+        """C [T][N] = A [T][K] . deq(W)^T on the matrix cores (A, C f32)."""
+        _check(lib().gh_prefill_gemm(self.h, mode, _addr(W), _addr(A), _addr(C), T, N, K),
+               "gh_prefill_gemm")
+
+    def prefill_gate_up_geglu(self, mode, Wg, Wu, A, act, T, N, K):
+        _check(lib().gh_prefill_gate_up_geglu(self.h, mode, _addr(Wg), _addr(Wu), _addr(A),
+                                              _addr(act), T, N, K), "gh_prefill_gate_up_geglu")
+
 
 def _addr(b):
     if isinstance(b, Buffer):
@@ -458,6 +470,23 @@ class Model:
         _check(lib().gh_dispatch_forward_token(self.h, _ptr(x), int(want_logits), clock, slot_idx,
                                                _ptr(act), act.size, C.byref(tok)),
                "gh_dispatch_forward_token")
+        return tok.value
+
+    def prefill(self, x, clocks, slots, actives, want_logits=True):
+        """T tokens in one call; actives[t] is token t's active slot list."""
+        x = np.ascontiguousarray(x, np.float32)
+        T = x.shape[0]
+        clocks = np.ascontiguousarray(clocks, np.uint64)
+        slots = np.ascontiguousarray(slots, np.uint32)
+        n_act = np.array([len(a) for a in actives], np.uint32)
+        stride = int(n_act.max())
+        act = np.zeros((T, stride), np.uint32)
+        for t, a in enumerate(actives):
+            act[t, :len(a)] = a
+        tok = _u32()
+        _check(lib().gh_model_prefill(self.h, _ptr(x), T, _ptr(clocks), _ptr(slots), _ptr(act),
+                                      stride, _ptr(n_act), int(want_logits), C.byref(tok)),
+               "gh_model_prefill")
         return tok.value
 
     def embed(self, token):

@@ -196,6 +196,22 @@ gh_status gh_decode_attn(gh_context *ctx, const float *Q, const float *K_cache,
  * of the largest value.  out_token is a device u32. */
 gh_status gh_argmax(gh_context *ctx, const float *logits, uint32_t *out_token, uint32_t vocab);
 
+/* ---- batched prefill GEMMs (no reference counterpart: the reference
+ * prefills token by token through its decode graph, src/interactive.zig:33-37,
+ * src/gpu/model_dispatch.zig:144).  One projection of T prompt tokens on the
+ * matrix cores: C[T][N] = A[T][K] . deq(W)[N][K]^T with A f32 row-major
+ * (16-byte aligned) and W in the quant.zig row layout of mode (Q4 or Q8);
+ * the weights enter exactly (integer values, f32 block scales applied to the
+ * block sums), the activations as two fp16 halves, fp32 accumulation;
+ * K % 32 == 0.  All pointers are device pointers. */
+gh_status gh_prefill_gemm(gh_context *ctx, gh_quant_mode mode, const void *W, const float *A,
+                          float *C, uint32_t T, uint32_t N, uint32_t K);
+/* act[T][N] = gelu_tanh(A . deq(Wg)^T) * (A . deq(Wu)^T): the batched form of
+ * shaders/fused_mlp_q4.wgsl. */
+gh_status gh_prefill_gate_up_geglu(gh_context *ctx, gh_quant_mode mode, const void *Wg,
+                                   const void *Wu, const float *A, float *act, uint32_t T,
+                                   uint32_t N, uint32_t K);
+
 /* ---- ring bookkeeping: DynamicRingBuffer (src/ring_buffer.zig:7-147) -------
  * The host side of the [anchors | window | recall] ring: which slot a clock
  * maps to and which slots a token attends over.  The K/V values live in the
@@ -278,6 +294,22 @@ void gh_model_deinit(gh_model *m);
 gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits, uint64_t clock,
                                     uint32_t slot_idx, const uint32_t *active_slots,
                                     uint32_t n_active, uint32_t *out_token);
+/* T prompt tokens in one call: the result of calling gh_dispatch_forward_token
+ * for each token in order (want_logits only on the last), computed layer by
+ * layer over the whole batch with the prefill GEMMs (no reference
+ * counterpart; the reference has no batched prefill).  x is [T][hidden]
+ * (host); token t has position clocks[t], ring slot slot_idx[t] and active
+ * list active[t * active_stride ..] of n_active[t] entries (host, as
+ * ring.activateSlot / getActiveSlots give them).  Every layer writes each
+ * token's K/V at its slot.  The batch must not write one slot twice, and no
+ * token's active list may contain a slot that a later token of the batch
+ * writes (GH_ERR_UNSUPPORTED: split the batch or use the per-token call).
+ * The first call allocates the model's prefill buffers for T tokens (not
+ * inside graph capture). */
+gh_status gh_model_prefill(gh_model *m, const float *x, uint32_t T, const uint64_t *clocks,
+                           const uint32_t *slot_idx, const uint32_t *active,
+                           uint32_t active_stride, const uint32_t *n_active, int want_logits,
+                           uint32_t *out_token);
 /* x = bf16(E[token]) * sqrt(hidden) (src/model/forward.zig:33-37) for a
  * synthetic model, whose bf16 embedding lives on the device. */
 gh_status gh_model_embed(gh_model *m, uint32_t token, float *x_host);

@@ -1,0 +1,153 @@
+"""GPU parity of the batched prefill: the MFMA Q4_0/Q8_0 dequant GEMMs against
+an fp64 product of the same dequantized weights, and gh_model_prefill against
+the oracle's sequential per-token forward (the reference prefills token by
+token, src/interactive.zig:33-37, so that is the semantics to match)."""
+import os
+
+import numpy as np
+import pytest
+
+import gemma_hip as gh
+import numpy_ref as nr
+import oracle as orc
+from model_ref import oracle_model
+from tol import assert_close
+
+pytestmark = pytest.mark.gpu
+NT = min(16, os.cpu_count() or 1)
+
+
+def quantized(rows, cols, mode, seed):
+    w = nr.bf16_rne(gh.synth_normal(rows * cols, 0, seed, 0.0, 0.02).reshape(rows, cols))
+    wq = nr.quantize_q4(w) if mode == gh.QUANT_Q4 else nr.quantize_q8(w)
+    deq = nr.dequant_q4(wq, cols) if mode == gh.QUANT_Q4 else nr.dequant_q8(wq, cols)
+    return wq, deq
+
+
+# (T, N, K): single row, ragged T and N, the 12B K, T past one 128-row tile
+GEMM_SHAPES = [(1, 64, 128), (7, 96, 256), (64, 384, 3840), (130, 256, 512), (300, 128, 1024)]
+
+
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("T,N,K", GEMM_SHAPES)
+def test_prefill_gemm(gpu, mode, T, N, K):
+    wq, deq = quantized(N, K, mode, 300 + T)
+    a = gh.synth_normal(T * K, 1, 301, 0.0, 1.0).reshape(T, K)
+    W, A, C = gpu.upload(wq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gemm(mode, W, A, C, T, N, K)
+    got = C.read(np.float32, T * N).reshape(T, N)
+    assert_close(got, np.asarray(a, np.float64) @ deq.T, what="prefill GEMM")
+
+
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("T,N,K", [(1, 64, 128), (45, 192, 512), (256, 512, 3840)])
+def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
+    gq, gdeq = quantized(N, K, mode, 310)
+    uq, udeq = quantized(N, K, mode, 311)
+    a = gh.synth_normal(T * K, 1, 312, 0.0, 1.0).reshape(T, K)
+    Wg, Wu, A, act = gpu.upload(gq), gpu.upload(uq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gate_up_geglu(mode, Wg, Wu, A, act, T, N, K)
+    got = act.read(np.float32, T * N).reshape(T, N)
+    a64 = np.asarray(a, np.float64)
+    ref = nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T)
+    assert_close(got, ref, what="prefill GeGLU")
+
+
+def test_prefill_gemm_rejects_bad_shapes(gpu):
+    W, A, C = gpu.alloc(4096), gpu.alloc(4096), gpu.alloc(4096)
+    with pytest.raises(gh.GhError):
+        gpu.prefill_gemm(gh.QUANT_Q4, W, A, C, 4, 8, 100)  # K % 32
+    with pytest.raises(gh.GhError):
+        gpu.prefill_gemm(gh.QUANT_NONE, W, A, C, 4, 8, 128)
+
+
+def tiny_cfg(**kw):
+    args = dict(vocab=1024, hidden=256, intermediate=512, layers=3, heads=4, kv_heads=2,
+                head_dim=64, max_slots=24, global_kv_heads=2, global_head_dim=128,
+                full_layers=(2,))
+    args.update(kw)
+    return gh.model_config(**args)
+
+
+def ring_lists(ring, clocks):
+    slots, actives = [], []
+    for c in clocks:
+        slots.append(ring.activate_slot(0, c))
+        actives.append(np.array(ring.active_slots(0, c), np.uint32))
+    return slots, actives
+
+
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+def test_model_prefill_matches_sequential_oracle(gpu, mode):
+    # 12 prompt tokens (4 anchors, then the window), one batch, then two decode
+    # steps through the per-token graph on the caches the prefill wrote
+    cfg = tiny_cfg()
+    m = gh.Model(gpu, cfg, mode=mode, seed=11)
+    try:
+        om, layers = oracle_model(m, cfg, mode)
+        ring = gh.Ring(cfg.num_hidden_layers, 4, 16, 4)
+        tokens = np.random.default_rng(5).integers(0, cfg.vocab_size, 14)
+        xs = np.stack([m.embed(int(t)) for t in tokens])
+        T = 12
+        slots, actives = ring_lists(ring, range(T))
+        tok = m.prefill(xs[:T], np.arange(T), slots, actives, True)
+        for c in range(T):
+            rtok, _, rlog = om.forward(xs[c], c, slots[c], actives[c], c == T - 1, NT)
+        logits = m.read(-1, gh.T_LOGITS, np.float32)
+        assert_close(logits, rlog, what="prefill last-token logits")
+        assert tok == orc.argmax(logits)
+        for l, d in enumerate(layers):
+            kvd = d["num_kv_heads"] * d["head_dim"]
+            kc = m.read(l, gh.T_K_CACHE, np.float32).reshape(cfg.max_slots, kvd)
+            vc = m.read(l, gh.T_V_CACHE, np.float32).reshape(cfg.max_slots, kvd)
+            assert_close(kc[slots], d["k_cache"][slots], what="prefill K cache layer %d" % l)
+            assert_close(vc[slots], d["v_cache"][slots], what="prefill V cache layer %d" % l)
+        for c in range(T, 14):
+            slot = ring.activate_slot(0, c)
+            act = ring.active_slots(0, c)
+            tok = m.forward(xs[c], c, slot, act, True)
+            rtok, _, rlog = om.forward(xs[c], c, slot, act, True, NT)
+            assert_close(m.read(-1, gh.T_LOGITS, np.float32), rlog, what="decode after prefill")
+    finally:
+        m.close()
+
+
+def test_model_prefill_equals_per_token_path(gpu):
+    # the batched prefill and T per-token calls leave the same caches (to
+    # tolerance) and pick the same final token on a 12B-width layer pair
+    cfg = gh.model_config(vocab=4096, hidden=3840, intermediate=15360, layers=2, heads=16,
+                          kv_heads=8, head_dim=256, max_slots=64, full_layers=(1,))
+    a = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=3)
+    b = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=3)
+    try:
+        ring_a, ring_b = gh.Ring(2, 8, 48, 8), gh.Ring(2, 8, 48, 8)
+        tokens = np.random.default_rng(9).integers(0, cfg.vocab_size, 40)
+        xs = np.stack([a.embed(int(t)) for t in tokens])
+        slots, actives = ring_lists(ring_a, range(40))
+        a.prefill(xs, np.arange(40), slots, actives, True)
+        for c in range(40):
+            slot = ring_b.activate_slot(0, c)
+            b.forward(xs[c], c, slot, ring_b.active_slots(0, c), c == 39)
+        assert_close(a.read(-1, gh.T_LOGITS, np.float32), b.read(-1, gh.T_LOGITS, np.float32),
+                     what="prefill vs per-token logits")
+        for l in range(2):
+            for t in (gh.T_K_CACHE, gh.T_V_CACHE):
+                ka = a.read(l, t, np.float32).reshape(64, -1)[slots]
+                kb = b.read(l, t, np.float32).reshape(64, -1)[slots]
+                assert_close(ka, kb, what="prefill vs per-token cache %d/%d" % (l, t))
+    finally:
+        a.close()
+        b.close()
+
+
+def test_model_prefill_rejects_slot_reuse(gpu):
+    cfg = tiny_cfg(layers=1, full_layers=())
+    m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=2)
+    try:
+        xs = np.stack([m.embed(i) for i in range(3)])
+        with pytest.raises(gh.GhError):  # one slot written twice
+            m.prefill(xs, [0, 1, 2], [5, 6, 5], [[5], [5, 6], [5, 6]], True)
+        with pytest.raises(gh.GhError):  # token 0 reads the slot token 1 writes
+            m.prefill(xs[:2], [0, 1], [5, 6], [[5, 6], [5, 6]], True)
+    finally:
+        m.close()

@@ -56,7 +56,7 @@ __device__ __forceinline__ u32x4 ldw(const void* p) {
 template <int NT>
 __device__ __forceinline__ void stage_x(const float* __restrict__ X, uint32_t K,
                                         float* xs, float* bsum) {
-  constexpr uint32_t U = 8;
+  constexpr uint32_t U = NT >= 1024 ? 4 : 8;  // one round up to K = 16384 (NT 1024) / 8192
   const uint32_t n4 = K >> 2;
   const float4* X4 = reinterpret_cast<const float4*>(X);
   for (uint32_t base = 0; base < n4; base += NT * U) {
@@ -719,11 +719,13 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 // pointers are separate kernel parameters: loaded out of a by-value struct
 // parameter they lose the kernel-argument address-space and alignment facts,
 // and the stream then needs ~100 more VGPRs (220 vs 126 for the Q4 d3 form).
-#define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED)                       \
-  extern "C" __global__ __launch_bounds__(256) void NAME##_t##T##_g##G##_d##D(          \
+#define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)      \
+  extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX(   \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                             \
-    stream_rows<FMT, T, G, D, 256, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);       \
+    stream_rows<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);        \
   }
+#define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED) \
+  GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, 256, )
 #define GH_UNPAREN(...) __VA_ARGS__
 
 #define GH_P_W (const uint8_t* W, float* Y)
@@ -749,6 +751,12 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 
 #define GH_SHAPES(X, D) X(16, 1, D) X(32, 1, D) X(64, 1, D) X(32, 2, D) X(64, 2, D) X(32, 4, D) X(64, 4, D)
 
+// Wide workgroups (1024 threads) for long rows: one x staging (up to 64 KB
+// of LDS for K = 15360) serves 16 wavefronts instead of 4.
+#define GH_WIDE(T, G, D)                                                                   \
+  GH_STREAM_KERNEL_NT(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)         \
+  GH_STREAM_KERNEL_NT(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)
+
 #if defined(GH_GEMV_NORMED)
 GH_SHAPES(GH_NORMED, 1)
 GH_SHAPES(GH_NORMED, 2)
@@ -757,4 +765,5 @@ GH_SHAPES(GH_NORMED, 3)
 GH_SHAPES(GH_PLAIN, 1)
 GH_SHAPES(GH_PLAIN, 2)
 GH_SHAPES(GH_PLAIN, 3)
+GH_WIDE(32, 4, 1) GH_WIDE(64, 2, 1) GH_WIDE(64, 4, 1)  // depth 2 at 1024 threads spills
 #endif

@@ -17,7 +17,7 @@ constexpr uint32_t kArgmaxMaxBlocks = 4096;
 constexpr size_t kArgmaxScratchBytes = (64 + 2 * kArgmaxMaxBlocks) * 4;
 
 struct GemvCfg {
-  int tpr, gpl, wgs_per_cu, depth;
+  int tpr, gpl, wgs_per_cu, depth, nt;
 };
 
 unsigned x_lds_bytes(uint32_t K);
@@ -25,7 +25,7 @@ unsigned x_lds_bytes(uint32_t K);
 // Lanes per row team (TPR) and 4-block groups per lane per row (GPL) with
 // TPR * GPL >= the row's group count and the least idle lanes; then a
 // persistent grid of wgs_per_cu workgroups per CU (bounded by LDS).
-GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8) {
+GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool wide_ok) {
   const uint32_t ng = K / 128;
   static const int kT[] = {16, 32, 64};
   int best_t = 64, best_g = 4;
@@ -45,13 +45,17 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8) {
   }
   // Measured on MI355X (graph replay, 12B decode shapes): one item in flight
   // per lane and 3 (Q4) or 2 (Q8) workgroups per CU read fastest.
-  GemvCfg c{best_t, best_g, q8 ? 2 : 3, 1};
-  if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning override "tpr,gpl,wgs_per_cu,depth"
-    int t = 0, g = 0, w = 0, d = 0;
-    if (sscanf(env, "%d,%d,%d,%d", &t, &g, &w, &d) == 4 && (t == 16 || t == 32 || t == 64) &&
-        (g == 1 || g == 2 || g == 4) && !(t == 16 && g > 1) && w >= 1 && w <= 32 &&
-        (uint32_t)(t * g) >= ng && d >= 1 && d <= 3) {
-      c = {t, g, w, d};
+  GemvCfg c{best_t, best_g, q8 ? 2 : 3, 1, 256};
+  // Long rows (the down projection, K = 15360): 1024-thread workgroups, so
+  // one LDS staging of x serves 16 wavefronts; measured 11.6 vs 13.6 us.
+  if (wide_ok && K >= 8192 && best_t * best_g >= 128) c = {best_t, best_g, 2, 1, 1024};
+  if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning "tpr,gpl,wgs_per_cu,depth[,nt]"
+    int t = 0, g = 0, w = 0, d = 0, n = 256;
+    const int got = sscanf(env, "%d,%d,%d,%d,%d", &t, &g, &w, &d, &n);
+    if (got >= 4 && (t == 16 || t == 32 || t == 64) && (g == 1 || g == 2 || g == 4) &&
+        !(t == 16 && g > 1) && w >= 1 && w <= 32 && (uint32_t)(t * g) >= ng && d >= 1 &&
+        d <= 3 && (n == 256 || (n == 1024 && wide_ok && t * g >= 128 && d == 1))) {
+      c = {t, g, w, d, n};
     }
   }
   const unsigned lds_cap = (unsigned)(ctx->max_lds / std::max(1u, x_lds_bytes(K)));
@@ -83,18 +87,20 @@ namespace gh {
 
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out) {
-  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr);
+  const bool plain_gemv = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0);
+  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, plain_gemv);
   out->lds = x_lds_bytes(K) + 64;
   if (out->lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
   out->name = std::string(family) + (normed ? "n" : "") + "_t" + std::to_string(c.tpr) + "_g" +
-              std::to_string(c.gpl) + "_d" + std::to_string(c.depth);
+              std::to_string(c.gpl) + "_d" + std::to_string(c.depth) + (c.nt == 1024 ? "_w" : "");
+  out->nt = (unsigned)c.nt;
   // A persistent grid larger than what the CUs hold at once would run its
   // last workgroups as a second, mostly idle wave.
-  const int occ = ctx->occupancy(out->name, 256, out->lds);
+  const int occ = ctx->occupancy(out->name, c.nt, out->lds);
   if (occ <= 0) return fail(GH_ERR_CODE_OBJECT, "kernel not found in the code objects: " + out->name);
   // The same number of workgroups on every CU (a multiple of the CU count)
   // measured faster than fewer workgroups with an equal row count per team.
-  const uint32_t teams_per_wg = 256 / c.tpr;
+  const uint32_t teams_per_wg = c.nt / c.tpr;
   const uint32_t cap = (uint32_t)ctx->num_cus * (uint32_t)std::min(c.wgs_per_cu, occ);
   out->grid = std::min<uint32_t>(cap, (M + teams_per_wg - 1) / teams_per_wg);
   if (const char* env = getenv("GH_GEMV_GRID")) {  // tuning: "bal" = balanced rows per team
@@ -117,7 +123,7 @@ gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> 
   XPro xpc = xp;
   std::vector<void*> args = std::move(fmt_params);
   args.insert(args.end(), {&xpc, &M, &K});
-  return ctx->launch(sh.name, dim3(sh.grid), dim3(256), sh.lds, args.data());
+  return ctx->launch(sh.name, dim3(sh.grid), dim3(sh.nt), sh.lds, args.data());
 }
 
 gh_status check_pro(const gh_context* ctx, const XPro& p, uint32_t K, const char* who) {

@@ -68,7 +68,7 @@ inline gh_status launch_stream(gh_context* ctx, const char* family, ArgmaxArgs* 
 // Kernel name and persistent grid of one row-stream launch.
 struct StreamShape {
   std::string name;
-  unsigned grid = 0, lds = 0;
+  unsigned grid = 0, lds = 0, nt = 256;
 };
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out);

@@ -45,6 +45,30 @@ __device__ __forceinline__ u32x4 ldw(const void* p) {
   return *(gvec_ptr)(p);
 }
 
+// Cross-lane sums with DPP row operations (a few cycles each) instead of
+// __shfl_xor, which lowers to an LDS-crossbar ds_bpermute per step.  Every
+// step adds a commutative pair, so all participating lanes end with the
+// same bit-identical value.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// sum over the 8 lanes of each half-row (lanes 8k .. 8k+7)
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  return v;
+}
+// sum over the 64 lanes of the wavefront
+__device__ __forceinline__ float sum64(float v) {
+  v = sum8(v);
+  v += dpp<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Stage x[K] into LDS (padded by group) and write the per-block sums.
 // K % 128 == 0.  All NT threads of the block must call it.  The loads of a
 // chunk of U float4 per thread are all issued before any is consumed, so
@@ -73,11 +97,9 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ X, uint32_t K,
       const uint32_t g = e >> 7, o = e & 127;  // group, offset in group
       float s = (v[u].x + v[u].y) + (v[u].z + v[u].w);
       if (i < n4) *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v[u];
-      // a block is 8 consecutive float4s = 8 consecutive lanes (n4 % 8 == 0,
-      // so a lane group of 8 is either fully in range or fully out)
-      s += __shfl_xor(s, 1, 8);
-      s += __shfl_xor(s, 2, 8);
-      s += __shfl_xor(s, 4, 8);
+      // a block is 8 consecutive float4s = the 8 lanes of a half-row (n4 % 8
+      // == 0, so a half-row is either fully in range or fully out)
+      s = sum8(s);
       if (i < n4 && (i & 7) == 0) bsum[i >> 3] = s;
     }
   }
@@ -162,10 +184,14 @@ __device__ __forceinline__ float q4_group_dot(const Q4G& g, const float* __restr
   return r;
 }
 
+// Sum over a row team of TPR (16, 32 or 64) consecutive lanes.
 template <int TPR>
 __device__ __forceinline__ float team_sum(float v) {
-#pragma unroll
-  for (int off = TPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, TPR);
+  static_assert(TPR == 16 || TPR == 32 || TPR == 64, "team of 16, 32 or 64 lanes");
+  v = sum8(v);
+  v += dpp<0x140>(v);  // row_mirror: the two half-rows of a row of 16
+  if (TPR >= 32) v += __shfl_xor(v, 16, 64);
+  if (TPR == 64) v += __shfl_xor(v, 32, 64);
   return v;
 }
 
@@ -187,26 +213,40 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 //           the GEMV consumes RMSNorm(xn) * w                  (add + norm)
 // Every norm is in * (mean(in^2) + eps)^-1/2 * w, as src/kernels.zig:46-52.
 // ------------------------------------------------------------------------
-template <int NT>
-__device__ __forceinline__ float block_sum(float v, float* red) {
+// Block-wide sums of NV values per thread; every thread gets the totals.
+// red holds (NT / 64) * NV floats and must not be reused before a barrier.
+template <int NT, int NV>
+__device__ __forceinline__ void block_sums(float (&v)[NV], float* red) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float t = 0.f;
+  for (int j = 0; j < NV; j++) v[j] = sum64(v[j]);
+  if ((threadIdx.x & 63) == 0) {
 #pragma unroll
-  for (int w = 0; w < NT / 64; w++) t += red[w];
+    for (int j = 0; j < NV; j++) red[(threadIdx.x >> 6) * NV + j] = v[j];
+  }
   __syncthreads();
-  return t;
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) t += red[w * NV + j];
+    v[j] = t;
+  }
 }
 
-// Extra LDS (floats) the prologue needs beyond the padded x and block sums.
-__host__ __device__ constexpr uint32_t pro_extra_floats(uint32_t) { return 16; }
+// Extra LDS (floats) the prologue and epilogues need beyond the padded x and
+// block sums (the host adds 4 * this many bytes).
+__host__ __device__ constexpr uint32_t pro_extra_floats() { return 64; }
 
 // Largest K of a normed prologue: each thread holds its float4 slices of x,
 // r and the two norm weights in registers (PRO_U per vector).
 #define PRO_U 4
 
+// The normed prologue takes one block-wide reduction, not two: for mode 2,
+// with q = r * wr and c = (mean(r^2) + eps)^-1/2 (q = r, c = 1 without wr),
+//   sum(xn^2) = s^2 (sum x^2 + 2 c sum x q + c^2 sum q^2)
+// so the four sums go through one reduction.  Only if that expansion
+// cancels (the total below 1e-3 of its positive terms) is sum(xn^2)
+// reduced directly from xn, as a second pass.
 template <int NT, bool NORMED>
 __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs, float* bsum,
                                             float* ext) {
@@ -214,9 +254,9 @@ __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs
     stage_x<NT>(p.x, K, xs, bsum);
     return;
   }
-  float* red = ext;  // [16]
   const uint32_t n4 = K >> 2;
   const bool add = p.mode == 2;
+  const bool has_wr = p.wr != nullptr;
   // one round trip: every load of the prologue is issued before any is used
   float4 vx[PRO_U], vr[PRO_U], vwr[PRO_U], vw[PRO_U];
 #pragma unroll
@@ -227,27 +267,43 @@ __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs
       vw[u] = reinterpret_cast<const float4*>(p.w)[i];
       if (add) {
         vr[u] = reinterpret_cast<const float4*>(p.r)[i];
-        if (p.wr) vwr[u] = reinterpret_cast<const float4*>(p.wr)[i];
+        if (has_wr) vwr[u] = reinterpret_cast<const float4*>(p.wr)[i];
       }
     }
   }
+  float inv;
   if (add) {
-    float ssr = 0.f;
+    float t[4] = {0.f, 0.f, 0.f, 0.f};  // sum r^2, x^2, x q, q^2
 #pragma unroll
-    for (uint32_t u = 0; u < PRO_U; u++)
-      if (u * NT + threadIdx.x < n4)
-        ssr += vr[u].x * vr[u].x + vr[u].y * vr[u].y + vr[u].z * vr[u].z + vr[u].w * vr[u].w;
-    const float inv_r = 1.0f / sqrtf(block_sum<NT>(ssr, red) / (float)K + p.eps);
+    for (uint32_t u = 0; u < PRO_U; u++) {
+      if (u * NT + threadIdx.x < n4) {
+        const float r[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+        const float x[4] = {vx[u].x, vx[u].y, vx[u].z, vx[u].w};
+        const float w[4] = {vwr[u].x, vwr[u].y, vwr[u].z, vwr[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float q = has_wr ? r[e] * w[e] : r[e];
+          t[0] += r[e] * r[e];
+          t[1] += x[e] * x[e];
+          t[2] += x[e] * q;
+          t[3] += q * q;
+        }
+      }
+    }
+    block_sums<NT, 4>(t, ext);
+    const float c = has_wr ? 1.0f / sqrtf(t[0] / (float)K + p.eps) : 1.0f;
+    const float pos = t[1] + c * c * t[3];
+    float s2 = p.s * p.s * (pos + 2.0f * c * t[2]);
 #pragma unroll
     for (uint32_t u = 0; u < PRO_U; u++) {
       const uint32_t i = u * NT + threadIdx.x;
       if (i < n4) {
         float4 rv = vr[u];
-        if (p.wr) {
-          rv.x = rv.x * inv_r * vwr[u].x;
-          rv.y = rv.y * inv_r * vwr[u].y;
-          rv.z = rv.z * inv_r * vwr[u].z;
-          rv.w = rv.w * inv_r * vwr[u].w;
+        if (has_wr) {
+          rv.x = rv.x * c * vwr[u].x;
+          rv.y = rv.y * c * vwr[u].y;
+          rv.z = rv.z * c * vwr[u].z;
+          rv.w = rv.w * c * vwr[u].w;
         }
         vx[u].x = (vx[u].x + rv.x) * p.s;
         vx[u].y = (vx[u].y + rv.y) * p.s;
@@ -256,13 +312,25 @@ __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs
         if (blockIdx.x == 0) reinterpret_cast<float4*>(p.xout)[i] = vx[u];
       }
     }
-  }
-  float ssx = 0.f;
+    if (!(s2 > 1e-3f * p.s * p.s * pos)) {  // cancellation (uniform branch): reduce xn^2 itself
+      float d[1] = {0.f};
 #pragma unroll
-  for (uint32_t u = 0; u < PRO_U; u++)
-    if (u * NT + threadIdx.x < n4)
-      ssx += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
-  const float inv = 1.0f / sqrtf(block_sum<NT>(ssx, red) / (float)K + p.eps);
+      for (uint32_t u = 0; u < PRO_U; u++)
+        if (u * NT + threadIdx.x < n4)
+          d[0] += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
+      block_sums<NT, 1>(d, ext + 4 * (NT / 64));
+      s2 = d[0];
+    }
+    inv = 1.0f / sqrtf(s2 / (float)K + p.eps);
+  } else {
+    float d[1] = {0.f};
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++)
+      if (u * NT + threadIdx.x < n4)
+        d[0] += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
+    block_sums<NT, 1>(d, ext);
+    inv = 1.0f / sqrtf(d[0] / (float)K + p.eps);
+  }
 #pragma unroll
   for (uint32_t u = 0; u < PRO_U; u++) {
     const uint32_t i = u * NT + threadIdx.x;
@@ -277,10 +345,8 @@ __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs
       *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v;
       s = (v.x + v.y) + (v.z + v.w);
     }
-    // block sums: 8 consecutive lanes hold one block (NT and n4 are multiples of 8)
-    s += __shfl_xor(s, 1, 8);
-    s += __shfl_xor(s, 2, 8);
-    s += __shfl_xor(s, 4, 8);
+    // block sums: the 8 lanes of a half-row hold one block (NT and n4 are multiples of 8)
+    s = sum8(s);
     if (i < n4 && (i & 7) == 0) bsum[i >> 3] = s;
   }
   __syncthreads();
@@ -752,7 +818,8 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 #define GH_SHAPES(X, D) X(16, 1, D) X(32, 1, D) X(64, 1, D) X(32, 2, D) X(64, 2, D) X(32, 4, D) X(64, 4, D)
 
 // Wide workgroups (1024 threads) for long rows: one x staging (up to 64 KB
-// of LDS for K = 15360) serves 16 wavefronts instead of 4.
+// of LDS for K = 15360) serves 16 wavefronts instead of 4.  (At K ~ 4096
+// they measured slower than 256-thread workgroups, so only these exist.)
 #define GH_WIDE(T, G, D)                                                                   \
   GH_STREAM_KERNEL_NT(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)         \
   GH_STREAM_KERNEL_NT(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)

@@ -87,9 +87,10 @@ namespace gh {
 
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out) {
-  const bool plain_gemv = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0);
-  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, plain_gemv);
-  out->lds = x_lds_bytes(K) + 64;
+  // 1024-thread variants exist for the plain GEMVs (long rows)
+  const bool wide_ok = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0);
+  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, wide_ok);
+  out->lds = x_lds_bytes(K) + 256;  // + the prologue/epilogue scratch (64 floats)
   if (out->lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
   out->name = std::string(family) + (normed ? "n" : "") + "_t" + std::to_string(c.tpr) + "_g" +
               std::to_string(c.gpl) + "_d" + std::to_string(c.depth) + (c.nt == 1024 ? "_w" : "");

@@ -128,18 +128,16 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
     for (int i = 0; i < A_PER; i++) {
       const uint32_t c = tid + i * PF_NT;
       const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
-      _Float16 hi[4], lo[4];
+      typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+      half4 hi, lo;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         hi[e] = (_Float16)v[e];
         lo[e] = (_Float16)(v[e] - (float)hi[e]);
       }
       const uint32_t o = (c / 8) * LDS_STRIDE + 4 * (c % 8);
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        Ah[o + e] = hi[e];
-        Al[o + e] = lo[e];
-      }
+      *reinterpret_cast<half4*>(&Ah[o]) = hi;
+      *reinterpret_cast<half4*>(&Al[o]) = lo;
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {

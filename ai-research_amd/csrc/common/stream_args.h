@@ -28,6 +28,4 @@ struct ArgmaxArgs {  // Q8ArgmaxFmt::Args
   const uint8_t* W;
   float* Y;
   uint32_t* partial;
-  uint32_t* counter;
-  uint32_t* token;
 };

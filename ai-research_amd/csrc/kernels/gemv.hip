@@ -602,9 +602,45 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 
 // Q8_0 vocab projection with the argmax fused in (shaders/gemv_q8.wgsl then
 // shaders/argmax.wgsl, src/gpu/model_dispatch.zig:124-126): every lane keeps
-// the best (logit, row) of its team's rows; block_end reduces the block,
-// writes one partial, and the last block to finish reduces the partials in
-// block order and writes the token.  Logits are stored only when Y != null.
+// the best (logit, row) of its team's rows and block_end writes the block's
+// best as one partial.  gh_argmax_final_k, launched right after, reduces the
+// partials to the token.  (A "last block reduces" scheme inside the stream
+// needs a device-scope fence per workgroup, which costs more than the whole
+// second launch.)  Logits are stored only when Y != null.
+__device__ __forceinline__ void wave_best(float& v, uint32_t& i) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const uint32_t oi = __shfl_xor(i, off, 64);
+    if (better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// Best (value, index) of the block: every thread passes its candidate;
+// thread 0 returns the result.  red holds 2 * NT / 64 words.
+template <int NT>
+__device__ __forceinline__ void block_best(float& bv, uint32_t& bi, float* red) {
+  constexpr int W = NT / 64;
+  float* rv = red;
+  uint32_t* ri = reinterpret_cast<uint32_t*>(red + W);
+  wave_best(bv, bi);
+  if ((threadIdx.x & 63) == 0) {
+    rv[threadIdx.x >> 6] = bv;
+    ri[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < W; w++)
+      if (better(rv[w], ri[w], bv, bi)) {
+        bv = rv[w];
+        bi = ri[w];
+      }
+  }
+}
+
 struct Q8ArgmaxFmt {
   static constexpr uint32_t kGroupBytes = 144, kBlockBytes = 36;
   using Item = Q8Fmt::Item;
@@ -615,9 +651,7 @@ struct Q8ArgmaxFmt {
   struct Args {
     const uint8_t* W;
     float* Y;
-    uint32_t* partial;  // 2 words per block
-    uint32_t* counter;  // zero between launches
-    uint32_t* token;
+    uint32_t* partial;  // 2 words per block: best value bits, its row
   };
   __device__ static void load(Item& it, const Args& a, size_t off) {
     load_q8g(it.w, a.W + off);
@@ -640,70 +674,14 @@ struct Q8ArgmaxFmt {
       c.bi = row;
     }
   }
-  __device__ static void wave_best(float& v, uint32_t& i) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(v, off, 64);
-      const uint32_t oi = __shfl_xor(i, off, 64);
-      if (better(ov, oi, v, i)) {
-        v = ov;
-        i = oi;
-      }
-    }
-  }
   template <int NT>
   __device__ static void block_end(const Acc& c, const Args& a, float* red) {
-    constexpr int W = NT / 64;
-    float* rv = red;
-    uint32_t* ri = reinterpret_cast<uint32_t*>(red + W);
-    uint32_t* last = ri + W;
     float bv = c.bv;
     uint32_t bi = c.bi;
-    wave_best(bv, bi);
-    if ((threadIdx.x & 63) == 0) {
-      rv[threadIdx.x >> 6] = bv;
-      ri[threadIdx.x >> 6] = bi;
-    }
-    __syncthreads();
+    block_best<NT>(bv, bi, red);
     if (threadIdx.x == 0) {
-      for (int w = 1; w < W; w++)
-        if (better(rv[w], ri[w], bv, bi)) {
-          bv = rv[w];
-          bi = ri[w];
-        }
       a.partial[2 * blockIdx.x] = __float_as_uint(bv);
       a.partial[2 * blockIdx.x + 1] = bi;
-      __threadfence();
-      last[0] = (atomicAdd(a.counter, 1u) == gridDim.x - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!last[0]) return;
-    __threadfence();
-    bv = -INFINITY;
-    bi = 0xFFFFFFFFu;
-    for (uint32_t b = threadIdx.x; b < gridDim.x; b += NT) {
-      const float v = __uint_as_float(__builtin_nontemporal_load(&a.partial[2 * b]));
-      const uint32_t i = __builtin_nontemporal_load(&a.partial[2 * b + 1]);
-      if (better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-      }
-    }
-    wave_best(bv, bi);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) {
-      rv[threadIdx.x >> 6] = bv;
-      ri[threadIdx.x >> 6] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < W; w++)
-        if (better(rv[w], ri[w], bv, bi)) {
-          bv = rv[w];
-          bi = ri[w];
-        }
-      a.token[0] = bi == 0xFFFFFFFFu ? 0u : bi;
-      a.counter[0] = 0;
     }
   }
 };
@@ -798,8 +776,8 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 #define GH_A_W (W, Y)
 #define GH_P_GU (const uint8_t* Wg, const uint8_t* Wu, float* Y)
 #define GH_A_GU (Wg, Wu, Y)
-#define GH_P_AM (const uint8_t* W, float* Y, uint32_t* partial, uint32_t* counter, uint32_t* token)
-#define GH_A_AM (W, Y, partial, counter, token)
+#define GH_P_AM (const uint8_t* W, float* Y, uint32_t* partial)
+#define GH_A_AM (W, Y, partial)
 
 #define GH_PLAIN(T, G, D)                                                        \
   GH_STREAM_KERNEL(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false)            \
@@ -833,4 +811,23 @@ GH_SHAPES(GH_PLAIN, 1)
 GH_SHAPES(GH_PLAIN, 2)
 GH_SHAPES(GH_PLAIN, 3)
 GH_WIDE(32, 4, 1) GH_WIDE(64, 2, 1) GH_WIDE(64, 4, 1)  // depth 2 at 1024 threads spills
+
+// The token from the n block partials of a fused argmax stream: the largest
+// value, the lowest row among equals (src/kernels.zig:164-174).  One block.
+extern "C" __global__ __launch_bounds__(256) void gh_argmax_final_k(const uint32_t* partial,
+                                                                   uint32_t n, uint32_t* token) {
+  __shared__ float red[8];
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t b = threadIdx.x; b < n; b += 256) {
+    const float v = __uint_as_float(partial[2 * b]);
+    const uint32_t i = partial[2 * b + 1];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  block_best<256>(bv, bi, red);
+  if (threadIdx.x == 0) token[0] = bi == 0xFFFFFFFFu ? 0u : bi;
+}
 #endif

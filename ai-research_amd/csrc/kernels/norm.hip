@@ -73,17 +73,14 @@ __device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
   }
 }
 
-// Two levels: every workgroup reduces a contiguous slice into a partial, the
-// last workgroup to finish reduces the partials (deterministic order) and
-// writes out_token.  partial: 2 * gridDim.x words; counter: 1 word, zero
-// between launches (reset by the last workgroup).
+// shaders/argmax.wgsl split over workgroups: each workgroup writes the best
+// (value, index) of its contiguous chunk to partial[2 b], [2 b + 1];
+// gh_argmax_final_k then reduces the partials to the token (no device-scope
+// fence per workgroup, see the fused LM-head stream).
 extern "C" __global__ __launch_bounds__(256) void gh_argmax_k(const float* __restrict__ logits,
-                                                              uint32_t n, uint32_t* out_token,
-                                                              uint32_t* partial,
-                                                              uint32_t* counter) {
+                                                              uint32_t n, uint32_t* partial) {
   __shared__ float sv[4];
   __shared__ uint32_t si[4];
-  __shared__ uint32_t last;
   const uint32_t per = (n + gridDim.x - 1) / gridDim.x;
   const uint32_t b0 = blockIdx.x * per, b1 = min(n, b0 + per);
   float bv = -INFINITY;
@@ -110,35 +107,5 @@ extern "C" __global__ __launch_bounds__(256) void gh_argmax_k(const float* __res
       }
     partial[2 * blockIdx.x] = __float_as_uint(bv);
     partial[2 * blockIdx.x + 1] = bi;
-    __threadfence();
-    last = (atomicAdd(counter, 1u) == gridDim.x - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  bv = -INFINITY;
-  bi = 0xFFFFFFFFu;
-  for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
-    const float v = __uint_as_float(__builtin_nontemporal_load(&partial[2 * b]));
-    const uint32_t i = __builtin_nontemporal_load(&partial[2 * b + 1]);
-    if (better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
-    }
-  }
-  wave_argmax(bv, bi);
-  if (lane == 0) {
-    sv[wave] = bv;
-    si[wave] = bi;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; w++)
-      if (better(sv[w], si[w], bv, bi)) {
-        bv = sv[w];
-        bi = si[w];
-      }
-    out_token[0] = bi == 0xFFFFFFFFu ? 0u : bi;
-    counter[0] = 0;
   }
 }

@@ -127,6 +127,19 @@ gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> 
   return ctx->launch(sh.name, dim3(sh.grid), dim3(sh.nt), sh.lds, args.data());
 }
 
+gh_status launch_argmax_stream(gh_context* ctx, ArgmaxArgs* a, const XPro& xp, uint32_t M,
+                               uint32_t K, uint32_t* token) {
+  StreamShape sh;
+  gh_status st = stream_shape(ctx, "gh_argmax_q8", xp.mode != 0, M, K, &sh);
+  if (st != GH_OK) return st;
+  if (sh.grid > kArgmaxMaxBlocks) return fail(GH_ERR_UNSUPPORTED, "argmax stream: grid too large");
+  if ((st = launch_stream(ctx, "gh_argmax_q8", {&a->W, &a->Y, &a->partial}, xp, M, K)) != GH_OK)
+    return st;
+  uint32_t n = sh.grid;
+  void* args[] = {&a->partial, &n, &token};
+  return ctx->launch("gh_argmax_final_k", dim3(1), dim3(256), 0, args);
+}
+
 gh_status check_pro(const gh_context* ctx, const XPro& p, uint32_t K, const char* who) {
   if (p.mode > 2) return fail(GH_ERR_INVALID, std::string(who) + ": prologue mode must be 0..2");
   if (!p.x || (reinterpret_cast<uintptr_t>(p.x) & 15))
@@ -235,12 +248,8 @@ gh_status gh_norm_gemv_argmax_q8(gh_context* ctx, const void* W, float* logits,
   st = ctx->ensure_zeroed(&ctx->argmax_scratch, &ctx->argmax_scratch_bytes, kArgmaxScratchBytes);
   if (st != GH_OK) return st;
   uint32_t* base = static_cast<uint32_t*>(ctx->argmax_scratch);
-  ArgmaxArgs a{static_cast<const uint8_t*>(W), logits, base + 64, base, token};
-  gh::StreamShape sh;
-  if ((st = gh::stream_shape(ctx, "gh_argmax_q8", p.mode != 0, M, K, &sh)) != GH_OK) return st;
-  if (sh.grid > kArgmaxMaxBlocks)
-    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gemv_argmax_q8: grid too large");
-  return launch_stream(ctx, "gh_argmax_q8", &a, p, M, K);
+  ArgmaxArgs a{static_cast<const uint8_t*>(W), logits, base + 64};
+  return gh::launch_argmax_stream(ctx, &a, p, M, K, token);
 }
 
 gh_status gh_rmsnorm(gh_context* ctx, const float* X, const float* W, float* Y, uint32_t dim,
@@ -397,10 +406,13 @@ gh_status gh_argmax(gh_context* ctx, const float* logits, uint32_t* out_token, u
   gh_status st = ctx->ensure_zeroed(&ctx->argmax_scratch, &ctx->argmax_scratch_bytes,
                                     kArgmaxScratchBytes);
   if (st != GH_OK) return st;
-  uint32_t* counter = static_cast<uint32_t*>(ctx->argmax_scratch);
-  uint32_t* partial = counter + 64;
-  void* args[] = {const_cast<float**>(&logits), &vocab, &out_token, &partial, &counter};
-  return ctx->launch("gh_argmax_k", dim3(grid), dim3(256), 0, args);
+  uint32_t* partial = static_cast<uint32_t*>(ctx->argmax_scratch) + 64;
+  void* args[] = {const_cast<float**>(&logits), &vocab, &partial};
+  gh_status st2 = ctx->launch("gh_argmax_k", dim3(grid), dim3(256), 0, args);
+  if (st2 != GH_OK) return st2;
+  uint32_t n = grid;
+  void* fargs[] = {&partial, &n, &out_token};
+  return ctx->launch("gh_argmax_final_k", dim3(1), dim3(256), 0, fargs);
 }
 
 }  // extern "C"

@@ -186,7 +186,7 @@ gh_status plan(gh_model* m) {
   }
   m->nsplit = gh::attention_splits(m->ctx, max_nkv, c.max_slots);
   m->attn_part = take((size_t)max_nkv * m->nsplit * max_g * (max_d + 4) * 4);
-  m->amax = take((64 + 2 * 4096) * 4);
+  m->amax = take(2 * 4096 * 4);  // LM-head argmax partials: 2 words per workgroup
   m->arena_bytes = off;
   return GH_OK;
 }
@@ -351,14 +351,10 @@ gh_status record_forward(gh_model* m, bool logits) {
     p.eps = c.rms_norm_eps;
     p.mode = 2;
     m->hidden_final = xoth;
-    uint32_t* amax = m->at<uint32_t>(m->amax);
-    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), amax + 64, amax,
-                  m->at<uint32_t>(m->token)};
-    gh::StreamShape sh;
-    if ((st = gh::stream_shape(ctx, "gh_argmax_q8", true, c.vocab_size, H, &sh)) != GH_OK)
+    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
+    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
+        GH_OK)
       return st;
-    if (sh.grid > 4096) return fail(GH_ERR_UNSUPPORTED, "model: LM head grid too large");
-    if ((st = gh::launch_stream(ctx, "gh_argmax_q8", &aa, p, c.vocab_size, H)) != GH_OK) return st;
     e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost,
                        ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "record: token copy");
@@ -838,10 +834,10 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     p.eps = c.rms_norm_eps;
     p.mode = 2;
     m->hidden_final = m->x1;
-    uint32_t* amax = m->at<uint32_t>(m->amax);
-    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), amax + 64, amax,
-                  m->at<uint32_t>(m->token)};
-    if ((st = gh::launch_stream(ctx, "gh_argmax_q8", &aa, p, c.vocab_size, H)) != GH_OK) return st;
+    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
+    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
+        GH_OK)
+      return st;
   }
   return GH_OK;
 }

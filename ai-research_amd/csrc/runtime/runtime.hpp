@@ -60,11 +60,10 @@ inline gh_status launch_stream(gh_context* ctx, const char* family, GateUpArgs* 
                                const XPro& xp, uint32_t M, uint32_t K) {
   return launch_stream(ctx, family, {&a->Wg, &a->Wu, &a->Y}, xp, M, K);
 }
-inline gh_status launch_stream(gh_context* ctx, const char* family, ArgmaxArgs* a,
-                               const XPro& xp, uint32_t M, uint32_t K) {
-  return launch_stream(ctx, family, {&a->W, &a->Y, &a->partial, &a->counter, &a->token}, xp, M,
-                       K);
-}
+// The fused Q8 LM-head stream (family gh_argmax_q8) followed by the
+// reduction of its block partials to the token.
+gh_status launch_argmax_stream(gh_context* ctx, ArgmaxArgs* a, const XPro& xp, uint32_t M,
+                               uint32_t K, uint32_t* token);
 // Kernel name and persistent grid of one row-stream launch.
 struct StreamShape {
   std::string name;

@@ -326,9 +326,11 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   const uint32_t bn_big = pair ? 64 : 128;
   const bool big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128) >= cus;
   const uint32_t bm = big ? 128 : 64, bn = big ? bn_big : 64;
+  int kb = 1;  // quant blocks per K step (tuning: GH_PF_KB=2)
+  if (const char* env = getenv("GH_PF_KB")) kb = atoi(env) == 2 ? 2 : 1;
   std::string name = std::string(pair ? "gh_pf_gateup_" : "gh_pf_gemm_") +
                      (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
-                     std::to_string(bn);
+                     std::to_string(bn) + "_k" + std::to_string(kb);
   dim3 grid((N + bn - 1) / bn, (T + bm - 1) / bm);
   if (pair) {
     void* args[] = {&A, const_cast<void**>(&W0), const_cast<void**>(&W1), &C, &T, &N, &K};

@@ -109,7 +109,7 @@ def test_gemv_rejects_unsupported_shapes(gpu):
 
 
 # ---------------------------------------------------------------- Q8 GEMV -
-@pytest.mark.parametrize("M,K", [(4096, 3840), (777, 1024), (1, 128)])
+@pytest.mark.parametrize("M,K", [(4096, 3840), (777, 1024), (1, 128), (3840, 15360)])
 def test_gemv_q8_parity(gpu, M, K):
     w = gh.synth_normal(M * K, 0, 2000 + M, 0.0, 0.02, bf16=True).reshape(M, K)
     wq = orc.quantize_q8(w, NT)
@@ -186,6 +186,28 @@ def test_norm_gemv_prologues(gpu, mode, with_rnorm):
     assert_close(Y.read(np.float32, M), orc.gemv_q4(wq, xin, K, NT), what="norm_gemv mode %d" % mode)
     if mode == 2:
         assert_close(XO.read(np.float32, K), xn, what="residual stream")
+
+
+@pytest.mark.parametrize("with_rnorm", [True, False])
+def test_norm_gemv_residual_cancellation(gpu, with_rnorm):
+    # x + r' nearly cancels: the prologue's one-pass sum of squares (expanded
+    # from sum x^2, sum x r', sum r'^2) would lose the result, so it reduces
+    # the residual itself; the output must still match the oracle
+    M, K = 512, 3840
+    wq = q4_weights(M, K, 0, 4050)
+    r = gh.synth_normal(K, 0, 51, 0.0, 1.0)
+    wr = _bf16r(gh.synth_normal(K, 0, 52, 1.0, 0.1))
+    wn = _bf16r(gh.synth_normal(K, 0, 53, 1.0, 0.1))
+    rr = orc.rmsnorm(r, wr) if with_rnorm else r
+    x = (-rr + 1e-3 * gh.synth_normal(K, 0, 54, 0.0, 1.0)).astype(np.float32)
+    X, R, WN, WR, XO, Y = (gpu.upload(x), gpu.upload(r), gpu.upload(wn), gpu.upload(wr),
+                           gpu.alloc(K * 4), gpu.alloc(M * 4))
+    pro = gpu.prologue(X, 2, norm=WN, r=R, r_norm=WR if with_rnorm else None, x_out=XO, scalar=1.0)
+    gpu.norm_gemv(gh.QUANT_Q4, gpu.upload(wq), Y, M, K, pro)
+    xn = (x + rr).astype(np.float32)
+    assert_close(XO.read(np.float32, K), xn, what="residual stream")
+    assert_close(Y.read(np.float32, M), orc.gemv_q4(wq, orc.rmsnorm(xn, wn), K, NT),
+                 what="norm_gemv under cancellation")
 
 
 def test_norm_gate_up_matches_oracle(gpu):

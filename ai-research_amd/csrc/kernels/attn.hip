@@ -420,9 +420,11 @@ extern "C" __global__ __launch_bounds__(64) void gh_pf_qkv_rope_k(AttnArgs a,
 
 // Combine the split partials of one query head:
 // out = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s.  One workgroup of
-// 256 threads per query head; wave w takes splits w, w + 4, ... and issues
-// all its partial-row loads before consuming any (one L2 round trip for up
-// to 32 splits); the four waves' sums combine in wave order through LDS.
+// 256 threads per query head; wave w takes splits w, w + 4, ...  Every load
+// of the common case (D <= 256, up to 32 splits) -- the thread's (m, l) and
+// its partial-row slices -- is issued before any is used, with clamped
+// indices, so the kernel costs one L2 round trip; only the weights wait for
+// the block-wide max.  The four waves' sums combine in wave order through LDS.
 #define MERGE_U 8
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) {
   __shared__ float c[MAX_SPLIT];
@@ -433,9 +435,20 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a)
   const uint32_t kvh = h / G, g = h % G, PS = D + 4, ns = a.nsplit;
   const float* allp = a.part + (size_t)kvh * ns * G * PS + (size_t)g * PS;
   const size_t stride = (size_t)G * PS;  // one split to the next
-  // running max and weights: thread t owns split t (ns <= 256)
-  const float ms = tid < ns ? allp[tid * stride + D] : -INFINITY;
-  const float ls = tid < ns ? allp[tid * stride + D + 1] : 0.f;
+  const uint32_t D4 = D / 4;
+  auto row = [&](uint32_t sp, uint32_t col) {  // clamped: out-of-range reads get weight 0
+    sp = sp < ns ? sp : ns - 1;
+    col = col < D4 ? col : D4 - 1;
+    return *reinterpret_cast<const float4*>(allp + sp * stride + col * 4);
+  };
+  // thread t owns split t's (m, l) (ns <= 256); the first column pass's rows
+  const uint32_t tc = tid < ns ? tid : ns - 1;
+  const float2 mlv = *reinterpret_cast<const float2*>(allp + tc * stride + D);
+  float4 t0[MERGE_U];
+#pragma unroll
+  for (int u = 0; u < MERGE_U; u++) t0[u] = row(wave + u * ATT_WAVES, lane);
+  const float ms = tid < ns ? mlv.x : -INFINITY;
+  const float ls = tid < ns ? mlv.y : 0.f;
   float M = ms;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
@@ -445,23 +458,19 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a)
   const float cs = ms == -INFINITY ? 0.f : __expf(ms - M);
   if (tid < ns) c[tid] = cs;
   float L = wave_allsum(cs * ls);
-  __syncthreads();  // red[] reads done
+  __syncthreads();  // red[] reads done, c[] written
   if (lane == 0) red[wave] = L;
   __syncthreads();
   L = (red[0] + red[1]) + (red[2] + red[3]);
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   // weighted column sums: lane -> float4 column, wave -> splits w, w+4, ...
-  const uint32_t D4 = D / 4;
   for (uint32_t col = lane; col < D4; col += 64) {
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t sp0 = wave; sp0 < ns; sp0 += ATT_WAVES * MERGE_U) {
       float4 t[MERGE_U];
+      const bool first = col == lane && sp0 == wave;
 #pragma unroll
-      for (int u = 0; u < MERGE_U; u++) {
-        const uint32_t sp = sp0 + u * ATT_WAVES;
-        t[u] = sp < ns ? *reinterpret_cast<const float4*>(allp + sp * stride + col * 4)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int u = 0; u < MERGE_U; u++) t[u] = first ? t0[u] : row(sp0 + u * ATT_WAVES, col);
 #pragma unroll
       for (int u = 0; u < MERGE_U; u++) {
         const uint32_t sp = sp0 + u * ATT_WAVES;

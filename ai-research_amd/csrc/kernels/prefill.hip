@@ -82,7 +82,11 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 
 // NMAT = 1: C = A W^T.  NMAT = 2: C = gelu_tanh(A Wg^T) * (A Wu^T).  A, C f32.
 // Each step covers KB quant blocks (32 KB elements of K).
-template <class F, int BM, int BN, int NMAT, int KB>
+// SPLIT (split-K, for few tiles): workgroup z of gridDim.z runs K steps
+// [z S / Z, (z + 1) S / Z) and writes its raw sums to C as partial plane
+// (z, matrix) of [Z][NMAT][T][N]; gh_pf_splitk_k adds the planes in z order
+// and applies the epilogue.
+template <class F, int BM, int BN, int NMAT, int KB, bool SPLIT>
 __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
                                           const uint8_t* __restrict__ W0,
                                           const uint8_t* __restrict__ W1, float* __restrict__ C,
@@ -174,11 +178,14 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[q][i][j][r] = 0.f;
 
-  load_step(0);
-  for (uint32_t step = 0; step < nsteps; step++) {
+  const uint32_t nz = SPLIT ? gridDim.z : 1u, z = SPLIT ? blockIdx.z : 0u;
+  const uint32_t s_begin = (uint32_t)((uint64_t)nsteps * z / nz);
+  const uint32_t s_end = (uint32_t)((uint64_t)nsteps * (z + 1) / nz);
+  if (s_begin < s_end) load_step(s_begin);
+  for (uint32_t step = s_begin; step < s_end; step++) {
     store_step(step);
     __syncthreads();
-    if (step + 1 < nsteps) load_step(step + 1);  // in flight through this step's MFMAs
+    if (step + 1 < s_end) load_step(step + 1);  // in flight through this step's MFMAs
 #pragma unroll
     for (int kq = 0; kq < KB; kq++) {
       half8 ah[2][TM], al[2][TM];
@@ -224,41 +231,73 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
       for (int r = 0; r < 16; r++) {
         const uint32_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
         if (row < T && col < N) {
-          if constexpr (NMAT == 1)
+          if constexpr (SPLIT) {
+#pragma unroll
+            for (int q = 0; q < NMAT; q++)
+              C[((size_t)(z * NMAT + q) * T + row) * N + col] = acc[q][i][j][r];
+          } else if constexpr (NMAT == 1) {
             C[(size_t)row * N + col] = acc[0][i][j][r];
-          else
+          } else {
             C[(size_t)row * N + col] = gelu_tanh(acc[0][i][j][r]) * acc[1][i][j][r];
+          }
         }
       }
     }
 }
 
-#define GH_GEMM(NAME, F, BM, BN, KB)                                                      \
-  extern "C" __global__ __launch_bounds__(PF_NT) void NAME##_k##KB(                        \
+#define GH_GEMM(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                   \
+  extern "C" __global__ __launch_bounds__(PF_NT) void NAME##_k##KB##SUFFIX(                \
       const float* A, const uint8_t* W, float* C, uint32_t T, uint32_t N, uint32_t K) {    \
-    gemm_tile<F, BM, BN, 1, KB>(A, W, W, C, T, N, K);                                      \
+    gemm_tile<F, BM, BN, 1, KB, SPLIT>(A, W, W, C, T, N, K);                           \
   }
-#define GH_GEMM_PAIR(NAME, F, BM, BN, KB)                                                 \
-  extern "C" __global__ __launch_bounds__(PF_NT) void NAME##_k##KB(                        \
+#define GH_GEMM_PAIR(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                              \
+  extern "C" __global__ __launch_bounds__(PF_NT) void NAME##_k##KB##SUFFIX(                \
       const float* A, const uint8_t* Wg, const uint8_t* Wu, float* Act, uint32_t T,        \
       uint32_t N, uint32_t K) {                                                            \
-    gemm_tile<F, BM, BN, 2, KB>(A, Wg, Wu, Act, T, N, K);                                  \
+    gemm_tile<F, BM, BN, 2, KB, SPLIT>(A, Wg, Wu, Act, T, N, K);                       \
   }
-#define GH_GEMM_ALL(KB)                                            \
-  GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, KB)              \
-  GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, KB)                  \
-  GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, KB)              \
-  GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, KB)                  \
-  GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, KB)         \
-  GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, KB)           \
-  GH_GEMM_PAIR(gh_pf_gateup_q8_m128_n64, Q8W, 128, 64, KB)         \
-  GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, KB)
+#define GH_GEMM_ALL(KB)                                                   \
+  GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, KB, false, )            \
+  GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, KB, false, )                \
+  GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, KB, false, )            \
+  GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, KB, false, )                \
+  GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, KB, false, )       \
+  GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, KB, false, )         \
+  GH_GEMM_PAIR(gh_pf_gateup_q8_m128_n64, Q8W, 128, 64, KB, false, )       \
+  GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, KB, false, )
 
 // One quant block per K step measured fastest (12B prefill 62.7 ms vs 65.9
 // and 68.4 ms at 2 and 4 blocks): the step is bound by the per-block scale
 // FMAs and operand conversions, not by load latency.
 GH_GEMM_ALL(1)
 GH_GEMM_ALL(2)
+
+// Split-K forms of the small tile, for batches whose tiles alone cannot
+// fill the CUs (a few prompt tokens): without them each workgroup walks all
+// of K one block per step, and that serial chain, not bandwidth, sets the time.
+GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
+GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
+GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
+GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
+
+// C[T][N] from the Z partial planes of a split-K GEMM, added in z order (so
+// the result does not depend on scheduling): the plain sum (nmat 1) or
+// gelu_tanh(sum of gate planes) * (sum of up planes) (nmat 2).
+extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* __restrict__ P,
+                                                                  float* __restrict__ C,
+                                                                  uint32_t T, uint32_t N,
+                                                                  uint32_t nz, uint32_t nmat) {
+  const size_t tn = (size_t)T * N;
+  for (size_t i = (size_t)blockIdx.x * PF_NT + threadIdx.x; i < tn; i += (size_t)gridDim.x * PF_NT) {
+    float g = 0.f, u = 0.f;
+#pragma unroll 4
+    for (uint32_t z = 0; z < nz; z++) {
+      g += P[(size_t)z * nmat * tn + i];
+      if (nmat == 2) u += P[((size_t)z * 2 + 1) * tn + i];
+    }
+    C[i] = nmat == 2 ? gelu_tanh(g) * u : g;
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Row-wise x prologue for T tokens (the batched form of the decode GEMVs'
@@ -281,48 +320,53 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-#define PF_ROW_MAX 32  // elements per thread: hidden <= 8192
+#define PF_NORM_NT 1024
+#define PF_ROW_MAX 8  // elements per thread: hidden <= 8192
 
-extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_norm_k(
+// Every load (x, r, wr, w) is issued before any is used, with clamped
+// indices and stand-in pointers for the operands a mode does not read, so
+// the row costs one global round trip rather than one per operand.
+extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     float* X, const float* R, const float* wr, const float* w, float* Xn, uint32_t H,
     float s, float eps, uint32_t mode) {
-  __shared__ float red[PF_NT / 64];
+  __shared__ float red[PF_NORM_NT / 64];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  const bool add = mode == 2, has_wr = wr != nullptr;
   float* x = X + (size_t)t * H;
-  float v[PF_ROW_MAX];
+  const float* r = add ? R + (size_t)t * H : x;
+  const float* wrp = has_wr ? wr : w;
+  float v[PF_ROW_MAX], rv[PF_ROW_MAX], wv[PF_ROW_MAX], wrv[PF_ROW_MAX];
 #pragma unroll
   for (int u = 0; u < PF_ROW_MAX; u++) {
-    const uint32_t i = tid + u * PF_NT;
-    v[u] = i < H ? x[i] : 0.f;
+    uint32_t i = tid + u * PF_NORM_NT;
+    i = i < H ? i : H - 1;
+    v[u] = x[i];
+    rv[u] = r[i];
+    wv[u] = w[i];
+    wrv[u] = wrp[i];
   }
-  if (mode == 2) {
-    const float* r = R + (size_t)t * H;
-    float rv[PF_ROW_MAX];
+  if (add) {
     float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < PF_ROW_MAX; u++) {
-      const uint32_t i = tid + u * PF_NT;
-      rv[u] = i < H ? r[i] : 0.f;
-      ss += rv[u] * rv[u];
-    }
-    const float inv_r = 1.0f / sqrtf(block_sum<PF_NT>(ss, red) / (float)H + eps);
+    for (int u = 0; u < PF_ROW_MAX; u++)
+      if (tid + u * PF_NORM_NT < H) ss += rv[u] * rv[u];
+    const float inv_r = has_wr ? 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps) : 1.0f;
 #pragma unroll
     for (int u = 0; u < PF_ROW_MAX; u++) {
-      const uint32_t i = tid + u * PF_NT;
-      if (i < H) {
-        const float rr = wr ? rv[u] * inv_r * wr[i] : rv[u];
-        v[u] = (v[u] + rr) * s;
-        x[i] = v[u];
-      }
+      const uint32_t i = tid + u * PF_NORM_NT;
+      const float rr = has_wr ? rv[u] * inv_r * wrv[u] : rv[u];
+      v[u] = (v[u] + rr) * s;
+      if (i < H) x[i] = v[u];
     }
   }
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < PF_ROW_MAX; u++) ss += v[u] * v[u];
-  const float inv = 1.0f / sqrtf(block_sum<PF_NT>(ss, red) / (float)H + eps);
+  for (int u = 0; u < PF_ROW_MAX; u++)
+    if (tid + u * PF_NORM_NT < H) ss += v[u] * v[u];
+  const float inv = 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps);
 #pragma unroll
   for (int u = 0; u < PF_ROW_MAX; u++) {
-    const uint32_t i = tid + u * PF_NT;
-    if (i < H) Xn[(size_t)t * H + i] = v[u] * inv * w[i];
+    const uint32_t i = tid + u * PF_NORM_NT;
+    if (i < H) Xn[(size_t)t * H + i] = v[u] * inv * wv[u];
   }
 }

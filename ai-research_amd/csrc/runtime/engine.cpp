@@ -332,12 +332,39 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
                      (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
                      std::to_string(bn) + "_k" + std::to_string(kb);
   dim3 grid((N + bn - 1) / bn, (T + bm - 1) / bm);
-  if (pair) {
-    void* args[] = {&A, const_cast<void**>(&W0), const_cast<void**>(&W1), &C, &T, &N, &K};
-    return ctx->launch(name, grid, dim3(256), 0, args);
+  // Split K when the tiles alone leave CUs idle: about two workgroups per CU,
+  // at least 8 K steps per split (GH_PF_SPLIT=n forces n, 1 disables).
+  const uint32_t tiles = grid.x * grid.y, nsteps = K / 32;
+  uint32_t nz = 1;
+  if (!big && tiles < cus) nz = std::min<uint32_t>((2 * cus + tiles - 1) / tiles, std::max(1u, nsteps / 8));
+  if (const char* env = getenv("GH_PF_SPLIT")) {
+    const int v = atoi(env);
+    if (v >= 1 && !big) nz = std::min<uint32_t>((uint32_t)v, nsteps);
   }
-  void* args[] = {&A, const_cast<void**>(&W0), &C, &T, &N, &K};
-  return ctx->launch(name, grid, dim3(256), 0, args);
+  nz = std::min<uint32_t>(nz, 64u);
+  float* out = C;
+  const uint32_t nmat = pair ? 2u : 1u;
+  if (nz > 1) {
+    const size_t need = (size_t)nz * nmat * T * N * sizeof(float);
+    gh_status st = ctx->ensure_zeroed(&ctx->gemm_scratch, &ctx->gemm_scratch_bytes, need);
+    if (st != GH_OK) return st;
+    out = static_cast<float*>(ctx->gemm_scratch);
+    name += "_s";
+    grid.z = nz;
+  }
+  gh_status st;
+  if (pair) {
+    void* args[] = {&A, const_cast<void**>(&W0), const_cast<void**>(&W1), &out, &T, &N, &K};
+    st = ctx->launch(name, grid, dim3(256), 0, args);
+  } else {
+    void* args[] = {&A, const_cast<void**>(&W0), &out, &T, &N, &K};
+    st = ctx->launch(name, grid, dim3(256), 0, args);
+  }
+  if (st != GH_OK || nz == 1) return st;
+  const uint64_t tn = (uint64_t)T * N;
+  const unsigned rgrid = (unsigned)std::min<uint64_t>((tn + 255) / 256, 4ull * cus);
+  void* rargs[] = {&out, &C, &T, &N, &nz, const_cast<uint32_t*>(&nmat)};
+  return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {

@@ -743,7 +743,7 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   float* Xn = m->pf_xn;
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
                   &Xn, &H, &s, &eps, &mode};
-  return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(256), 0, args);
+  return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
 }
 
 gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {

@@ -24,6 +24,8 @@ struct gh_context {
   size_t attn_scratch_bytes = 0;
   void* argmax_scratch = nullptr;
   size_t argmax_scratch_bytes = 0;
+  void* gemm_scratch = nullptr;  // split-K partial planes of the prefill GEMM
+  size_t gemm_scratch_bytes = 0;
   gh_status ensure_zeroed(void** buf, size_t* have, size_t need);
   std::unordered_map<std::string, hipFunction_t> fns;
   std::mutex mu;

@@ -53,6 +53,28 @@ def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     assert_close(got, ref, what="prefill GeGLU")
 
 
+@pytest.mark.parametrize("pair", [False, True])
+@pytest.mark.parametrize("split", ["1", "3", "200"])
+def test_prefill_split_k(gpu, monkeypatch, pair, split):
+    # a few tokens: the split-K forms (forced 1 = unsplit, 3 = an even split
+    # of 120 K steps, 200 = clamped to the 64-split cap, so one or two K steps
+    # per split) against the product
+    T, N, K = 5, 320, 3840
+    monkeypatch.setenv("GH_PF_SPLIT", split)
+    gq, gdeq = quantized(N, K, gh.QUANT_Q4, 320)
+    uq, udeq = quantized(N, K, gh.QUANT_Q4, 321)
+    a = gh.synth_normal(T * K, 1, 322, 0.0, 1.0).reshape(T, K)
+    A, C = gpu.upload(a), gpu.alloc(T * N * 4)
+    a64 = np.asarray(a, np.float64)
+    if pair:
+        gpu.prefill_gate_up_geglu(gh.QUANT_Q4, gpu.upload(gq), gpu.upload(uq), A, C, T, N, K)
+        ref = nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T)
+    else:
+        gpu.prefill_gemm(gh.QUANT_Q4, gpu.upload(gq), A, C, T, N, K)
+        ref = a64 @ gdeq.T
+    assert_close(C.read(np.float32, T * N).reshape(T, N), ref, what="split-K %s" % split)
+
+
 def test_prefill_gemm_rejects_bad_shapes(gpu):
     W, A, C = gpu.alloc(4096), gpu.alloc(4096), gpu.alloc(4096)
     with pytest.raises(gh.GhError):

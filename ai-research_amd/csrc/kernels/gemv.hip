@@ -70,7 +70,8 @@ __device__ __forceinline__ float sum64(float v) {
 }
 
 // Stage x[K] into LDS (padded by group) and write the per-block sums.
-// K % 128 == 0.  All NT threads of the block must call it.  The loads of a
+// K % 128 == 0.  Called by the first NT threads of the block (whole
+// wavefronts); the caller synchronises.  The loads of a
 // chunk of U float4 per thread are all issued before any is consumed, so
 // staging costs one L2 round trip per chunk.  The loads are unconditional
 // (indices clamped into range) and every loaded value is consumed within its
@@ -80,7 +81,7 @@ __device__ __forceinline__ float sum64(float v) {
 template <int NT>
 __device__ __forceinline__ void stage_x(const float* __restrict__ X, uint32_t K,
                                         float* xs, float* bsum) {
-  constexpr uint32_t U = NT >= 1024 ? 4 : 8;  // one round up to K = 16384 (NT 1024) / 8192
+  constexpr uint32_t U = 8;  // float4 per thread per round
   const uint32_t n4 = K >> 2;
   const float4* X4 = reinterpret_cast<const float4*>(X);
   for (uint32_t base = 0; base < n4; base += NT * U) {
@@ -103,7 +104,6 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ X, uint32_t K,
       if (i < n4 && (i & 7) == 0) bsum[i >> 3] = s;
     }
   }
-  __syncthreads();
 }
 
 // Nibble/byte masks go through an opaque v_and_b32: when the compiler sees
@@ -250,8 +250,9 @@ __host__ __device__ constexpr uint32_t pro_extra_floats() { return 64; }
 template <int NT, bool NORMED>
 __device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs, float* bsum,
                                             float* ext) {
-  if (!NORMED || p.mode == 0) {
+  if (p.mode == 0) {
     stage_x<NT>(p.x, K, xs, bsum);
+    __syncthreads();
     return;
   }
   const uint32_t n4 = K >> 2;
@@ -728,13 +729,31 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
     return (size_t)row * row_bytes + (size_t)g * F::kGroupBytes;
   };
 
-  // The first D items' weight loads go out before x is staged, so the x
-  // round trip through L2 overlaps the weight latency.
+  // Plain streams: the first NS threads stage x while the others' first D
+  // weight loads are already in flight, then issue their own.  A wave's
+  // loads complete in order, so x loads issued behind its own weight loads
+  // would wait for them; the barrier does not wait for outstanding loads.
+  // Normed streams: the whole block runs the prologue (its reductions need
+  // every thread), behind every wave's first loads.
+  constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
+  const bool late = !NORMED && threadIdx.x < NS;
   typename F::Item buf[D];
+  if (!late) {
 #pragma unroll
-  for (int d = 0; d < D; d++)
-    if (d < n_items) F::load(buf[d], a, offset_of(d));
-  stage_x_pro<NT, NORMED>(xp, K, xs, bsum, ext);
+    for (int d = 0; d < D; d++)
+      if (d < n_items) F::load(buf[d], a, offset_of(d));
+  }
+  if constexpr (NORMED) {
+    stage_x_pro<NT, NORMED>(xp, K, xs, bsum, ext);
+  } else {
+    if (late) stage_x<NS>(xp.x, K, xs, bsum);
+    __syncthreads();
+    if (late) {
+#pragma unroll
+      for (int d = 0; d < D; d++)
+        if (d < n_items) F::load(buf[d], a, offset_of(d));
+    }
+  }
   typename F::Acc acc;
   F::init(acc);
 #pragma unroll 1

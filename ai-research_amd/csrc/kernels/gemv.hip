@@ -247,31 +247,55 @@ __host__ __device__ constexpr uint32_t pro_extra_floats() { return 64; }
 // so the four sums go through one reduction.  Only if that expansion
 // cancels (the total below 1e-3 of its positive terms) is sum(xn^2)
 // reduced directly from xn, as a second pass.
-template <int NT, bool NORMED>
-__device__ __forceinline__ void stage_x_pro(const XPro& p, uint32_t K, float* xs, float* bsum,
-                                            float* ext) {
-  if (p.mode == 0) {
-    stage_x<NT>(p.x, K, xs, bsum);
+// The prologue's inputs (float4 slices of x, r, wr and w per thread).
+struct ProIn {
+  float4 vx[PRO_U], vr[PRO_U], vwr[PRO_U], vw[PRO_U];
+};
+
+// Issue every load of the prologue, unconditionally (clamped indices; x
+// stands in for the vectors a mode does not read), so they can go out
+// before the stream's first weight loads and complete first.
+template <int NT>
+__device__ __forceinline__ void pro_load(const XPro& p, uint32_t K, ProIn& in) {
+  const uint32_t n4 = K >> 2;
+  const bool add = p.mode == 2;
+  const float4* x = reinterpret_cast<const float4*>(p.x);
+  const float4* w = reinterpret_cast<const float4*>(p.mode >= 1 ? p.w : p.x);
+  const float4* r = reinterpret_cast<const float4*>(add ? p.r : p.x);
+  const float4* wr = reinterpret_cast<const float4*>(add && p.wr ? p.wr : p.x);
+#pragma unroll
+  for (uint32_t u = 0; u < PRO_U; u++) {
+    uint32_t i = u * NT + threadIdx.x;
+    i = i < n4 ? i : n4 - 1;
+    in.vx[u] = x[i];
+    in.vw[u] = w[i];
+    in.vr[u] = r[i];
+    in.vwr[u] = wr[i];
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void pro_finish(const XPro& p, uint32_t K, ProIn& in, float* xs,
+                                           float* bsum, float* ext) {
+  const uint32_t n4 = K >> 2;
+  float4* vx = in.vx;
+  const float4* vr = in.vr;
+  const float4* vwr = in.vwr;
+  const float4* vw = in.vw;
+  if (p.mode == 0) {  // x as given
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++) {
+      const uint32_t i = u * NT + threadIdx.x;
+      const uint32_t e = i << 2, g = e >> 7, o = e & 127;
+      if (i < n4) *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = vx[u];
+      const float s = sum8((vx[u].x + vx[u].y) + (vx[u].z + vx[u].w));
+      if (i < n4 && (i & 7) == 0) bsum[i >> 3] = s;
+    }
     __syncthreads();
     return;
   }
-  const uint32_t n4 = K >> 2;
   const bool add = p.mode == 2;
   const bool has_wr = p.wr != nullptr;
-  // one round trip: every load of the prologue is issued before any is used
-  float4 vx[PRO_U], vr[PRO_U], vwr[PRO_U], vw[PRO_U];
-#pragma unroll
-  for (uint32_t u = 0; u < PRO_U; u++) {
-    const uint32_t i = u * NT + threadIdx.x;
-    if (i < n4) {
-      vx[u] = reinterpret_cast<const float4*>(p.x)[i];
-      vw[u] = reinterpret_cast<const float4*>(p.w)[i];
-      if (add) {
-        vr[u] = reinterpret_cast<const float4*>(p.r)[i];
-        if (has_wr) vwr[u] = reinterpret_cast<const float4*>(p.wr)[i];
-      }
-    }
-  }
   float inv;
   if (add) {
     float t[4] = {0.f, 0.f, 0.f, 0.f};  // sum r^2, x^2, x q, q^2
@@ -729,23 +753,28 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
     return (size_t)row * row_bytes + (size_t)g * F::kGroupBytes;
   };
 
-  // Plain streams: the first NS threads stage x while the others' first D
-  // weight loads are already in flight, then issue their own.  A wave's
-  // loads complete in order, so x loads issued behind its own weight loads
-  // would wait for them; the barrier does not wait for outstanding loads.
-  // Normed streams: the whole block runs the prologue (its reductions need
-  // every thread), behind every wave's first loads.
-  constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
-  const bool late = !NORMED && threadIdx.x < NS;
+  // A wave's loads complete in order, so x loads issued behind its own
+  // weight loads would wait for them (barriers do not wait for outstanding
+  // loads).  Plain streams: the first NS threads stage x while the others'
+  // first D weight loads are already in flight, then issue their own.
+  // Normed streams: every thread issues the prologue's loads first, then its
+  // weight loads, then runs the prologue (its reductions need every thread).
   typename F::Item buf[D];
-  if (!late) {
+  if constexpr (NORMED) {
+    ProIn pin;
+    pro_load<NT>(xp, K, pin);
 #pragma unroll
     for (int d = 0; d < D; d++)
       if (d < n_items) F::load(buf[d], a, offset_of(d));
-  }
-  if constexpr (NORMED) {
-    stage_x_pro<NT, NORMED>(xp, K, xs, bsum, ext);
+    pro_finish<NT>(xp, K, pin, xs, bsum, ext);
   } else {
+    constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
+    const bool late = threadIdx.x < NS;
+    if (!late) {
+#pragma unroll
+      for (int d = 0; d < D; d++)
+        if (d < n_items) F::load(buf[d], a, offset_of(d));
+    }
     if (late) stage_x<NS>(xp.x, K, xs, bsum);
     __syncthreads();
     if (late) {

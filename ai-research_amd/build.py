@@ -25,6 +25,10 @@ DEVICE_FLAGS = ["--offload-arch=gfx950", "--genco", "--no-gpu-bundle-output", "-
 
 KERNEL_FAMILIES = ["gemv", "gemv_norm", "util", "attn", "norm", "prefill"]
 
+# Per-family extra flags.  The prefill GEMMs scale each 32-block's MFMA sum on
+# the VALU; in VGPR form the MFMA results need no v_accvgpr_read first.
+FAMILY_FLAGS = {"prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 HOST_SOURCES = ["runtime.cpp", "engine.cpp", "model.cpp", "ring.cpp"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-pthread", "-ffp-contract=off",
               "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
@@ -51,7 +55,7 @@ def build_kernels():
         if not os.path.exists(src):
             continue
         out = os.path.join(PKG, "gh_%s.hsaco" % fam)
-        jobs.append([HIPCC] + DEVICE_FLAGS + [src, "-o", out])
+        jobs.append([HIPCC] + DEVICE_FLAGS + FAMILY_FLAGS.get(fam, []) + [src, "-o", out])
     with ThreadPoolExecutor(max_workers=min(8, max(1, len(jobs)))) as ex:
         list(ex.map(_run, jobs))
 

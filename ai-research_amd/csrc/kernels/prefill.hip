@@ -11,8 +11,12 @@
 //  * weights enter exactly: the MFMA B operand is the integer n - 8 (Q4) or
 //    q (Q8), exact in fp16, and each 32-block's f32 scale d is applied to the
 //    block's fp32 partial sum (acc += d * block_sum), as the GEMV does;
-//  * activations are split a = hi + lo with hi = fp16(a), lo = fp16(a - hi),
-//    and both halves go through the MFMA (22+ significant bits of a);
+//  * activations are split a = s (hi + lo) with hi = fp16(a / s),
+//    lo = fp16(a / s - hi) and s a power of two per row that puts the row's
+//    largest |a| / s in [2^13, 2^14) (no fp16 overflow for any row), and both
+//    halves go through the MFMA (22+ significant bits of a).  The split is
+//    made once per row by gh_pf_halves_k, not in every tile that reads the
+//    row, and s is applied in the epilogue (exact: a power of two);
 //  * accumulation is fp32.
 //
 // Tiling: a workgroup of 256 threads (2 x 2 wavefronts) owns a BM x BN tile
@@ -80,26 +84,29 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
-// NMAT = 1: C = A W^T.  NMAT = 2: C = gelu_tanh(A Wg^T) * (A Wu^T).  A, C f32.
+// NMAT = 1: C = A W^T.  NMAT = 2: C = gelu_tanh(A Wg^T) * (A Wu^T).  A as its
+// fp16 hi/lo planes Ah, Al ([T][K]) and row scales rs; C f32.
 // Each step covers KB quant blocks (32 KB elements of K).
 // SPLIT (split-K, for few tiles): workgroup z of gridDim.z runs K steps
 // [z S / Z, (z + 1) S / Z) and writes its raw sums to C as partial plane
 // (z, matrix) of [Z][NMAT][T][N]; gh_pf_splitk_k adds the planes in z order
 // and applies the epilogue.
 template <class F, int BM, int BN, int NMAT, int KB, bool SPLIT>
-__device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
+__device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
+                                          const _Float16* __restrict__ Al,
+                                          const float* __restrict__ rs,
                                           const uint8_t* __restrict__ W0,
                                           const uint8_t* __restrict__ W1, float* __restrict__ C,
                                           uint32_t T, uint32_t N, uint32_t K) {
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave in M and N
   constexpr int BK = 32 * KB;
   constexpr int LS = BK + 8;                 // LDS row stride in halves (+8: bank spread)
-  constexpr int A_PER = BM * (BK / 4) / PF_NT;               // float4 A chunks per thread
+  constexpr int A_PER = BM * (BK / 8) / PF_NT;               // 16-B chunks per plane and thread
   constexpr int B_ROWS = NMAT * BN;                          // weight rows per step
   constexpr int B_HALVES = 2 * KB * B_ROWS;                  // 16-element half-blocks
   constexpr int B_PER = (B_HALVES + PF_NT - 1) / PF_NT;
-  static_assert(A_PER >= 1 && (BM * (BK / 4)) % PF_NT == 0, "A chunks divide the workgroup");
-  __shared__ _Float16 Ah[BM * LS], Al[BM * LS];
+  static_assert(A_PER >= 1 && (BM * (BK / 8)) % PF_NT == 0, "A chunks divide the workgroup");
+  __shared__ _Float16 Sh[BM * LS], Sl[BM * LS];
   __shared__ _Float16 Bs[B_ROWS * LS];
   __shared__ float Ds[B_ROWS * KB];
 
@@ -111,17 +118,18 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
 
   // global -> register staging of one K step (blocks past K load block nb - 1
   // and are multiplied by a zero scale)
-  float4 ra[A_PER];
+  uint4 rah[A_PER], ral[A_PER];
   uint32_t rb[B_PER][F::kWords];
   auto load_step = [&](uint32_t step) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      const uint32_t c = tid + i * PF_NT;  // row c / (BK/4), float4 c % (BK/4)
-      uint32_t r = m0 + c / (BK / 4);
+      const uint32_t c = tid + i * PF_NT;  // row c / (BK/8), 8 halves c % (BK/8)
+      uint32_t r = m0 + c / (BK / 8);
       r = r < T ? r : T - 1;
-      uint32_t k = step * BK + 4 * (c % (BK / 4));
-      k = k < K ? k : K - 4;
-      ra[i] = *reinterpret_cast<const float4*>(A + (size_t)r * K + k);
+      uint32_t k = step * BK + 8 * (c % (BK / 8));
+      k = k < K ? k : K - 8;
+      rah[i] = *reinterpret_cast<const uint4*>(Ah + (size_t)r * K + k);
+      ral[i] = *reinterpret_cast<const uint4*>(Al + (size_t)r * K + k);
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -141,17 +149,9 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
       const uint32_t c = tid + i * PF_NT;
-      const float v[4] = {ra[i].x, ra[i].y, ra[i].z, ra[i].w};
-      typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-      half4 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        hi[e] = (_Float16)v[e];
-        lo[e] = (_Float16)(v[e] - (float)hi[e]);
-      }
-      const uint32_t o = (c / (BK / 4)) * LS + 4 * (c % (BK / 4));
-      *reinterpret_cast<half4*>(&Ah[o]) = hi;
-      *reinterpret_cast<half4*>(&Al[o]) = lo;
+      const uint32_t o = (c / (BK / 8)) * LS + 8 * (c % (BK / 8));
+      *reinterpret_cast<uint4*>(&Sh[o]) = rah[i];
+      *reinterpret_cast<uint4*>(&Sl[o]) = ral[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -194,8 +194,8 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           const uint32_t o = (wm + 32 * i + lane % 32) * LS + 32 * kq + 16 * h + 8 * (lane / 32);
-          ah[h][i] = *reinterpret_cast<const half8*>(&Ah[o]);
-          al[h][i] = *reinterpret_cast<const half8*>(&Al[o]);
+          ah[h][i] = *reinterpret_cast<const half8*>(&Sh[o]);
+          al[h][i] = *reinterpret_cast<const half8*>(&Sl[o]);
         }
 #pragma unroll
       for (int q = 0; q < NMAT; q++)
@@ -231,46 +231,53 @@ __device__ __forceinline__ void gemm_tile(const float* __restrict__ A,
       for (int r = 0; r < 16; r++) {
         const uint32_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
         if (row < T && col < N) {
+          const float sr = rs[row];
           if constexpr (SPLIT) {
 #pragma unroll
             for (int q = 0; q < NMAT; q++)
-              C[((size_t)(z * NMAT + q) * T + row) * N + col] = acc[q][i][j][r];
+              C[((size_t)(z * NMAT + q) * T + row) * N + col] = acc[q][i][j][r] * sr;
           } else if constexpr (NMAT == 1) {
-            C[(size_t)row * N + col] = acc[0][i][j][r];
+            C[(size_t)row * N + col] = acc[0][i][j][r] * sr;
           } else {
-            C[(size_t)row * N + col] = gelu_tanh(acc[0][i][j][r]) * acc[1][i][j][r];
+            C[(size_t)row * N + col] = gelu_tanh(acc[0][i][j][r] * sr) * (acc[1][i][j][r] * sr);
           }
         }
       }
     }
 }
 
-#define GH_GEMM(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                   \
-  extern "C" __global__ __launch_bounds__(PF_NT) void NAME##_k##KB##SUFFIX(                \
-      const float* A, const uint8_t* W, float* C, uint32_t T, uint32_t N, uint32_t K) {    \
-    gemm_tile<F, BM, BN, 1, KB, SPLIT>(A, W, W, C, T, N, K);                           \
+#define GH_GEMM(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                       \
+  extern "C" __global__ __launch_bounds__(PF_NT) GH_PF_OCC_##BM void NAME##_k##KB##SUFFIX( \
+      const _Float16* Ah, const _Float16* Al, const float* rs, const uint8_t* W, float* C,  \
+      uint32_t T, uint32_t N, uint32_t K) {                                                \
+    gemm_tile<F, BM, BN, 1, KB, SPLIT>(Ah, Al, rs, W, W, C, T, N, K);                          \
   }
-#define GH_GEMM_PAIR(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                              \
-  extern "C" __global__ __launch_bounds__(PF_NT) void NAME##_k##KB##SUFFIX(                \
-      const float* A, const uint8_t* Wg, const uint8_t* Wu, float* Act, uint32_t T,        \
-      uint32_t N, uint32_t K) {                                                            \
-    gemm_tile<F, BM, BN, 2, KB, SPLIT>(A, Wg, Wu, Act, T, N, K);                       \
+#define GH_GEMM_PAIR(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                  \
+  extern "C" __global__ __launch_bounds__(PF_NT) GH_PF_OCC_##BM void NAME##_k##KB##SUFFIX( \
+      const _Float16* Ah, const _Float16* Al, const float* rs, const uint8_t* Wg,          \
+      const uint8_t* Wu, float* Act, uint32_t T, uint32_t N, uint32_t K) {                 \
+    gemm_tile<F, BM, BN, 2, KB, SPLIT>(Ah, Al, rs, Wg, Wu, Act, T, N, K);                      \
   }
-#define GH_GEMM_ALL(KB)                                                   \
-  GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, KB, false, )            \
-  GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, KB, false, )                \
-  GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, KB, false, )            \
-  GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, KB, false, )                \
-  GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, KB, false, )       \
-  GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, KB, false, )         \
-  GH_GEMM_PAIR(gh_pf_gateup_q8_m128_n64, Q8W, 128, 64, KB, false, )       \
-  GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, KB, false, )
+// The 128-row tiles are held to 2 waves per SIMD: at 3 (the register count
+// allows it) they measured ~2x slower, the third workgroup's tiles evicting
+// the first two's operands.
+#define GH_PF_OCC_128 __attribute__((amdgpu_waves_per_eu(1, 2)))
+#define GH_PF_OCC_64
+#define GH_GEMM_ALL                                                       \
+  GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, 1, false, )             \
+  GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, 1, false, )                 \
+  GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, 1, false, )             \
+  GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, false, )                 \
+  GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, 1, false, )        \
+  GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, false, )          \
+  GH_GEMM_PAIR(gh_pf_gateup_q8_m128_n64, Q8W, 128, 64, 1, false, )        \
+  GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, 1, false, )
 
 // One quant block per K step measured fastest (12B prefill 62.7 ms vs 65.9
-// and 68.4 ms at 2 and 4 blocks): the step is bound by the per-block scale
-// FMAs and operand conversions, not by load latency.
-GH_GEMM_ALL(1)
-GH_GEMM_ALL(2)
+// and 68.4 ms at 2 and 4 blocks), and loading 2 or 3 steps ahead in a
+// register ring slower (72-77 ms vs 64): the step is bound by its barriers
+// and MFMA dependency chains, not by load latency.
+GH_GEMM_ALL
 
 // Split-K forms of the small tile, for batches whose tiles alone cannot
 // fill the CUs (a few prompt tokens): without them each workgroup walks all
@@ -279,6 +286,65 @@ GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
+
+// The row scale of the GEMM's A operand for a row whose largest |x| is m:
+// s = 2^(e - 14) with 2^(e-1) <= m < 2^e (1 for m = 0), so every |x| / s
+// < 2^14 fits fp16; returns s and sets *inv = 1 / s (both exact).
+__device__ __forceinline__ float row_scale(float m, float* inv) {
+  int e = 0;
+  if (m > 0.f) frexpf(m, &e);
+  const int sh = m > 0.f ? e - 14 : 0;
+  *inv = ldexpf(1.f, -sh);
+  return ldexpf(1.f, sh);
+}
+
+// The MFMA A operand of one f32 row (K <= PF_HALVES_K): hi = fp16(a / s),
+// lo = fp16(a / s - hi) with s = row_scale(max|a|).  One workgroup per row;
+// rs[t] = s.
+#define PF_HALVES_NT 1024
+#define PF_HALVES_U 4
+#define PF_HALVES_K (4 * PF_HALVES_NT * PF_HALVES_U)
+extern "C" __global__ __launch_bounds__(PF_HALVES_NT) void gh_pf_halves_k(
+    const float* __restrict__ A, _Float16* __restrict__ Ah, _Float16* __restrict__ Al,
+    float* __restrict__ rs, uint32_t K) {
+  __shared__ float red[PF_HALVES_NT / 64];
+  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, n4 = K / 4;
+  const float4* a = reinterpret_cast<const float4*>(A + (size_t)t * K);
+  float4 v[PF_HALVES_U];
+  float m = 0.f;
+#pragma unroll
+  for (int u = 0; u < PF_HALVES_U; u++) {
+    const uint32_t i = tid + u * PF_HALVES_NT;
+    v[u] = a[i < n4 ? i : n4 - 1];
+    if (i < n4) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = 0.f;
+#pragma unroll
+  for (int w = 0; w < PF_HALVES_NT / 64; w++) m = fmaxf(m, red[w]);
+  float inv;
+  const float sc = row_scale(m, &inv);
+#pragma unroll
+  for (int u = 0; u < PF_HALVES_U; u++) {
+    const uint32_t i = tid + u * PF_HALVES_NT;
+    if (i < n4) {
+      const float x[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
+      half4 hi, lo;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        hi[k] = (_Float16)x[k];
+        lo[k] = (_Float16)(x[k] - (float)hi[k]);
+      }
+      *reinterpret_cast<half4*>(Ah + (size_t)t * K + 4 * i) = hi;
+      *reinterpret_cast<half4*>(Al + (size_t)t * K + 4 * i) = lo;
+    }
+  }
+  if (tid == 0) rs[t] = sc;
+}
 
 // C[T][N] from the Z partial planes of a split-K GEMM, added in z order (so
 // the result does not depend on scheduling): the plain sum (nmat 1) or
@@ -325,10 +391,25 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 
 // Every load (x, r, wr, w) is issued before any is used, with clamped
 // indices and stand-in pointers for the operands a mode does not read, so
-// the row costs one global round trip rather than one per operand.
+// the row costs one global round trip rather than one per operand.  The
+// normed row goes out as the GEMM's A operand: fp16 hi/lo planes Xh, Xl
+// ([T][H]) and the row scale rs[t], as gh_pf_halves_k makes them.
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; w++) t = fmaxf(t, red[w]);
+  __syncthreads();
+  return t;
+}
+
 extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
-    float* X, const float* R, const float* wr, const float* w, float* Xn, uint32_t H,
-    float s, float eps, uint32_t mode) {
+    float* X, const float* R, const float* wr, const float* w, _Float16* Xh, _Float16* Xl,
+    float* rs, uint32_t H, float s, float eps, uint32_t mode) {
   __shared__ float red[PF_NORM_NT / 64];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   const bool add = mode == 2, has_wr = wr != nullptr;
@@ -364,9 +445,23 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
   for (int u = 0; u < PF_ROW_MAX; u++)
     if (tid + u * PF_NORM_NT < H) ss += v[u] * v[u];
   const float inv = 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps);
+  float m = 0.f;
+#pragma unroll
+  for (int u = 0; u < PF_ROW_MAX; u++) {
+    v[u] = v[u] * inv * wv[u];
+    if (tid + u * PF_NORM_NT < H) m = fmaxf(m, fabsf(v[u]));
+  }
+  float sinv;
+  const float sc = row_scale(block_max<PF_NORM_NT>(m, red), &sinv);
 #pragma unroll
   for (int u = 0; u < PF_ROW_MAX; u++) {
     const uint32_t i = tid + u * PF_NORM_NT;
-    if (i < H) Xn[(size_t)t * H + i] = v[u] * inv * wv[u];
+    if (i < H) {
+      const float y = v[u] * sinv;
+      const _Float16 hi = (_Float16)y;
+      Xh[(size_t)t * H + i] = hi;
+      Xl[(size_t)t * H + i] = (_Float16)(y - (float)hi);
+    }
   }
+  if (tid == 0) rs[t] = sc;
 }

@@ -310,27 +310,29 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
   return ctx->launch("gh_attn_merge_k", dim3(L.args.nq), dim3(256), 0, args);
 }
 
-gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
-                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K) {
+gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
+                                    const void* W1, const void* Ah, const void* Al,
+                                    const float* rs, float* C, uint32_t T, uint32_t N, uint32_t K) {
   if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
     return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4 or Q8");
-  if (!W0 || !A || !C || T == 0 || N == 0 || K == 0)
+  if (!W0 || !Ah || !Al || !rs || !C || T == 0 || N == 0 || K == 0)
     return fail(GH_ERR_INVALID, "prefill GEMM: null pointer or zero size");
   if (K % 32 != 0) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K must be a multiple of 32");
-  if ((reinterpret_cast<uintptr_t>(A) & 15) || (reinterpret_cast<uintptr_t>(W0) & 3) ||
+  if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
+  if ((reinterpret_cast<uintptr_t>(Ah) & 15) || (reinterpret_cast<uintptr_t>(Al) & 15) ||
+      (reinterpret_cast<uintptr_t>(W0) & 3) ||
       (W1 && (reinterpret_cast<uintptr_t>(W1) & 3)))
-    return fail(GH_ERR_INVALID, "prefill GEMM: A must be 16-byte and W 4-byte aligned");
+    return fail(GH_ERR_INVALID, "prefill GEMM: A planes must be 16-byte and W 4-byte aligned");
   const bool pair = W1 != nullptr;
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup
   const uint32_t bn_big = pair ? 64 : 128;
   const bool big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128) >= cus;
   const uint32_t bm = big ? 128 : 64, bn = big ? bn_big : 64;
-  int kb = 1;  // quant blocks per K step (tuning: GH_PF_KB=2)
-  if (const char* env = getenv("GH_PF_KB")) kb = atoi(env) == 2 ? 2 : 1;
   std::string name = std::string(pair ? "gh_pf_gateup_" : "gh_pf_gemm_") +
                      (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
-                     std::to_string(bn) + "_k" + std::to_string(kb);
+                     std::to_string(bn) + "_k1";
+
   dim3 grid((N + bn - 1) / bn, (T + bm - 1) / bm);
   // Split K when the tiles alone leave CUs idle: about two workgroups per CU,
   // at least 8 K steps per split (GH_PF_SPLIT=n forces n, 1 disables).
@@ -354,10 +356,12 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   }
   gh_status st;
   if (pair) {
-    void* args[] = {&A, const_cast<void**>(&W0), const_cast<void**>(&W1), &out, &T, &N, &K};
+    void* args[] = {const_cast<void**>(&Ah), const_cast<void**>(&Al), const_cast<float**>(&rs),
+                    const_cast<void**>(&W0), const_cast<void**>(&W1), &out, &T, &N, &K};
     st = ctx->launch(name, grid, dim3(256), 0, args);
   } else {
-    void* args[] = {&A, const_cast<void**>(&W0), &out, &T, &N, &K};
+    void* args[] = {const_cast<void**>(&Ah), const_cast<void**>(&Al), const_cast<float**>(&rs),
+                    const_cast<void**>(&W0), &out, &T, &N, &K};
     st = ctx->launch(name, grid, dim3(256), 0, args);
   }
   if (st != GH_OK || nz == 1) return st;
@@ -365,6 +369,27 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   const unsigned rgrid = (unsigned)std::min<uint64_t>((tn + 255) / 256, 4ull * cus);
   void* rargs[] = {&out, &C, &T, &N, &nz, const_cast<uint32_t*>(&nmat)};
   return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
+}
+
+// f32 A: split into fp16 hi/lo planes with a power-of-two scale per row
+// (gh_pf_halves_k, once per row rather than in every tile that reads it),
+// then the GEMM.
+gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
+                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K) {
+  if (!A || T == 0 || K == 0 || K % 32 != 0) return fail(GH_ERR_INVALID, "prefill GEMM: bad A");
+  if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
+  if (reinterpret_cast<uintptr_t>(A) & 15) return fail(GH_ERR_INVALID, "prefill GEMM: A must be 16-byte aligned");
+  const size_t plane = (size_t)T * K * 2;
+  gh_status st = ctx->ensure_zeroed(&ctx->half_scratch, &ctx->half_scratch_bytes,
+                                    2 * plane + (size_t)T * sizeof(float));
+  if (st != GH_OK) return st;
+  char* hb = static_cast<char*>(ctx->half_scratch);
+  void* Ah = hb;
+  void* Al = hb + plane;
+  float* rs = reinterpret_cast<float*>(hb + 2 * plane);
+  void* args[] = {const_cast<float**>(&A), &Ah, &Al, &rs, &K};
+  if ((st = ctx->launch("gh_pf_halves_k", dim3(T), dim3(1024), 0, args)) != GH_OK) return st;
+  return launch_prefill_gemm_split(ctx, mode, W0, W1, Ah, Al, rs, C, T, N, K);
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {

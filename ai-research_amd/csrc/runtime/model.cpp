@@ -67,6 +67,7 @@ struct gh_model {
   uint8_t* pf_arena = nullptr;
   float *pf_x = nullptr, *pf_qkv = nullptr, *pf_o = nullptr, *pf_m = nullptr;
   float *pf_xn = nullptr, *pf_attn = nullptr, *pf_act = nullptr;
+  float* pf_rs = nullptr;  // row scales of the normed rows (pf_xn holds their fp16 hi/lo planes)
   uint32_t *pf_meta = nullptr, *pf_active = nullptr;
 
   template <typename T>
@@ -709,7 +710,7 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   const size_t o_o = take((size_t)T * H * 4), o_m = take((size_t)T * H * 4);
   const size_t o_xn = take((size_t)T * H * 4), o_attn = take((size_t)T * m->max_q * 4);
   const size_t o_act = take((size_t)T * I * 4), o_meta = take((size_t)3 * T * 4);
-  const size_t o_active = take((size_t)T * stride * 4);
+  const size_t o_active = take((size_t)T * stride * 4), o_rs = take((size_t)T * 4);
   if (m->pf_arena) {
     hipStreamSynchronize(m->ctx->stream);
     hipFree(m->pf_arena);
@@ -729,6 +730,7 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   m->pf_act = f32(o_act);
   m->pf_meta = u32(o_meta);
   m->pf_active = u32(o_active);
+  m->pf_rs = f32(o_rs);
   m->pf_cap = T;
   m->pf_stride = stride;
   return GH_OK;
@@ -740,9 +742,12 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   uint32_t H = m->cfg.hidden_size;
   float eps = m->cfg.rms_norm_eps;
   float* X = m->pf_x;
-  float* Xn = m->pf_xn;
+  // the normed rows as the GEMM's A operand: fp16 hi/lo planes in pf_xn
+  uint16_t* Xh = reinterpret_cast<uint16_t*>(m->pf_xn);
+  uint16_t* Xl = Xh + (size_t)T * H;
+  float* rs = m->pf_rs;
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
-                  &Xn, &H, &s, &eps, &mode};
+                  &Xh, &Xl, &rs, &H, &s, &eps, &mode};
   return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
 }
 
@@ -766,8 +771,10 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     }
     if (st != GH_OK) return st;
     // 2. [q|k|v] rows of every token
-    if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.qkv), nullptr, m->pf_xn,
-                                      m->pf_qkv, T, L.qkv_rows, H)) != GH_OK)
+    const uint16_t* xh = reinterpret_cast<const uint16_t*>(m->pf_xn);
+    if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.qkv), nullptr, xh,
+                                            xh + (size_t)T * H, m->pf_rs, m->pf_qkv, T, L.qkv_rows,
+                                            H)) != GH_OK)
       return st;
     // 3. q/k norm + RoPE in place, K/V into the caches, then attention
     AttnArgs a{};
@@ -813,8 +820,9 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
                              L.post_attn == kNone ? nullptr : m->at<float>(L.post_attn),
                              m->at<float>(L.pre_ffn), 1.0f, 2)) != GH_OK)
       return st;
-    if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.gate), m->at<uint8_t>(L.up),
-                                      m->pf_xn, m->pf_act, T, I, H)) != GH_OK)
+    if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.gate),
+                                            m->at<uint8_t>(L.up), xh, xh + (size_t)T * H,
+                                            m->pf_rs, m->pf_act, T, I, H)) != GH_OK)
       return st;
     // 6. m = W_down . act
     if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.down), nullptr, m->pf_act,

@@ -136,6 +136,7 @@ gh_context::~gh_context() {
     if (attn_scratch) hipFree(attn_scratch);
     if (argmax_scratch) hipFree(argmax_scratch);
     if (gemm_scratch) hipFree(gemm_scratch);
+    if (half_scratch) hipFree(half_scratch);
     hipStreamDestroy(stream);
   }
   for (hipModule_t m : modules) hipModuleUnload(m);

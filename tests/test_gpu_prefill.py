@@ -53,6 +53,29 @@ def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     assert_close(got, ref, what="prefill GeGLU")
 
 
+def test_prefill_gemm_row_range(gpu):
+    # rows far outside fp16 range (1e6, 1e-7), a zero row and mixed magnitudes
+    # within a row: the per-row power-of-two scale keeps every row exact to
+    # the tolerance
+    T, N, K = 6, 128, 512
+    wq, deq = quantized(N, K, gh.QUANT_Q4, 330)
+    a = gh.synth_normal(T * K, 1, 331, 0.0, 1.0).reshape(T, K).astype(np.float64)
+    a[0] *= 1e6
+    a[1] *= 1e-7
+    a[2] = 0.0
+    a[3, ::2] *= 1e4
+    a = a.astype(np.float32)
+    W, A, C = gpu.upload(wq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gemm(gh.QUANT_Q4, W, A, C, T, N, K)
+    got = C.read(np.float32, T * N).reshape(T, N)
+    ref = np.asarray(a, np.float64) @ deq.T
+    for t in range(T):
+        if t == 2:
+            assert np.all(got[t] == 0.0)
+        else:
+            assert_close(got[t], ref[t], what="prefill GEMM row %d" % t)
+
+
 @pytest.mark.parametrize("pair", [False, True])
 @pytest.mark.parametrize("split", ["1", "3", "200"])
 def test_prefill_split_k(gpu, monkeypatch, pair, split):

@@ -279,11 +279,15 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
 // and MFMA dependency chains, not by load latency.
 GH_GEMM_ALL
 
-// Split-K forms of the small tile, for batches whose tiles alone cannot
-// fill the CUs (a few prompt tokens): without them each workgroup walks all
-// of K one block per step, and that serial chain, not bandwidth, sets the time.
+// Split-K forms, for products whose tiles alone cannot fill the CUs: the
+// small tile for a few prompt tokens (without the split each workgroup walks
+// all of K one block per step, and that serial chain, not bandwidth, sets the
+// time), and the large plain tile for the narrow products of a long prompt
+// (o and down, N = 3840), which otherwise fall back to the small tile.
 GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
+GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, 1, true, _s)
+GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
 

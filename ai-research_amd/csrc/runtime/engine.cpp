@@ -325,9 +325,13 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
     return fail(GH_ERR_INVALID, "prefill GEMM: A planes must be 16-byte and W 4-byte aligned");
   const bool pair = W1 != nullptr;
   const uint32_t cus = (uint32_t)ctx->num_cus;
-  // the large tile when it still gives every CU a workgroup
+  // the large tile when it still gives every CU a workgroup, or (plain
+  // products of at least 128 tokens) when splitting K lifts it to that
   const uint32_t bn_big = pair ? 64 : 128;
-  const bool big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128) >= cus;
+  const uint32_t tiles_big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128);
+  const bool big_split = !pair && T >= 128 && tiles_big < cus && 4 * tiles_big >= cus &&
+                         getenv("GH_PF_NO_BIG_SPLIT") == nullptr;
+  const bool big = tiles_big >= cus || big_split;
   const uint32_t bm = big ? 128 : 64, bn = big ? bn_big : 64;
   std::string name = std::string(pair ? "gh_pf_gateup_" : "gh_pf_gemm_") +
                      (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
@@ -339,9 +343,10 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   const uint32_t tiles = grid.x * grid.y, nsteps = K / 32;
   uint32_t nz = 1;
   if (!big && tiles < cus) nz = std::min<uint32_t>((2 * cus + tiles - 1) / tiles, std::max(1u, nsteps / 8));
+  if (big_split) nz = std::min<uint32_t>((cus + tiles - 1) / tiles, std::max(1u, nsteps / 8));
   if (const char* env = getenv("GH_PF_SPLIT")) {
     const int v = atoi(env);
-    if (v >= 1 && !big) nz = std::min<uint32_t>((uint32_t)v, nsteps);
+    if (v >= 1 && (!big || big_split)) nz = std::min<uint32_t>((uint32_t)v, nsteps);
   }
   nz = std::min<uint32_t>(nz, 64u);
   float* out = C;

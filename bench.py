@@ -195,14 +195,15 @@ def bench_decode(ctx, n_prompt=512, n_decode=128):
             "decode_tokens_head": [int(t) for t in toks[:8]]}
 
 
-def cpu_baseline(x, host_w, budget_s=10.0):
+def cpu_baseline(x, host_w, budget_s=10.0, threads=None):
     """The oracle's restatement of the reference CPU path (src/test_q4_exec.zig
     dequant loop inside gatedMlp's 16-job row split, src/kernels.zig:100-129)
-    timed on this host over whole MLP steps."""
+    timed on this host over whole MLP steps (threads: 16 or the host's count
+    if lower, unless given)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
 
-    nt = max(1, min(16, os.cpu_count() or 1))
+    nt = threads or max(1, min(16, os.cpu_count() or 1))
     wg, wu, wd = (w.reshape(r, -1) for w, r in zip(host_w, (I, I, H)))
     orc.gated_mlp_q4(x, wg, wu, wd, nt)  # warm-up
     n, t0 = 0, time.perf_counter()
@@ -256,13 +257,16 @@ def main():
         rec = json.load(open(tpath)).get("gh_gateup_q4")
         traffic = rec["hbm_bytes"] if rec else None
 
-    cpu = None
+    cpu = cpu1 = None
     if not args.no_cpu:
         n, dt, nt = cpu_baseline(x, host_w)
         cpu = {"value": round(step_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": nt,
                "kind": "port",
                "sample": "%d full MLP steps (3840/15360 Q4_0, copy 0 of the weights) in %.1f s "
                          "with the oracle's 16-way row split" % (n, dt)}
+        n1, dt1, _ = cpu_baseline(x, host_w, budget_s=4.0, threads=1)
+        cpu1 = {"value": round(step_bytes * n1 / dt1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "sample": "%d full MLP steps in %.1f s on one thread" % (n1, dt1)}
 
     line = {
         "metric": METRIC,
@@ -291,6 +295,7 @@ def main():
                   "down_proj_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
                   "gemv_q4_8192x2048_gbs": round(gemv_gbs, 1),
                   "gemv_q4_8192x2048_us": round(gemv_us, 3),
+                  "cpu_baseline_1thread": cpu1,
                   "decode_12b": dec},
     }
     ctx.close()

@@ -24,7 +24,9 @@
 // advances one quant block (32) per step: the A slice (as hi and lo) and the
 // integer W slice with its scales go to LDS (row stride padded to 40 halves
 // so the 16-byte operand reads of 32 consecutive rows spread over all
-// banks), while the next step's global loads are already in flight.
+// banks).  Two LDS stages: while the MFMAs of step s read one, step s+1's
+// global loads are in flight and then stored into the other, one barrier
+// per step.
 //
 // MFMA 32x32x16 f16 operand layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32], e = 0..7; result
@@ -106,9 +108,11 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
   constexpr int B_HALVES = 2 * KB * B_ROWS;                  // 16-element half-blocks
   constexpr int B_PER = (B_HALVES + PF_NT - 1) / PF_NT;
   static_assert(A_PER >= 1 && (BM * (BK / 8)) % PF_NT == 0, "A chunks divide the workgroup");
-  __shared__ _Float16 Sh[BM * LS], Sl[BM * LS];
-  __shared__ _Float16 Bs[B_ROWS * LS];
-  __shared__ float Ds[B_ROWS * KB];
+  // two LDS stages: the MFMAs of step s read one while step s+1 is stored
+  // into the other, so a K step needs one barrier
+  __shared__ _Float16 Sh[2][BM * LS], Sl[2][BM * LS];
+  __shared__ _Float16 Bs[2][B_ROWS * LS];
+  __shared__ float Ds[2][B_ROWS * KB];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -145,13 +149,13 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
       }
     }
   };
-  auto store_step = [&](uint32_t step) {
+  auto store_step = [&](int sb, uint32_t step) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
       const uint32_t c = tid + i * PF_NT;
       const uint32_t o = (c / (BK / 8)) * LS + 8 * (c % (BK / 8));
-      *reinterpret_cast<uint4*>(&Sh[o]) = rah[i];
-      *reinterpret_cast<uint4*>(&Sl[o]) = ral[i];
+      *reinterpret_cast<uint4*>(&Sh[sb][o]) = rah[i];
+      *reinterpret_cast<uint4*>(&Sl[sb][o]) = ral[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -160,10 +164,10 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
         const uint32_t lr = hb / (2 * KB), kq = (hb / 2) % KB;
         _Float16 v[16];
         F::ints(rb[i], v);
-        _Float16* dst = &Bs[lr * LS + 32 * kq + 16 * (hb % 2)];
+        _Float16* dst = &Bs[sb][lr * LS + 32 * kq + 16 * (hb % 2)];
         *reinterpret_cast<half8*>(dst) = *reinterpret_cast<const half8*>(v);
         *reinterpret_cast<half8*>(dst + 8) = *reinterpret_cast<const half8*>(v + 8);
-        if (hb % 2 == 0) Ds[lr * KB + kq] = step * KB + kq < nb ? __uint_as_float(rb[i][0]) : 0.f;
+        if (hb % 2 == 0) Ds[sb][lr * KB + kq] = step * KB + kq < nb ? __uint_as_float(rb[i][0]) : 0.f;
       }
     }
   };
@@ -181,10 +185,13 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
   const uint32_t nz = SPLIT ? gridDim.z : 1u, z = SPLIT ? blockIdx.z : 0u;
   const uint32_t s_begin = (uint32_t)((uint64_t)nsteps * z / nz);
   const uint32_t s_end = (uint32_t)((uint64_t)nsteps * (z + 1) / nz);
-  if (s_begin < s_end) load_step(s_begin);
+  if (s_begin < s_end) {
+    load_step(s_begin);
+    store_step(0, s_begin);
+  }
+  __syncthreads();
   for (uint32_t step = s_begin; step < s_end; step++) {
-    store_step(step);
-    __syncthreads();
+    const int cb = (step - s_begin) & 1;
     if (step + 1 < s_end) load_step(step + 1);  // in flight through this step's MFMAs
 #pragma unroll
     for (int kq = 0; kq < KB; kq++) {
@@ -194,18 +201,19 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           const uint32_t o = (wm + 32 * i + lane % 32) * LS + 32 * kq + 16 * h + 8 * (lane / 32);
-          ah[h][i] = *reinterpret_cast<const half8*>(&Sh[o]);
-          al[h][i] = *reinterpret_cast<const half8*>(&Sl[o]);
+          ah[h][i] = *reinterpret_cast<const half8*>(&Sh[cb][o]);
+          al[h][i] = *reinterpret_cast<const half8*>(&Sl[cb][o]);
         }
 #pragma unroll
       for (int q = 0; q < NMAT; q++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
           const uint32_t brow = q * BN + wn + 32 * j + lane % 32;
-          const half8 b0 = *reinterpret_cast<const half8*>(&Bs[brow * LS + 32 * kq + 8 * (lane / 32)]);
+          const half8 b0 =
+              *reinterpret_cast<const half8*>(&Bs[cb][brow * LS + 32 * kq + 8 * (lane / 32)]);
           const half8 b1 =
-              *reinterpret_cast<const half8*>(&Bs[brow * LS + 32 * kq + 16 + 8 * (lane / 32)]);
-          const float d = Ds[brow * KB + kq];
+              *reinterpret_cast<const half8*>(&Bs[cb][brow * LS + 32 * kq + 16 + 8 * (lane / 32)]);
+          const float d = Ds[cb][brow * KB + kq];
 #pragma unroll
           for (int i = 0; i < TM; i++) {
             f32x16 blk = {};
@@ -218,7 +226,10 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
           }
         }
     }
-    __syncthreads();  // LDS is rewritten by the next step
+    if (step + 1 < s_end) store_step(cb ^ 1, step + 1);
+    // the next step reads the stage just stored, and then stores into the
+    // stage read here
+    __syncthreads();
   }
 
   // epilogue: result register r of lane l -> row 8 (r/4) + 4 (l/32) + r%4, col l % 32

@@ -850,14 +850,13 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
   GH_STREAM_KERNEL_NT(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)         \
   GH_STREAM_KERNEL_NT(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)
 
+// Depth 1 is the default everywhere; depth 2 stays for tuning (GH_GEMV_CFG).
 #if defined(GH_GEMV_NORMED)
 GH_SHAPES(GH_NORMED, 1)
 GH_SHAPES(GH_NORMED, 2)
-GH_SHAPES(GH_NORMED, 3)
 #else
 GH_SHAPES(GH_PLAIN, 1)
 GH_SHAPES(GH_PLAIN, 2)
-GH_SHAPES(GH_PLAIN, 3)
 GH_WIDE(32, 4, 1) GH_WIDE(64, 2, 1) GH_WIDE(64, 4, 1)  // depth 2 at 1024 threads spills
 
 // The token from the n block partials of a fused argmax stream: the largest

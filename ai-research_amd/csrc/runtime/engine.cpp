@@ -54,7 +54,7 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool w
     const int got = sscanf(env, "%d,%d,%d,%d,%d", &t, &g, &w, &d, &n);
     if (got >= 4 && (t == 16 || t == 32 || t == 64) && (g == 1 || g == 2 || g == 4) &&
         !(t == 16 && g > 1) && w >= 1 && w <= 32 && (uint32_t)(t * g) >= ng && d >= 1 &&
-        d <= 3 && (n == 256 || (n == 1024 && wide_ok && t * g >= 128 && d == 1))) {
+        d <= 2 && (n == 256 || (n == 1024 && wide_ok && t * g >= 128 && d == 1))) {
       c = {t, g, w, d, n};
     }
   }

@@ -49,7 +49,11 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool w
   // Long rows (the down projection, K = 15360): 1024-thread workgroups, so
   // one LDS staging of x serves 16 wavefronts; measured 11.6 vs 13.6 us.
   if (wide_ok && K >= 8192 && best_t * best_g >= 128) c = {best_t, best_g, 2, 1, 1024};
-  if (const char* env = getenv("GH_GEMV_CFG")) {  // tuning "tpr,gpl,wgs_per_cu,depth[,nt]"
+  // tuning "tpr,gpl,wgs_per_cu,depth[,nt]": GH_GEMV_CFG_<M>x<K> for one shape,
+  // else GH_GEMV_CFG for every shape it fits
+  const std::string shape_key = "GH_GEMV_CFG_" + std::to_string(M) + "x" + std::to_string(K);
+  const char* shape_env = getenv(shape_key.c_str());
+  if (const char* env = shape_env ? shape_env : getenv("GH_GEMV_CFG")) {
     int t = 0, g = 0, w = 0, d = 0, n = 256;
     const int got = sscanf(env, "%d,%d,%d,%d,%d", &t, &g, &w, &d, &n);
     if (got >= 4 && (t == 16 || t == 32 || t == 64) && (g == 1 || g == 2 || g == 4) &&
@@ -60,7 +64,6 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool w
   }
   const unsigned lds_cap = (unsigned)(ctx->max_lds / std::max(1u, x_lds_bytes(K)));
   c.wgs_per_cu = std::max(1, std::min<int>(c.wgs_per_cu, (int)lds_cap));
-  (void)M;
   return c;
 }
 

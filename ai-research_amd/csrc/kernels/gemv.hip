@@ -16,11 +16,12 @@
 //    different groups at the same offset, land on different LDS banks.
 //  * In-register dequant without per-weight int->float of a signed value:
 //      sum_j (n_j - 8) d x_j = d (sum_j n_j x_j - 8 sum_j x_j)
-//    with the per-block sum_j x_j precomputed while staging x.  Nibbles are
-//    split with two ANDs (0x0F0F0F0F / 0xF0F0F0F0); each byte converts with
-//    one v_cvt_f32_ubyte{0..3}; the high nibbles carry a factor 16 that is
-//    removed once per block (exact power-of-two scale).  Q8 flips the sign
-//    bit of each byte (q + 128) and removes 128 sum x the same way.
+//    with the per-block sum_j x_j precomputed while staging x.  Q4: masks
+//    cut each word into nibble pairs that, read as two fp16 halves, are the
+//    exact denormals n 2^-24 (or 16 n 2^-24); v_fma_mix_f32 multiplies a half
+//    by an fp32 x into an fp32 sum, and the powers of two come off once per
+//    block.  Q8 flips the sign bit of each byte (q + 128), converts it with
+//    one v_cvt_f32_ubyte{0..3} and removes 128 sum x the same way.
 //  * fp32 accumulation throughout.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -45,8 +46,9 @@ __device__ __forceinline__ u32x4 ldw(const void* p) {
   return *(gvec_ptr)(p);
 }
 
-// Cross-lane sums with DPP row operations (a few cycles each) instead of
-// __shfl_xor, which lowers to an LDS-crossbar ds_bpermute per step.  Every
+// Cross-lane sums with DPP row operations and the gfx950 permlane swaps (a
+// few cycles each) instead of __shfl_xor, which lowers to an LDS-crossbar
+// ds_bpermute per step.  Every
 // step adds a commutative pair, so all participating lanes end with the
 // same bit-identical value.
 template <int CTRL>
@@ -60,13 +62,24 @@ __device__ __forceinline__ float sum8(float v) {
   v += dpp<0x141>(v);  // row_half_mirror
   return v;
 }
+// v + (v of lane l ^ 16): v_permlane16_swap exchanges rows 1 and 3 of one
+// operand with rows 0 and 2 of the other, so with both operands = v the two
+// results hold the values of lanes l and l ^ 16 (one VALU op, no LDS).
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v + (v of lane l ^ 32), with v_permlane32_swap (halves of the wavefront)
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 // sum over the 64 lanes of the wavefront
 __device__ __forceinline__ float sum64(float v) {
   v = sum8(v);
   v += dpp<0x140>(v);  // row_mirror
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+  v = add_xor16(v);
+  return add_xor32(v);
 }
 
 // Stage x[K] into LDS (padded by group) and write the per-block sums.
@@ -121,6 +134,39 @@ __device__ __forceinline__ float ub1(uint32_t x) { return (float)((x >> 8) & 0xF
 __device__ __forceinline__ float ub2(uint32_t x) { return (float)((x >> 16) & 0xFFu); }
 __device__ __forceinline__ float ub3(uint32_t x) { return (float)(x >> 24); }
 
+// Nibble pairs as fp16 denormals: (w & 0x000F000F) read as two halves is
+// exactly (n_a 2^-24, n_b 2^-24), and v_fma_mix_f32 multiplies one half by an
+// fp32 x into an fp32 sum, so no weight needs its own conversion: 8 weights
+// cost 4 masks, 1 shift and 8 FMAs (v_cvt_f32_ubyte per weight: 2 + 8 + 8).
+// Every product and partial sum is the conversion form's times 2^-24 (exact),
+// in the same order, so the results are bit-identical to it.
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2_t nib_pair(uint32_t w, uint32_t m) {
+  return __builtin_bit_cast(h2_t, opaque_and(w, m));
+}
+// One word (elements 8k .. 8k+7, xa = x[8k..8k+3], xc = x[8k+4..8k+7]):
+// sl += 2^-24 (n0 x0 + n2 x2 + n4 x4 + n6 x6), sh += 2^-20 (n1 x1 + ... + n7 x7)
+__device__ __forceinline__ void q4_word(uint32_t w, const float4& xa, const float4& xc, float& sl,
+                                        float& sh) {
+  const uint32_t t = w >> 8;
+  const h2_t p0 = nib_pair(w, 0x000F000Fu);  // elements 0, 4
+  const h2_t p1 = nib_pair(w, 0x00F000F0u);  // 16 x elements 1, 5
+  const h2_t p2 = nib_pair(t, 0x000F000Fu);  // elements 2, 6
+  const h2_t p3 = nib_pair(t, 0x00F000F0u);  // 16 x elements 3, 7
+  sl = __builtin_fmaf((float)p0.x, xa.x, sl);
+  sh = __builtin_fmaf((float)p1.x, xa.y, sh);
+  sl = __builtin_fmaf((float)p2.x, xa.z, sl);
+  sh = __builtin_fmaf((float)p3.x, xa.w, sh);
+  sl = __builtin_fmaf((float)p0.y, xc.x, sl);
+  sh = __builtin_fmaf((float)p1.y, xc.y, sh);
+  sl = __builtin_fmaf((float)p2.y, xc.z, sl);
+  sh = __builtin_fmaf((float)p3.y, xc.w, sh);
+}
+// sum_j n_j x_j from a block's two q4_word sums
+__device__ __forceinline__ float q4_sum(float sl, float sh) {
+  return (sl + sh * 0.0625f) * 16777216.0f;
+}
+
 // sum_j n_j x_j over one Q4 block, n_j = nibble j (0..15).
 __device__ __forceinline__ float q4_nx(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                        const float* __restrict__ xb) {
@@ -128,20 +174,11 @@ __device__ __forceinline__ float q4_nx(uint32_t w0, uint32_t w1, uint32_t w2, ui
   float sl = 0.f, sh = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const uint32_t lo = opaque_and(w[k], 0x0F0F0F0Fu);  // nibbles 0,2,4,6 -> elements 8k+0,2,4,6
-    const uint32_t hi = opaque_and(w[k], 0xF0F0F0F0u);  // 16 x nibbles 1,3,5,7
     const float4 xa = *reinterpret_cast<const float4*>(xb + 8 * k);
     const float4 xc = *reinterpret_cast<const float4*>(xb + 8 * k + 4);
-    sl += ub0(lo) * xa.x;
-    sh += ub0(hi) * xa.y;
-    sl += ub1(lo) * xa.z;
-    sh += ub1(hi) * xa.w;
-    sl += ub2(lo) * xc.x;
-    sh += ub2(hi) * xc.y;
-    sl += ub3(lo) * xc.z;
-    sh += ub3(hi) * xc.w;
+    q4_word(w[k], xa, xc, sl, sh);
   }
-  return sl + sh * 0.0625f;
+  return q4_sum(sl, sh);
 }
 
 // sum_j (q_j + 128) x_j over one Q8 block given its 8 packed words.
@@ -190,8 +227,8 @@ __device__ __forceinline__ float team_sum(float v) {
   static_assert(TPR == 16 || TPR == 32 || TPR == 64, "team of 16, 32 or 64 lanes");
   v = sum8(v);
   v += dpp<0x140>(v);  // row_mirror: the two half-rows of a row of 16
-  if (TPR >= 32) v += __shfl_xor(v, 16, 64);
-  if (TPR == 64) v += __shfl_xor(v, 32, 64);
+  if (TPR >= 32) v = add_xor16(v);
+  if (TPR == 64) v = add_xor32(v);
   return v;
 }
 
@@ -432,29 +469,13 @@ __device__ __forceinline__ void q4_group_dot2(const Q4G& a, const Q4G& b, const 
     float al = 0.f, ah = 0.f, bl = 0.f, bh = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const uint32_t alo = opaque_and(wa[k], 0x0F0F0F0Fu), ahi = opaque_and(wa[k], 0xF0F0F0F0u);
-      const uint32_t blo = opaque_and(wb[k], 0x0F0F0F0Fu), bhi = opaque_and(wb[k], 0xF0F0F0F0u);
       const float4 xa = *reinterpret_cast<const float4*>(xb + 8 * k);
       const float4 xc = *reinterpret_cast<const float4*>(xb + 8 * k + 4);
-      al += ub0(alo) * xa.x;
-      ah += ub0(ahi) * xa.y;
-      al += ub1(alo) * xa.z;
-      ah += ub1(ahi) * xa.w;
-      al += ub2(alo) * xc.x;
-      ah += ub2(ahi) * xc.y;
-      al += ub3(alo) * xc.z;
-      ah += ub3(ahi) * xc.w;
-      bl += ub0(blo) * xa.x;
-      bh += ub0(bhi) * xa.y;
-      bl += ub1(blo) * xa.z;
-      bh += ub1(bhi) * xa.w;
-      bl += ub2(blo) * xc.x;
-      bh += ub2(bhi) * xc.y;
-      bl += ub3(blo) * xc.z;
-      bh += ub3(bhi) * xc.w;
+      q4_word(wa[k], xa, xc, al, ah);
+      q4_word(wb[k], xa, xc, bl, bh);
     }
     // same operation order as q4_group_dot for each matrix
-    const float sa = al + ah * 0.0625f, sb = bl + bh * 0.0625f;
+    const float sa = q4_sum(al, ah), sb = q4_sum(bl, bh);
     if (j == 0) {
       ra = u2f(A[0]) * (sa - 8.0f * bs[0]);
       rb = u2f(B[0]) * (sb - 8.0f * bs[0]);
@@ -803,6 +824,50 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
     }
   }
   F::template block_end<NT>(acc, a, ext);
+}
+
+// ------------------------------------------------------------------------
+// Long rows split in two (plain x, single-sum formats Q4Fmt / Q8Fmt): virtual
+// row 2r + h is the h-th K half of row r (contiguous in memory), one team per
+// virtual row, one group per lane, so every lane holds exactly one item and
+// the whole matrix is in flight after one issue round.  The two half-sums of
+// a row (teams 2t and 2t + 1 of one workgroup) add in LDS at the end, first
+// half first.  Not persistent: the grid is ceil(2M / TEAMS) workgroups.
+// Requires (K / 128) even and K / 256 <= TPR.
+// ------------------------------------------------------------------------
+template <class F, int TPR, int NT>
+__device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
+                                           uint32_t K) {
+  extern __shared__ float lds[];
+  const uint32_t nb = K >> 5, ng = nb >> 2, ngh = ng >> 1;
+  float* xs = lds;
+  float* bsum = lds + ng * GROUP_STRIDE;
+  float* ext = bsum + nb;
+  constexpr uint32_t TEAMS = NT / TPR;
+  static_assert(TEAMS % 2 == 0 && TEAMS <= 64, "team pairs within the epilogue space");
+  const uint32_t lr = threadIdx.x % TPR, tw = threadIdx.x / TPR;
+  const uint32_t vrow = blockIdx.x * TEAMS + tw;
+  const uint32_t vr = vrow < 2 * M ? vrow : 2 * M - 1;  // tail teams load a duplicate
+  const uint32_t g = lr < ngh ? lr : ngh - 1;
+  const size_t off = (size_t)vr * (nb >> 1) * F::kBlockBytes + (size_t)g * F::kGroupBytes;
+  typename F::Item it;
+  constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
+  const bool late = threadIdx.x < NS;
+  if (!late) F::load(it, a, off);
+  if (late) stage_x<NS>(xp.x, K, xs, bsum);
+  __syncthreads();
+  if (late) F::load(it, a, off);
+  typename F::Acc acc;
+  F::init(acc);
+  const uint32_t gx = (vr & 1) * ngh + g;
+  F::fma(acc, it, xs + gx * GROUP_STRIDE, bsum + gx * 4, lr < ngh ? 1.0f : 0.0f);
+  const float v = team_sum<TPR>(acc.s);
+  if (lr == 0) ext[tw] = v;
+  __syncthreads();
+  if (threadIdx.x < TEAMS / 2) {
+    const uint32_t row = blockIdx.x * (TEAMS / 2) + threadIdx.x;
+    if (row < M) a.Y[row] = ext[2 * threadIdx.x] + ext[2 * threadIdx.x + 1];
+  }
 }
 
 // Kernel names: gh_<family>[n]_t<TPR>_g<GPL>_d<D>; the "n" variants carry the

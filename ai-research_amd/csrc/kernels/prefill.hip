@@ -86,16 +86,23 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return 0.5f * x * (1.0f + tanhf(inner));
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The GEMM's A operand layout ("ax"): row t of K elements is 2K halves, the
+// hi halves of block b (elements 32b .. 32b+31) at 64b, their lo halves at
+// 64b + 32.  Offset of element e's hi half within its row:
+__device__ __forceinline__ uint32_t pf_ax_off(uint32_t e) { return (e >> 5) * 64 + (e & 31); }
+
 // NMAT = 1: C = A W^T.  NMAT = 2: C = gelu_tanh(A Wg^T) * (A Wu^T).  A as its
-// fp16 hi/lo planes Ah, Al ([T][K]) and row scales rs; C f32.
+// fp16 hi/lo halves interleaved per 32-element block (pf_ax: a row's K step
+// is one contiguous 128-byte segment) and row scales rs; C f32.
 // Each step covers KB quant blocks (32 KB elements of K).
 // SPLIT (split-K, for few tiles): workgroup z of gridDim.z runs K steps
 // [z S / Z, (z + 1) S / Z) and writes its raw sums to C as partial plane
 // (z, matrix) of [Z][NMAT][T][N]; gh_pf_splitk_k adds the planes in z order
 // and applies the epilogue.
 template <class F, int BM, int BN, int NMAT, int KB, bool SPLIT>
-__device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
-                                          const _Float16* __restrict__ Al,
+__device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
                                           const float* __restrict__ rs,
                                           const uint8_t* __restrict__ W0,
                                           const uint8_t* __restrict__ W1, float* __restrict__ C,
@@ -103,14 +110,16 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave in M and N
   constexpr int BK = 32 * KB;
   constexpr int LS = BK + 8;                 // LDS row stride in halves (+8: bank spread)
-  constexpr int A_PER = BM * (BK / 8) / PF_NT;               // 16-B chunks per plane and thread
+  constexpr int A_CH = 8 * KB;                               // 16-B chunks per row and step
+  constexpr int A_PER = BM * A_CH / PF_NT;                   // 16-B chunks per thread
   constexpr int B_ROWS = NMAT * BN;                          // weight rows per step
   constexpr int B_HALVES = 2 * KB * B_ROWS;                  // 16-element half-blocks
   constexpr int B_PER = (B_HALVES + PF_NT - 1) / PF_NT;
-  static_assert(A_PER >= 1 && (BM * (BK / 8)) % PF_NT == 0, "A chunks divide the workgroup");
+  static_assert(A_PER >= 1 && (BM * A_CH) % PF_NT == 0, "A chunks divide the workgroup");
   // two LDS stages: the MFMAs of step s read one while step s+1 is stored
-  // into the other, so a K step needs one barrier
-  __shared__ _Float16 Sh[2][BM * LS], Sl[2][BM * LS];
+  // into the other, so a K step needs one barrier.  SA[stage] holds the hi
+  // plane, then the lo plane, BM rows of LS halves each.
+  __shared__ _Float16 SA[2][2 * BM * LS];
   __shared__ _Float16 Bs[2][B_ROWS * LS];
   __shared__ float Ds[2][B_ROWS * KB];
 
@@ -122,18 +131,19 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
 
   // global -> register staging of one K step (blocks past K load block nb - 1
   // and are multiplied by a zero scale)
-  uint4 rah[A_PER], ral[A_PER];
+  u32x4 ra[A_PER];  // a native vector: plain loads and stores, kept in registers
   uint32_t rb[B_PER][F::kWords];
   auto load_step = [&](uint32_t step) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      const uint32_t c = tid + i * PF_NT;  // row c / (BK/8), 8 halves c % (BK/8)
-      uint32_t r = m0 + c / (BK / 8);
+      // chunk c: row c / A_CH; q = c % A_CH -> block q / 8 of the step, plane
+      // (q / 4) % 2, 8 halves at (q % 4) * 8
+      const uint32_t c = tid + i * PF_NT, q = c % A_CH;
+      uint32_t r = m0 + c / A_CH;
       r = r < T ? r : T - 1;
-      uint32_t k = step * BK + 8 * (c % (BK / 8));
-      k = k < K ? k : K - 8;
-      rah[i] = *reinterpret_cast<const uint4*>(Ah + (size_t)r * K + k);
-      ral[i] = *reinterpret_cast<const uint4*>(Al + (size_t)r * K + k);
+      uint32_t blk = step * KB + q / 8;
+      blk = blk < nb ? blk : nb - 1;
+      ra[i] = *reinterpret_cast<const u32x4*>(Ax + (size_t)r * 2 * K + (size_t)blk * 64 + 8 * (q % 8));
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -152,10 +162,9 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
   auto store_step = [&](int sb, uint32_t step) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      const uint32_t c = tid + i * PF_NT;
-      const uint32_t o = (c / (BK / 8)) * LS + 8 * (c % (BK / 8));
-      *reinterpret_cast<uint4*>(&Sh[sb][o]) = rah[i];
-      *reinterpret_cast<uint4*>(&Sl[sb][o]) = ral[i];
+      const uint32_t c = tid + i * PF_NT, q = c % A_CH;
+      const uint32_t o = ((q / 4) % 2) * BM * LS + (c / A_CH) * LS + 32 * (q / 8) + 8 * (q % 4);
+      *reinterpret_cast<u32x4*>(&SA[sb][o]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -201,8 +210,8 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
 #pragma unroll
         for (int i = 0; i < TM; i++) {
           const uint32_t o = (wm + 32 * i + lane % 32) * LS + 32 * kq + 16 * h + 8 * (lane / 32);
-          ah[h][i] = *reinterpret_cast<const half8*>(&Sh[cb][o]);
-          al[h][i] = *reinterpret_cast<const half8*>(&Sl[cb][o]);
+          ah[h][i] = *reinterpret_cast<const half8*>(&SA[cb][o]);
+          al[h][i] = *reinterpret_cast<const half8*>(&SA[cb][BM * LS + o]);
         }
 #pragma unroll
       for (int q = 0; q < NMAT; q++)
@@ -259,15 +268,15 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ah,
 
 #define GH_GEMM(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                       \
   extern "C" __global__ __launch_bounds__(PF_NT) GH_PF_OCC_##BM void NAME##_k##KB##SUFFIX( \
-      const _Float16* Ah, const _Float16* Al, const float* rs, const uint8_t* W, float* C,  \
-      uint32_t T, uint32_t N, uint32_t K) {                                                \
-    gemm_tile<F, BM, BN, 1, KB, SPLIT>(Ah, Al, rs, W, W, C, T, N, K);                          \
+      const _Float16* Ax, const float* rs, const uint8_t* W, float* C, uint32_t T,         \
+      uint32_t N, uint32_t K) {                                                            \
+    gemm_tile<F, BM, BN, 1, KB, SPLIT>(Ax, rs, W, W, C, T, N, K);                          \
   }
 #define GH_GEMM_PAIR(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                  \
   extern "C" __global__ __launch_bounds__(PF_NT) GH_PF_OCC_##BM void NAME##_k##KB##SUFFIX( \
-      const _Float16* Ah, const _Float16* Al, const float* rs, const uint8_t* Wg,          \
-      const uint8_t* Wu, float* Act, uint32_t T, uint32_t N, uint32_t K) {                 \
-    gemm_tile<F, BM, BN, 2, KB, SPLIT>(Ah, Al, rs, Wg, Wu, Act, T, N, K);                      \
+      const _Float16* Ax, const float* rs, const uint8_t* Wg, const uint8_t* Wu,           \
+      float* Act, uint32_t T, uint32_t N, uint32_t K) {                                    \
+    gemm_tile<F, BM, BN, 2, KB, SPLIT>(Ax, rs, Wg, Wu, Act, T, N, K);                      \
   }
 // The 128-row tiles are held to 2 waves per SIMD: at 3 (the register count
 // allows it) they measured ~2x slower, the third workgroup's tiles evicting
@@ -314,13 +323,13 @@ __device__ __forceinline__ float row_scale(float m, float* inv) {
 }
 
 // The MFMA A operand of one f32 row (K <= PF_HALVES_K): hi = fp16(a / s),
-// lo = fp16(a / s - hi) with s = row_scale(max|a|).  One workgroup per row;
-// rs[t] = s.
+// lo = fp16(a / s - hi) with s = row_scale(max|a|), in the ax layout
+// (pf_ax_off).  One workgroup per row; rs[t] = s.
 #define PF_HALVES_NT 1024
 #define PF_HALVES_U 4
 #define PF_HALVES_K (4 * PF_HALVES_NT * PF_HALVES_U)
 extern "C" __global__ __launch_bounds__(PF_HALVES_NT) void gh_pf_halves_k(
-    const float* __restrict__ A, _Float16* __restrict__ Ah, _Float16* __restrict__ Al,
+    const float* __restrict__ A, _Float16* __restrict__ Ax,
     float* __restrict__ rs, uint32_t K) {
   __shared__ float red[PF_HALVES_NT / 64];
   typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -354,8 +363,9 @@ extern "C" __global__ __launch_bounds__(PF_HALVES_NT) void gh_pf_halves_k(
         hi[k] = (_Float16)x[k];
         lo[k] = (_Float16)(x[k] - (float)hi[k]);
       }
-      *reinterpret_cast<half4*>(Ah + (size_t)t * K + 4 * i) = hi;
-      *reinterpret_cast<half4*>(Al + (size_t)t * K + 4 * i) = lo;
+      _Float16* dst = Ax + (size_t)t * 2 * K + pf_ax_off(4 * i);
+      *reinterpret_cast<half4*>(dst) = hi;
+      *reinterpret_cast<half4*>(dst + 32) = lo;
     }
   }
   if (tid == 0) rs[t] = sc;
@@ -407,8 +417,9 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // Every load (x, r, wr, w) is issued before any is used, with clamped
 // indices and stand-in pointers for the operands a mode does not read, so
 // the row costs one global round trip rather than one per operand.  The
-// normed row goes out as the GEMM's A operand: fp16 hi/lo planes Xh, Xl
-// ([T][H]) and the row scale rs[t], as gh_pf_halves_k makes them.
+// normed row goes out as the GEMM's A operand: fp16 hi/lo halves in the ax
+// layout (pf_ax_off, [T][2H]) and the row scale rs[t], as gh_pf_halves_k
+// makes them.
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float* red) {
 #pragma unroll
@@ -423,7 +434,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
-    float* X, const float* R, const float* wr, const float* w, _Float16* Xh, _Float16* Xl,
+    float* X, const float* R, const float* wr, const float* w, _Float16* Xa,
     float* rs, uint32_t H, float s, float eps, uint32_t mode) {
   __shared__ float red[PF_NORM_NT / 64];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -474,8 +485,9 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     if (i < H) {
       const float y = v[u] * sinv;
       const _Float16 hi = (_Float16)y;
-      Xh[(size_t)t * H + i] = hi;
-      Xl[(size_t)t * H + i] = (_Float16)(y - (float)hi);
+      _Float16* dst = Xa + (size_t)t * 2 * H + pf_ax_off(i);
+      dst[0] = hi;
+      dst[32] = (_Float16)(y - (float)hi);
     }
   }
   if (tid == 0) rs[t] = sc;

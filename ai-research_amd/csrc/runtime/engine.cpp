@@ -314,18 +314,17 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
 }
 
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
-                                    const void* W1, const void* Ah, const void* Al,
-                                    const float* rs, float* C, uint32_t T, uint32_t N, uint32_t K) {
+                                    const void* W1, const void* Ax, const float* rs, float* C,
+                                    uint32_t T, uint32_t N, uint32_t K) {
   if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
     return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4 or Q8");
-  if (!W0 || !Ah || !Al || !rs || !C || T == 0 || N == 0 || K == 0)
+  if (!W0 || !Ax || !rs || !C || T == 0 || N == 0 || K == 0)
     return fail(GH_ERR_INVALID, "prefill GEMM: null pointer or zero size");
   if (K % 32 != 0) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K must be a multiple of 32");
   if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
-  if ((reinterpret_cast<uintptr_t>(Ah) & 15) || (reinterpret_cast<uintptr_t>(Al) & 15) ||
-      (reinterpret_cast<uintptr_t>(W0) & 3) ||
+  if ((reinterpret_cast<uintptr_t>(Ax) & 15) || (reinterpret_cast<uintptr_t>(W0) & 3) ||
       (W1 && (reinterpret_cast<uintptr_t>(W1) & 3)))
-    return fail(GH_ERR_INVALID, "prefill GEMM: A planes must be 16-byte and W 4-byte aligned");
+    return fail(GH_ERR_INVALID, "prefill GEMM: A halves must be 16-byte and W 4-byte aligned");
   const bool pair = W1 != nullptr;
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
@@ -364,12 +363,12 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   }
   gh_status st;
   if (pair) {
-    void* args[] = {const_cast<void**>(&Ah), const_cast<void**>(&Al), const_cast<float**>(&rs),
-                    const_cast<void**>(&W0), const_cast<void**>(&W1), &out, &T, &N, &K};
+    void* args[] = {const_cast<void**>(&Ax), const_cast<float**>(&rs), const_cast<void**>(&W0),
+                    const_cast<void**>(&W1), &out, &T, &N, &K};
     st = ctx->launch(name, grid, dim3(256), 0, args);
   } else {
-    void* args[] = {const_cast<void**>(&Ah), const_cast<void**>(&Al), const_cast<float**>(&rs),
-                    const_cast<void**>(&W0), &out, &T, &N, &K};
+    void* args[] = {const_cast<void**>(&Ax), const_cast<float**>(&rs), const_cast<void**>(&W0),
+                    &out, &T, &N, &K};
     st = ctx->launch(name, grid, dim3(256), 0, args);
   }
   if (st != GH_OK || nz == 1) return st;
@@ -379,7 +378,7 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
 }
 
-// f32 A: split into fp16 hi/lo planes with a power-of-two scale per row
+// f32 A: split into fp16 hi/lo halves with a power-of-two scale per row
 // (gh_pf_halves_k, once per row rather than in every tile that reads it),
 // then the GEMM.
 gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
@@ -387,17 +386,16 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   if (!A || T == 0 || K == 0 || K % 32 != 0) return fail(GH_ERR_INVALID, "prefill GEMM: bad A");
   if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
   if (reinterpret_cast<uintptr_t>(A) & 15) return fail(GH_ERR_INVALID, "prefill GEMM: A must be 16-byte aligned");
-  const size_t plane = (size_t)T * K * 2;
+  const size_t ax_bytes = (size_t)T * K * 4;  // 2 K halves per row
   gh_status st = ctx->ensure_zeroed(&ctx->half_scratch, &ctx->half_scratch_bytes,
-                                    2 * plane + (size_t)T * sizeof(float));
+                                    ax_bytes + (size_t)T * sizeof(float));
   if (st != GH_OK) return st;
   char* hb = static_cast<char*>(ctx->half_scratch);
-  void* Ah = hb;
-  void* Al = hb + plane;
-  float* rs = reinterpret_cast<float*>(hb + 2 * plane);
-  void* args[] = {const_cast<float**>(&A), &Ah, &Al, &rs, &K};
+  void* Ax = hb;
+  float* rs = reinterpret_cast<float*>(hb + ax_bytes);
+  void* args[] = {const_cast<float**>(&A), &Ax, &rs, &K};
   if ((st = ctx->launch("gh_pf_halves_k", dim3(T), dim3(1024), 0, args)) != GH_OK) return st;
-  return launch_prefill_gemm_split(ctx, mode, W0, W1, Ah, Al, rs, C, T, N, K);
+  return launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, T, N, K);
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {

@@ -742,12 +742,11 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   uint32_t H = m->cfg.hidden_size;
   float eps = m->cfg.rms_norm_eps;
   float* X = m->pf_x;
-  // the normed rows as the GEMM's A operand: fp16 hi/lo planes in pf_xn
-  uint16_t* Xh = reinterpret_cast<uint16_t*>(m->pf_xn);
-  uint16_t* Xl = Xh + (size_t)T * H;
+  // the normed rows as the GEMM's A operand: fp16 hi/lo halves ([T][2H]) in pf_xn
+  uint16_t* Xa = reinterpret_cast<uint16_t*>(m->pf_xn);
   float* rs = m->pf_rs;
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
-                  &Xh, &Xl, &rs, &H, &s, &eps, &mode};
+                  &Xa, &rs, &H, &s, &eps, &mode};
   return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
 }
 
@@ -773,8 +772,7 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     // 2. [q|k|v] rows of every token
     const uint16_t* xh = reinterpret_cast<const uint16_t*>(m->pf_xn);
     if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.qkv), nullptr, xh,
-                                            xh + (size_t)T * H, m->pf_rs, m->pf_qkv, T, L.qkv_rows,
-                                            H)) != GH_OK)
+                                            m->pf_rs, m->pf_qkv, T, L.qkv_rows, H)) != GH_OK)
       return st;
     // 3. q/k norm + RoPE in place, K/V into the caches, then attention
     AttnArgs a{};
@@ -821,8 +819,8 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
                              m->at<float>(L.pre_ffn), 1.0f, 2)) != GH_OK)
       return st;
     if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.gate),
-                                            m->at<uint8_t>(L.up), xh, xh + (size_t)T * H,
-                                            m->pf_rs, m->pf_act, T, I, H)) != GH_OK)
+                                            m->at<uint8_t>(L.up), xh, m->pf_rs, m->pf_act, T,
+                                            I, H)) != GH_OK)
       return st;
     // 6. m = W_down . act
     if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.down), nullptr, m->pf_act,

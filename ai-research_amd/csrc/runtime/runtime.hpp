@@ -26,7 +26,7 @@ struct gh_context {
   size_t argmax_scratch_bytes = 0;
   void* gemm_scratch = nullptr;  // split-K partial planes of the prefill GEMM
   size_t gemm_scratch_bytes = 0;
-  void* half_scratch = nullptr;  // the prefill GEMM's A operand: fp16 hi/lo planes, row scales
+  void* half_scratch = nullptr;  // the prefill GEMM's A operand: fp16 hi/lo halves, row scales
   size_t half_scratch_bytes = 0;
   gh_status ensure_zeroed(void** buf, size_t* have, size_t need);
   std::unordered_map<std::string, hipFunction_t> fns;
@@ -80,11 +80,12 @@ uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slot
 // W1, C = gelu_tanh(A . deq(W0)^T) * (A . deq(W1)^T); A and C f32.
 gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
                               const float* A, float* C, uint32_t T, uint32_t N, uint32_t K);
-// The same with A given as its fp16 hi/lo planes Ah, Al ([T][K]) and row
-// scales rs (A = rs[t] (Ah + Al)), as gh_pf_norm_k / gh_pf_halves_k write them.
+// The same with A given as its fp16 hi/lo halves Ax ([T][2K], the hi and lo
+// halves of each 32-element block side by side) and row scales rs
+// (A = rs[t] (hi + lo)), as gh_pf_norm_k / gh_pf_halves_k write them.
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
-                                    const void* W1, const void* Ah, const void* Al,
-                                    const float* rs, float* C, uint32_t T, uint32_t N, uint32_t K);
+                                    const void* W1, const void* Ax, const float* rs, float* C,
+                                    uint32_t T, uint32_t N, uint32_t K);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);
 }  // namespace gh

@@ -124,7 +124,17 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
   __shared__ float Ds[2][B_ROWS * KB];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // XCD-aware tile order: workgroups go to the 8 XCDs round-robin (w % 8), so
+  // XCD c takes the c-th contiguous eighth of the tiles in (split, m, n)
+  // order, n fastest.  The tiles of one XCD then share their A rows (one
+  // 128-row block of a 512-token prompt is 2 MB: it stays in the XCD's L2)
+  // instead of every XCD cycling through all of A.
+  const uint32_t gx = gridDim.x, gy = gridDim.y, gz = SPLIT ? gridDim.z : 1u;
+  const uint32_t G = gx * gy * gz;
+  uint32_t w = blockIdx.x + gx * (blockIdx.y + gy * (SPLIT ? blockIdx.z : 0u));
+  if (G % 8 == 0) w = (w % 8) * (G / 8) + w / 8;
+  const uint32_t tn = w % gx, tm = (w / gx) % gy;
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
   const uint32_t wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
   const uint32_t nb = K / 32, nsteps = (nb + KB - 1) / KB;
   const size_t row_bytes = (size_t)nb * F::kBlockBytes;
@@ -191,7 +201,7 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[q][i][j][r] = 0.f;
 
-  const uint32_t nz = SPLIT ? gridDim.z : 1u, z = SPLIT ? blockIdx.z : 0u;
+  const uint32_t nz = gz, z = w / (gx * gy);
   const uint32_t s_begin = (uint32_t)((uint64_t)nsteps * z / nz);
   const uint32_t s_end = (uint32_t)((uint64_t)nsteps * (z + 1) / nz);
   if (s_begin < s_end) {

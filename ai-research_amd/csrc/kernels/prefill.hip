@@ -107,21 +107,28 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
                                           const uint8_t* __restrict__ W0,
                                           const uint8_t* __restrict__ W1, float* __restrict__ C,
                                           uint32_t T, uint32_t N, uint32_t K) {
+  static_assert(KB == 1, "one quant block per K step (the LDS swizzle assumes it)");
   constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave in M and N
-  constexpr int BK = 32 * KB;
-  constexpr int LS = BK + 8;                 // LDS row stride in halves (+8: bank spread)
   constexpr int A_CH = 8 * KB;                               // 16-B chunks per row and step
   constexpr int A_PER = BM * A_CH / PF_NT;                   // 16-B chunks per thread
   constexpr int B_ROWS = NMAT * BN;                          // weight rows per step
   constexpr int B_HALVES = 2 * KB * B_ROWS;                  // 16-element half-blocks
   constexpr int B_PER = (B_HALVES + PF_NT - 1) / PF_NT;
   static_assert(A_PER >= 1 && (BM * A_CH) % PF_NT == 0, "A chunks divide the workgroup");
-  // two LDS stages: the MFMAs of step s read one while step s+1 is stored
-  // into the other, so a K step needs one barrier.  SA[stage] holds the hi
-  // plane, then the lo plane, BM rows of LS halves each.
-  __shared__ _Float16 SA[2][2 * BM * LS];
-  __shared__ _Float16 Bs[2][B_ROWS * LS];
+  // Two LDS stages: the MFMAs of step s read one while step s+1 is stored
+  // into the other, so a K step needs one barrier.  A row of a stage is 128 B
+  // (8 chunks of 8 halves: hi 0-3, lo 4-7), a weight row 64 B (4 chunks), with
+  // no padding; chunk k of row r sits at k ^ sa(r) (A) or k ^ sb(r) (weights).
+  // The swizzles keep every ds_read_b128 of the MFMA operands (16 rows at one
+  // chunk) and every ds_write_b128 of a stage (2 A rows, or 8 weight rows at
+  // two chunks) on distinct banks, for 8-lane phases over 32 banks as well as
+  // 16-lane phases over 64.  (An 80-byte padded row was conflict-free to read
+  // but not to write: write conflicts cost as many LDS cycles as the reads.)
+  __shared__ _Float16 SA[2][BM * 64];
+  __shared__ _Float16 Bs[2][B_ROWS * 32];
   __shared__ float Ds[2][B_ROWS * KB];
+  auto a_at = [](uint32_t r, uint32_t k) { return r * 64 + 8 * (k ^ ((r & 7) ^ ((r >> 3) & 1))); };
+  auto b_at = [](uint32_t r, uint32_t k) { return r * 32 + 8 * (k ^ (((r >> 1) ^ (r >> 2)) & 3)); };
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // XCD-aware tile order: workgroups go to the 8 XCDs round-robin (w % 8), so
@@ -172,9 +179,8 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
   auto store_step = [&](int sb, uint32_t step) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      const uint32_t c = tid + i * PF_NT, q = c % A_CH;
-      const uint32_t o = ((q / 4) % 2) * BM * LS + (c / A_CH) * LS + 32 * (q / 8) + 8 * (q % 4);
-      *reinterpret_cast<u32x4*>(&SA[sb][o]) = ra[i];
+      const uint32_t c = tid + i * PF_NT;
+      *reinterpret_cast<u32x4*>(&SA[sb][a_at(c / A_CH, c % A_CH)]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
@@ -183,9 +189,9 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
         const uint32_t lr = hb / (2 * KB), kq = (hb / 2) % KB;
         _Float16 v[16];
         F::ints(rb[i], v);
-        _Float16* dst = &Bs[sb][lr * LS + 32 * kq + 16 * (hb % 2)];
-        *reinterpret_cast<half8*>(dst) = *reinterpret_cast<const half8*>(v);
-        *reinterpret_cast<half8*>(dst + 8) = *reinterpret_cast<const half8*>(v + 8);
+        *reinterpret_cast<half8*>(&Bs[sb][b_at(lr, 2 * (hb % 2))]) = *reinterpret_cast<const half8*>(v);
+        *reinterpret_cast<half8*>(&Bs[sb][b_at(lr, 2 * (hb % 2) + 1)]) =
+            *reinterpret_cast<const half8*>(v + 8);
         if (hb % 2 == 0) Ds[sb][lr * KB + kq] = step * KB + kq < nb ? __uint_as_float(rb[i][0]) : 0.f;
       }
     }
@@ -219,19 +225,17 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
       for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-          const uint32_t o = (wm + 32 * i + lane % 32) * LS + 32 * kq + 16 * h + 8 * (lane / 32);
-          ah[h][i] = *reinterpret_cast<const half8*>(&SA[cb][o]);
-          al[h][i] = *reinterpret_cast<const half8*>(&SA[cb][BM * LS + o]);
+          const uint32_t r = wm + 32 * i + lane % 32, k = 2 * h + lane / 32;
+          ah[h][i] = *reinterpret_cast<const half8*>(&SA[cb][a_at(r, k)]);
+          al[h][i] = *reinterpret_cast<const half8*>(&SA[cb][a_at(r, 4 + k)]);
         }
 #pragma unroll
       for (int q = 0; q < NMAT; q++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
           const uint32_t brow = q * BN + wn + 32 * j + lane % 32;
-          const half8 b0 =
-              *reinterpret_cast<const half8*>(&Bs[cb][brow * LS + 32 * kq + 8 * (lane / 32)]);
-          const half8 b1 =
-              *reinterpret_cast<const half8*>(&Bs[cb][brow * LS + 32 * kq + 16 + 8 * (lane / 32)]);
+          const half8 b0 = *reinterpret_cast<const half8*>(&Bs[cb][b_at(brow, lane / 32)]);
+          const half8 b1 = *reinterpret_cast<const half8*>(&Bs[cb][b_at(brow, 2 + lane / 32)]);
           const float d = Ds[cb][brow * KB + kq];
 #pragma unroll
           for (int i = 0; i < TM; i++) {

@@ -54,12 +54,21 @@ struct Q4W {  // src/quant.zig:55-90: {f32 d, 4 words of nibbles}
     w[1] = p[1 + 2 * h];
     w[2] = p[2 + 2 * h];
   }
-  __device__ static void ints(const uint32_t* w, _Float16* out) {  // n - 8
+  // n - 8 as fp16 pairs, exactly: (w >> 4j) & 0x000F000F | 0x64006400 read as
+  // two halves is (1024 + n_j, 1024 + n_{j+4}), and one packed subtract of
+  // 1032 leaves (n_j - 8, n_{j+4} - 8).  So the 8 elements of a word come out
+  // in the K order (0,4,1,5,2,6,3,7); the A operand is stored in the same
+  // order (pf_ax_pos with perm).  out: 8 words = the half-block's 16 halves.
+  __device__ static void ints(const uint32_t* w, uint32_t* out) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
 #pragma unroll
     for (int k = 0; k < 2; k++)
 #pragma unroll
-      for (int n = 0; n < 8; n++)
-        out[8 * k + n] = (_Float16)((int)((w[1 + k] >> (4 * n)) & 15u) - 8);
+      for (int j = 0; j < 4; j++) {
+        const uint32_t pr = ((w[1 + k] >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+        out[4 * k + j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pr) + bias);
+      }
   }
 };
 
@@ -72,11 +81,16 @@ struct Q8W {  // src/quant.zig:20-51: {f32 d, 8 words of int8}
 #pragma unroll
     for (int k = 0; k < 4; k++) w[1 + k] = p[1 + 4 * h + k];
   }
-  __device__ static void ints(const uint32_t* w, _Float16* out) {  // q
+  __device__ static void ints(const uint32_t* w, uint32_t* out) {  // q as fp16, in K order
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int k = 0; k < 4; k++)
 #pragma unroll
-      for (int n = 0; n < 4; n++) out[4 * k + n] = (_Float16)(int)(int8_t)((w[1 + k] >> (8 * n)) & 0xFFu);
+      for (int n = 0; n < 4; n += 2) {
+        const h2 v = {(_Float16)(int)(int8_t)((w[1 + k] >> (8 * n)) & 0xFFu),
+                      (_Float16)(int)(int8_t)((w[1 + k] >> (8 * n + 8)) & 0xFFu)};
+        out[2 * k + n / 2] = __builtin_bit_cast(uint32_t, v);
+      }
   }
 };
 
@@ -90,8 +104,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // The GEMM's A operand layout ("ax"): row t of K elements is 2K halves, the
 // hi halves of block b (elements 32b .. 32b+31) at 64b, their lo halves at
-// 64b + 32.  Offset of element e's hi half within its row:
-__device__ __forceinline__ uint32_t pf_ax_off(uint32_t e) { return (e >> 5) * 64 + (e & 31); }
+// 64b + 32.  With perm (Q4_0 weights) the 8 elements of each group sit in the
+// order Q4W::ints unpacks a word: position 2m holds element m, 2m + 1 element
+// m + 4.  Offset of element e's hi half within its row:
+__device__ __forceinline__ uint32_t pf_ax_pos(uint32_t e, bool perm) {
+  const uint32_t j = e & 7;
+  return (e >> 5) * 64 + (e & 24) + (perm ? ((j & 3) << 1) | (j >> 2) : j);
+}
 
 // NMAT = 1: C = A W^T.  NMAT = 2: C = gelu_tanh(A Wg^T) * (A Wu^T).  A as its
 // fp16 hi/lo halves interleaved per 32-element block (pf_ax: a row's K step
@@ -187,11 +206,10 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
       const uint32_t hb = tid + i * PF_NT;
       if (hb < (uint32_t)B_HALVES) {
         const uint32_t lr = hb / (2 * KB), kq = (hb / 2) % KB;
-        _Float16 v[16];
+        uint32_t v[8];
         F::ints(rb[i], v);
-        *reinterpret_cast<half8*>(&Bs[sb][b_at(lr, 2 * (hb % 2))]) = *reinterpret_cast<const half8*>(v);
-        *reinterpret_cast<half8*>(&Bs[sb][b_at(lr, 2 * (hb % 2) + 1)]) =
-            *reinterpret_cast<const half8*>(v + 8);
+        *reinterpret_cast<u32x4*>(&Bs[sb][b_at(lr, 2 * (hb % 2))]) = u32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<u32x4*>(&Bs[sb][b_at(lr, 2 * (hb % 2) + 1)]) = u32x4{v[4], v[5], v[6], v[7]};
         if (hb % 2 == 0) Ds[sb][lr * KB + kq] = step * KB + kq < nb ? __uint_as_float(rb[i][0]) : 0.f;
       }
     }
@@ -338,24 +356,44 @@ __device__ __forceinline__ float row_scale(float m, float* inv) {
 
 // The MFMA A operand of one f32 row (K <= PF_HALVES_K): hi = fp16(a / s),
 // lo = fp16(a / s - hi) with s = row_scale(max|a|), in the ax layout
-// (pf_ax_off).  One workgroup per row; rs[t] = s.
+// (pf_ax_pos).  One workgroup per row; rs[t] = s.
 #define PF_HALVES_NT 1024
-#define PF_HALVES_U 4
-#define PF_HALVES_K (4 * PF_HALVES_NT * PF_HALVES_U)
+#define PF_HALVES_G 2  // 8-element groups per thread
+#define PF_HALVES_K (8 * PF_HALVES_NT * PF_HALVES_G)
+
+// hi = fp16(x), lo = fp16(x - hi) of one 8-element group, stored in the ax
+// layout at dst (16-byte aligned): the group's hi halves, and 32 halves on its
+// lo halves, each as one 16-byte store (in the Q4 K order with perm).
+__device__ __forceinline__ void pf_store_group(const float (&x)[8], bool perm, _Float16* dst) {
+  half8 hi, lo;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int p = perm ? ((k & 3) << 1) | (k >> 2) : k;
+    const _Float16 h = (_Float16)x[k];
+    hi[p] = h;
+    lo[p] = (_Float16)(x[k] - (float)h);
+  }
+  *reinterpret_cast<half8*>(dst) = hi;
+  *reinterpret_cast<half8*>(dst + 32) = lo;
+}
+
 extern "C" __global__ __launch_bounds__(PF_HALVES_NT) void gh_pf_halves_k(
     const float* __restrict__ A, _Float16* __restrict__ Ax,
-    float* __restrict__ rs, uint32_t K) {
+    float* __restrict__ rs, uint32_t K, uint32_t perm) {
   __shared__ float red[PF_HALVES_NT / 64];
-  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-  const uint32_t t = blockIdx.x, tid = threadIdx.x, n4 = K / 4;
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, n8 = K / 8;
   const float4* a = reinterpret_cast<const float4*>(A + (size_t)t * K);
-  float4 v[PF_HALVES_U];
+  float4 v[PF_HALVES_G][2];
   float m = 0.f;
 #pragma unroll
-  for (int u = 0; u < PF_HALVES_U; u++) {
-    const uint32_t i = tid + u * PF_HALVES_NT;
-    v[u] = a[i < n4 ? i : n4 - 1];
-    if (i < n4) m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+  for (int u = 0; u < PF_HALVES_G; u++) {
+    const uint32_t g = tid + u * PF_HALVES_NT, gc = g < n8 ? g : n8 - 1;
+    v[u][0] = a[2 * gc];
+    v[u][1] = a[2 * gc + 1];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      if (g < n8)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u][h].x), fabsf(v[u][h].y)), fmaxf(fabsf(v[u][h].z), fabsf(v[u][h].w))));
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
@@ -367,19 +405,12 @@ extern "C" __global__ __launch_bounds__(PF_HALVES_NT) void gh_pf_halves_k(
   float inv;
   const float sc = row_scale(m, &inv);
 #pragma unroll
-  for (int u = 0; u < PF_HALVES_U; u++) {
-    const uint32_t i = tid + u * PF_HALVES_NT;
-    if (i < n4) {
-      const float x[4] = {v[u].x * inv, v[u].y * inv, v[u].z * inv, v[u].w * inv};
-      half4 hi, lo;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        hi[k] = (_Float16)x[k];
-        lo[k] = (_Float16)(x[k] - (float)hi[k]);
-      }
-      _Float16* dst = Ax + (size_t)t * 2 * K + pf_ax_off(4 * i);
-      *reinterpret_cast<half4*>(dst) = hi;
-      *reinterpret_cast<half4*>(dst + 32) = lo;
+  for (int u = 0; u < PF_HALVES_G; u++) {
+    const uint32_t g = tid + u * PF_HALVES_NT;
+    if (g < n8) {
+      const float x[8] = {v[u][0].x * inv, v[u][0].y * inv, v[u][0].z * inv, v[u][0].w * inv,
+                          v[u][1].x * inv, v[u][1].y * inv, v[u][1].z * inv, v[u][1].w * inv};
+      pf_store_group(x, perm != 0, Ax + (size_t)t * 2 * K + pf_ax_pos(8 * g, false));
     }
   }
   if (tid == 0) rs[t] = sc;
@@ -426,13 +457,13 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 #define PF_NORM_NT 1024
-#define PF_ROW_MAX 8  // elements per thread: hidden <= 8192
+#define PF_ROW_MAX 8  // elements per thread (one 8-element group): hidden <= 8192
 
 // Every load (x, r, wr, w) is issued before any is used, with clamped
 // indices and stand-in pointers for the operands a mode does not read, so
 // the row costs one global round trip rather than one per operand.  The
 // normed row goes out as the GEMM's A operand: fp16 hi/lo halves in the ax
-// layout (pf_ax_off, [T][2H]) and the row scale rs[t], as gh_pf_halves_k
+// layout (pf_ax_pos, [T][2H]) and the row scale rs[t], as gh_pf_halves_k
 // makes them.
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float* red) {
@@ -449,60 +480,60 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 
 extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     float* X, const float* R, const float* wr, const float* w, _Float16* Xa,
-    float* rs, uint32_t H, float s, float eps, uint32_t mode) {
+    float* rs, uint32_t H, float s, float eps, uint32_t mode, uint32_t perm) {
   __shared__ float red[PF_NORM_NT / 64];
-  const uint32_t t = blockIdx.x, tid = threadIdx.x;
-  const bool add = mode == 2, has_wr = wr != nullptr;
+  // thread t owns the 8-element group t of the row (H <= 8 * PF_NORM_NT)
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, n8 = H / 8;
+  const bool add = mode == 2, has_wr = wr != nullptr, act = tid < n8;
+  const uint32_t e0 = 8 * (act ? tid : n8 - 1);
   float* x = X + (size_t)t * H;
   const float* r = add ? R + (size_t)t * H : x;
   const float* wrp = has_wr ? wr : w;
-  float v[PF_ROW_MAX], rv[PF_ROW_MAX], wv[PF_ROW_MAX], wrv[PF_ROW_MAX];
-#pragma unroll
-  for (int u = 0; u < PF_ROW_MAX; u++) {
-    uint32_t i = tid + u * PF_NORM_NT;
-    i = i < H ? i : H - 1;
-    v[u] = x[i];
-    rv[u] = r[i];
-    wv[u] = w[i];
-    wrv[u] = wrp[i];
-  }
+  float v[8], rv[8], wv[8], wrv[8];
+  auto load8 = [&](const float* p, float (&o)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p + e0);
+    const float4 b = *reinterpret_cast<const float4*>(p + e0 + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  };
+  load8(x, v);
+  load8(r, rv);
+  load8(w, wv);
+  load8(wrp, wrv);
   if (add) {
     float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < PF_ROW_MAX; u++)
-      if (tid + u * PF_NORM_NT < H) ss += rv[u] * rv[u];
+    for (int k = 0; k < 8; k++) ss += rv[k] * rv[k];
+    ss = act ? ss : 0.f;
     const float inv_r = has_wr ? 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps) : 1.0f;
 #pragma unroll
-    for (int u = 0; u < PF_ROW_MAX; u++) {
-      const uint32_t i = tid + u * PF_NORM_NT;
-      const float rr = has_wr ? rv[u] * inv_r * wrv[u] : rv[u];
-      v[u] = (v[u] + rr) * s;
-      if (i < H) x[i] = v[u];
+    for (int k = 0; k < 8; k++) {
+      const float rr = has_wr ? rv[k] * inv_r * wrv[k] : rv[k];
+      v[k] = (v[k] + rr) * s;
+    }
+    if (act) {
+      *reinterpret_cast<float4*>(x + e0) = make_float4(v[0], v[1], v[2], v[3]);
+      *reinterpret_cast<float4*>(x + e0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
     }
   }
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < PF_ROW_MAX; u++)
-    if (tid + u * PF_NORM_NT < H) ss += v[u] * v[u];
+  for (int k = 0; k < 8; k++) ss += v[k] * v[k];
+  ss = act ? ss : 0.f;
   const float inv = 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps);
   float m = 0.f;
 #pragma unroll
-  for (int u = 0; u < PF_ROW_MAX; u++) {
-    v[u] = v[u] * inv * wv[u];
-    if (tid + u * PF_NORM_NT < H) m = fmaxf(m, fabsf(v[u]));
+  for (int k = 0; k < 8; k++) {
+    v[k] = v[k] * inv * wv[k];
+    m = fmaxf(m, fabsf(v[k]));
   }
   float sinv;
-  const float sc = row_scale(block_max<PF_NORM_NT>(m, red), &sinv);
+  const float sc = row_scale(block_max<PF_NORM_NT>(act ? m : 0.f, red), &sinv);
+  if (act) {
+    float y[8];
 #pragma unroll
-  for (int u = 0; u < PF_ROW_MAX; u++) {
-    const uint32_t i = tid + u * PF_NORM_NT;
-    if (i < H) {
-      const float y = v[u] * sinv;
-      const _Float16 hi = (_Float16)y;
-      _Float16* dst = Xa + (size_t)t * 2 * H + pf_ax_off(i);
-      dst[0] = hi;
-      dst[32] = (_Float16)(y - (float)hi);
-    }
+    for (int k = 0; k < 8; k++) y[k] = v[k] * sinv;
+    pf_store_group(y, perm != 0, Xa + (size_t)t * 2 * H + pf_ax_pos(e0, false));
   }
   if (tid == 0) rs[t] = sc;
 }

@@ -393,7 +393,8 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   char* hb = static_cast<char*>(ctx->half_scratch);
   void* Ax = hb;
   float* rs = reinterpret_cast<float*>(hb + ax_bytes);
-  void* args[] = {const_cast<float**>(&A), &Ax, &rs, &K};
+  uint32_t perm = mode == GH_QUANT_Q4 ? 1u : 0u;  // K order of the Q4 unpacking
+  void* args[] = {const_cast<float**>(&A), &Ax, &rs, &K, &perm};
   if ((st = ctx->launch("gh_pf_halves_k", dim3(T), dim3(1024), 0, args)) != GH_OK) return st;
   return launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, T, N, K);
 }

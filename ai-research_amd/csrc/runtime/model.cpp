@@ -745,8 +745,9 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   // the normed rows as the GEMM's A operand: fp16 hi/lo halves ([T][2H]) in pf_xn
   uint16_t* Xa = reinterpret_cast<uint16_t*>(m->pf_xn);
   float* rs = m->pf_rs;
+  uint32_t perm = m->mode == GH_QUANT_Q4 ? 1u : 0u;  // K order of the Q4 unpacking
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
-                  &Xa, &rs, &H, &s, &eps, &mode};
+                  &Xa, &rs, &H, &s, &eps, &mode, &perm};
   return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
 }
 

@@ -60,6 +60,9 @@ Q4_SHAPES = [
     (3840, 4096),    # o_proj
     (3840, 15360),   # down_proj
     (1, 128), (5, 256), (37, 1024), (1000, 3840), (3, 15360),  # ragged row tails
+    # x longer than the staging registers hold (K > 16 x threads): the workgroup
+    # splits into x stagers and first streamers (256 and 1024 threads)
+    (64, 6144), (40, 32768),
 ]
 
 
@@ -109,7 +112,7 @@ def test_gemv_rejects_unsupported_shapes(gpu):
 
 
 # ---------------------------------------------------------------- Q8 GEMV -
-@pytest.mark.parametrize("M,K", [(4096, 3840), (777, 1024), (1, 128), (3840, 15360)])
+@pytest.mark.parametrize("M,K", [(4096, 3840), (777, 1024), (1, 128), (3840, 15360), (64, 6144)])
 def test_gemv_q8_parity(gpu, M, K):
     w = gh.synth_normal(M * K, 0, 2000 + M, 0.0, 0.02, bf16=True).reshape(M, K)
     wq = orc.quantize_q8(w, NT)

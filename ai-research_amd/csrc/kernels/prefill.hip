@@ -15,18 +15,19 @@
 //    lo = fp16(a / s - hi) and s a power of two per row that puts the row's
 //    largest |a| / s in [2^13, 2^14) (no fp16 overflow for any row), and both
 //    halves go through the MFMA (22+ significant bits of a).  The split is
-//    made once per row by gh_pf_halves_k, not in every tile that reads the
-//    row, and s is applied in the epilogue (exact: a power of two);
+//    made once per row (gh_pf_halves_k, or gh_pf_norm_k for normed rows),
+//    not in every tile that reads the row, and s is applied in the epilogue
+//    (exact: a power of two);
 //  * accumulation is fp32.
 //
 // Tiling: a workgroup of 256 threads (2 x 2 wavefronts) owns a BM x BN tile
 // of C; each wavefront a (BM/2) x (BN/2) sub-tile of 32 x 32 MFMA blocks.  K
 // advances one quant block (32) per step: the A slice (as hi and lo) and the
-// integer W slice with its scales go to LDS (row stride padded to 40 halves
-// so the 16-byte operand reads of 32 consecutive rows spread over all
-// banks).  Two LDS stages: while the MFMAs of step s read one, step s+1's
-// global loads are in flight and then stored into the other, one barrier
-// per step.
+// integer W slice with its scales go to LDS in unpadded, XOR-swizzled rows
+// (bank-conflict-free operand reads and stage writes).  Two LDS stages:
+// while the MFMAs of step s read one, step s+1's global loads are in flight
+// and then stored into the other, one barrier per step.  Workgroups take
+// their tiles in an XCD-aware order (the tiles of one XCD share A rows).
 //
 // MFMA 32x32x16 f16 operand layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32], e = 0..7; result
@@ -38,7 +39,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define PF_NT 256
-#define LDS_STRIDE 40  // halves per LDS row of a 32-wide K slice (+8 pad)
 
 // Weight words through an explicit global-address-space pointer: the matrix
 // is picked at run time (gate or up), which would otherwise degrade to FLAT.

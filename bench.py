@@ -168,10 +168,17 @@ def bench_decode(ctx, n_prompt=512, n_decode=128):
         slots.append(ring.activate_slot(0, c))
         actives.append(np.array(ring.active_slots(0, c), np.uint32))
     clocks = np.arange(n_prompt)
-    m.prefill(xs, clocks, slots, actives, True)  # allocates the prefill buffers
-    t0 = time.perf_counter()
-    tok = m.prefill(xs, clocks, slots, actives, True)  # rewrites the same K/V
-    prefill_s = time.perf_counter() - t0
+    # Two untimed calls (the first allocates the prefill buffers; the GPU comes
+    # up to clock after the idle embedding read), then the median of three
+    # timed calls, each rewriting the same K/V.
+    for _ in range(2):
+        m.prefill(xs, clocks, slots, actives, True)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        tok = m.prefill(xs, clocks, slots, actives, True)
+        times.append(time.perf_counter() - t0)
+    prefill_s = sorted(times)[1]
     toks = []
     t0 = time.perf_counter()
     for i in range(n_decode):
@@ -189,7 +196,7 @@ def bench_decode(ctx, n_prompt=512, n_decode=128):
             "decode_weight_gbs": round(step_bytes * n_decode / decode_s / 1e9, 1),
             "prefill_tok_s": round(n_prompt / prefill_s, 1),
             "prefill_ms": round(prefill_s * 1e3, 2),
-            "prefill_path": "batched (MFMA Q4 dequant GEMM), one call",
+            "prefill_path": "batched (MFMA Q4 dequant GEMM), one call; median of 3 after 2 warm-up calls",
             "prefill_gemm_tflops": round(gemm_flop / prefill_s / 1e12, 1),
             "model_init_s": round(init_s, 2),
             "decode_tokens_head": [int(t) for t in toks[:8]]}

@@ -23,4 +23,7 @@ struct AttnArgs {
   const uint32_t* n_active;
   float* out_rows;
   uint32_t q_stride, active_stride, out_stride;
+  // grouped prefill (gh_pf_attn_g_*): tokens in the batch; active/n_active
+  // then hold one union list per group of consecutive tokens
+  uint32_t n_tokens;
 };

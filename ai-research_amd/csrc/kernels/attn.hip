@@ -389,6 +389,169 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d2_k(AttnArgs a)
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d4_k(AttnArgs a) { attn_split<4, 8, true>(a); }
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d8_k(AttnArgs a) { attn_split<8, 4, true>(a); }
 
+// v + (v of lane l ^ 16) and v + (v of lane l ^ 32), with the gfx950 lane
+// swaps (no LDS round trip); both partners compute the same sum.
+__device__ __forceinline__ float swap16_add(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap32_add(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float wave_allsum_swap(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return swap32_add(swap16_add(v));
+}
+
+// Batched prefill over groups of PF_GT consecutive tokens: grid (kv heads,
+// token groups), group ngroups-1-blockIdx.y first (the longest lists of a
+// causal batch start first).  A workgroup walks the union of its tokens'
+// active lists once (entries: slot | token mask << 24, built on the host),
+// so each K/V row it loads serves all PF_GT tokens x G query heads; a token
+// skips the slots its mask bit does not cover.  Requires G <= 2 and D <= 256;
+// the online softmax, wave merge and output follow attn_split.
+#define PF_GT 4
+#define PF_QN (PF_GT * 2)  // query vectors per workgroup: tokens x heads (G <= 2)
+#define PF_MAXD 256
+template <int DPL, int TT>
+__device__ __forceinline__ void attn_pf_group(const AttnArgs& a) {
+  __shared__ float qs[PF_QN][PF_MAXD];
+  __shared__ uint32_t sidx[ATT_CHUNK];
+  __shared__ float wm[ATT_WAVES][PF_QN], wl[ATT_WAVES][PF_QN];
+  __shared__ float wo[ATT_WAVES][PF_QN][PF_MAXD];
+
+  const uint32_t D = a.D, G = a.nq / a.nkv, gsh = G == 2 ? 1u : 0u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t kv_dim = (size_t)a.nkv * D;
+  const uint32_t kvh = blockIdx.x, grp = gridDim.y - 1 - blockIdx.y;
+  const uint32_t t0 = grp * PF_GT, nt = min((uint32_t)PF_GT, a.n_tokens - t0);
+  const uint32_t qn_used = nt * G;
+  const uint32_t S = a.n_active[grp];
+  const uint32_t* list = a.active + (size_t)grp * a.active_stride;
+  const uint32_t n0 = min(S, (uint32_t)ATT_CHUNK);
+  const uint32_t idx0 = tid < n0 ? list[tid] : 0u;  // ATT_CHUNK == ATT_NT
+
+  // 1. the group's query vectors (token i, head g at qs[i * G + g]) into LDS
+  for (uint32_t i = tid; i < qn_used * D; i += ATT_NT) {
+    const uint32_t qn = i / D, d = i % D;
+    const uint32_t t = t0 + (qn >> gsh), g = qn & (G - 1);
+    qs[qn][d] = a.q[(size_t)t * a.q_stride + (size_t)(kvh * G + g) * D + d];
+  }
+  if (tid < n0) sidx[tid] = idx0;
+  __syncthreads();
+
+  // 2. online softmax over the union list, per query vector
+  const uint32_t d0 = lane * DPL;
+  const bool dl = d0 < D;
+  float q[PF_QN][DPL], o[PF_QN][DPL], m[PF_QN], l[PF_QN];
+#pragma unroll
+  for (int qn = 0; qn < PF_QN; qn++) {
+    m[qn] = -INFINITY;
+    l[qn] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; j++) {
+      q[qn][j] = ((uint32_t)qn < qn_used && dl) ? qs[qn][d0 + j] : 0.f;
+      o[qn][j] = 0.f;
+    }
+  }
+  const float* kbase = a.k_cache + (size_t)kvh * D + d0;
+  const float* vbase = a.v_cache + (size_t)kvh * D + d0;
+
+  for (uint32_t r0 = 0; r0 < S; r0 += ATT_CHUNK) {
+    const uint32_t n = min(S - r0, (uint32_t)ATT_CHUNK);
+    if (r0 != 0) {
+      __syncthreads();
+      for (uint32_t t = tid; t < n; t += ATT_NT) sidx[t] = list[r0 + t];
+      __syncthreads();
+    }
+    for (uint32_t base = wave * TT; base < n; base += ATT_WAVES * TT) {
+      float kr[TT][DPL], vr[TT][DPL];
+      uint32_t msk[TT], any = 0;
+#pragma unroll
+      for (int j = 0; j < TT; j++) {
+        const uint32_t e = sidx[min(base + j, n - 1)];
+        const uint32_t slot = e & 0xFFFFFFu;
+        msk[j] = base + j < n ? e >> 24 : 0u;
+        any |= msk[j];
+        if (dl) {
+          load_row<DPL>(kbase + (size_t)slot * kv_dim, kr[j]);
+          load_row<DPL>(vbase + (size_t)slot * kv_dim, vr[j]);
+        } else {
+#pragma unroll
+          for (int e2 = 0; e2 < DPL; e2++) kr[j][e2] = vr[j][e2] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int qn = 0; qn < PF_QN; qn++) {
+        const uint32_t bit = (uint32_t)qn >> gsh;
+        if ((uint32_t)qn >= qn_used || !((any >> bit) & 1u)) continue;  // wave-uniform
+        float s[TT];
+#pragma unroll
+        for (int j = 0; j < TT; j++) {
+          float p = 0.f;
+#pragma unroll
+          for (int e2 = 0; e2 < DPL; e2++) p += q[qn][e2] * kr[j][e2];
+          s[j] = p;
+        }
+#pragma unroll
+        for (int j = 0; j < TT; j++) s[j] = wave_allsum_swap(s[j]) * a.scale;
+        float mt = m[qn];
+#pragma unroll
+        for (int j = 0; j < TT; j++)
+          if ((msk[j] >> bit) & 1u) mt = fmaxf(mt, s[j]);
+        const float corr = __expf(m[qn] - mt);  // m = -inf, mt finite: 0
+        l[qn] *= corr;
+#pragma unroll
+        for (int e2 = 0; e2 < DPL; e2++) o[qn][e2] *= corr;
+#pragma unroll
+        for (int j = 0; j < TT; j++) {
+          const float p = (msk[j] >> bit) & 1u ? __expf(s[j] - mt) : 0.f;
+          l[qn] += p;
+#pragma unroll
+          for (int e2 = 0; e2 < DPL; e2++) o[qn][e2] += p * vr[j][e2];
+        }
+        m[qn] = mt;
+      }
+    }
+  }
+
+  // 3. merge the waves (wave order) and write each token's output rows
+#pragma unroll
+  for (int qn = 0; qn < PF_QN; qn++) {
+    if ((uint32_t)qn >= qn_used) break;
+    if (lane == 0) {
+      wm[wave][qn] = m[qn];
+      wl[wave][qn] = l[qn];
+    }
+    if (dl) {
+#pragma unroll
+      for (int e2 = 0; e2 < DPL; e2++) wo[wave][qn][d0 + e2] = o[qn][e2];
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < qn_used * D; i += ATT_NT) {
+    const uint32_t qn = i / D, d = i % D;
+    const uint32_t t = t0 + (qn >> gsh), g = qn & (G - 1);
+    float M = -INFINITY;
+    for (int w = 0; w < ATT_WAVES; w++) M = fmaxf(M, wm[w][qn]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < ATT_WAVES; w++) {
+      const float c = wm[w][qn] == -INFINITY ? 0.f : __expf(wm[w][qn] - M);
+      L += wl[w][qn] * c;
+      O += wo[w][qn][d] * c;
+    }
+    a.out_rows[(size_t)t * a.out_stride + (size_t)(kvh * G + g) * D + d] = L > 0.f ? O / L : 0.f;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_g_d1_k(AttnArgs a) { attn_pf_group<1, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_g_d2_k(AttnArgs a) { attn_pf_group<2, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_g_d4_k(AttnArgs a) { attn_pf_group<4, 8>(a); }
+
 // Batched q/k norm + RoPE + cache write (qkv_rope.wgsl for T tokens): grid
 // (nq + nkv heads, tokens), one wavefront each.  Token t's q/k/v rows start
 // at a.q + t * q_stride (q, then k, then v unless k_eq_v); its position and

@@ -39,6 +39,7 @@ struct Layer {
 };
 
 constexpr size_t kNone = ~(size_t)0;
+constexpr uint32_t kPfGroup = 4;  // tokens per grouped prefill attention workgroup (PF_GT in attn.hip)
 
 }  // namespace
 
@@ -69,6 +70,11 @@ struct gh_model {
   float *pf_xn = nullptr, *pf_attn = nullptr, *pf_act = nullptr;
   float* pf_rs = nullptr;  // row scales of the normed rows (pf_xn holds their fp16 hi/lo planes)
   uint32_t *pf_meta = nullptr, *pf_active = nullptr;
+  // grouped prefill attention: per group of PF_GROUP consecutive tokens, the
+  // union of their active lists (slot | token mask << 24) and its length
+  uint32_t *pf_union = nullptr, *pf_ucount = nullptr;
+  uint32_t pf_ustride = 0;
+  bool pf_grouped = false;  // this call's unions are valid
 
   template <typename T>
   T* at(size_t off) const {
@@ -657,6 +663,41 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   hipError_t e = hipMemcpyAsync(m->pf_x, x, (size_t)T * c.hidden_size * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(m->pf_meta, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(m->pf_active, act.data(), act.size() * 4, hipMemcpyHostToDevice, s);
+  // union lists of each group of kPfGroup consecutive tokens, in order of
+  // first appearance; a list that names one slot twice keeps every layer on
+  // the per-token kernel (a union entry counts a slot once per token)
+  const uint32_t groups = (T + kPfGroup - 1) / kPfGroup;
+  std::vector<uint32_t> uni((size_t)groups * m->pf_ustride), ucount(groups);
+  m->pf_grouped = c.max_slots <= (1u << 24);
+  {
+    std::vector<uint32_t> stamp(c.max_slots, 0u), pos(c.max_slots);
+    for (uint32_t g = 0; g < groups && m->pf_grouped; g++) {
+      uint32_t* u = &uni[(size_t)g * m->pf_ustride];
+      uint32_t n = 0;
+      for (uint32_t i = 0; i < kPfGroup && g * kPfGroup + i < T && m->pf_grouped; i++) {
+        const uint32_t t = g * kPfGroup + i;
+        const uint32_t* row = active + (size_t)t * active_stride;
+        for (uint32_t k = 0; k < n_active[t]; k++) {
+          const uint32_t slot = row[k];
+          if (stamp[slot] != g + 1) {
+            stamp[slot] = g + 1;
+            pos[slot] = n;
+            u[n++] = slot | (1u << (24 + i));
+          } else if (u[pos[slot]] & (1u << (24 + i))) {
+            m->pf_grouped = false;
+            break;
+          } else {
+            u[pos[slot]] |= 1u << (24 + i);
+          }
+        }
+      }
+      ucount[g] = n;
+    }
+  }
+  if (m->pf_grouped && e == hipSuccess)
+    e = hipMemcpyAsync(m->pf_union, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, s);
+  if (m->pf_grouped && e == hipSuccess)
+    e = hipMemcpyAsync(m->pf_ucount, ucount.data(), ucount.size() * 4, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: input copies");
   if ((st = prefill_forward(m, T, want_logits != 0)) != GH_OK) return st;
   if (want_logits) {
@@ -711,6 +752,9 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   const size_t o_xn = take((size_t)T * H * 4), o_attn = take((size_t)T * m->max_q * 4);
   const size_t o_act = take((size_t)T * I * 4), o_meta = take((size_t)3 * T * 4);
   const size_t o_active = take((size_t)T * stride * 4), o_rs = take((size_t)T * 4);
+  const uint32_t groups = (T + kPfGroup - 1) / kPfGroup;
+  const uint32_t ustride = std::min(kPfGroup * stride, c.max_slots);
+  const size_t o_union = take((size_t)groups * ustride * 4), o_ucount = take((size_t)groups * 4);
   if (m->pf_arena) {
     hipStreamSynchronize(m->ctx->stream);
     hipFree(m->pf_arena);
@@ -731,6 +775,9 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   m->pf_meta = u32(o_meta);
   m->pf_active = u32(o_active);
   m->pf_rs = f32(o_rs);
+  m->pf_union = u32(o_union);
+  m->pf_ucount = u32(o_ucount);
+  m->pf_ustride = ustride;
   m->pf_cap = T;
   m->pf_stride = stride;
   return GH_OK;
@@ -803,12 +850,24 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
         return st;
     }
     {
-      const uint32_t D = L.head_dim;
-      const char* name = D <= 64 ? "gh_pf_attn_d1_k"
-                         : D <= 128 ? "gh_pf_attn_d2_k"
-                         : D <= 256 ? "gh_pf_attn_d4_k" : "gh_pf_attn_d8_k";
+      const uint32_t D = L.head_dim, G = a.nq / a.nkv;
       void* args[] = {&a};
-      if ((st = ctx->launch(name, dim3(a.nkv, T), dim3(256), 0, args)) != GH_OK) return st;
+      if (m->pf_grouped && G <= 2 && D <= 256) {
+        // one workgroup per (kv head, group of kPfGroup tokens) over the union list
+        a.active = m->pf_union;
+        a.n_active = m->pf_ucount;
+        a.active_stride = m->pf_ustride;
+        a.n_tokens = T;
+        const char* name = D <= 64 ? "gh_pf_attn_g_d1_k" : D <= 128 ? "gh_pf_attn_g_d2_k"
+                                                                    : "gh_pf_attn_g_d4_k";
+        const uint32_t groups = (T + kPfGroup - 1) / kPfGroup;
+        if ((st = ctx->launch(name, dim3(a.nkv, groups), dim3(256), 0, args)) != GH_OK) return st;
+      } else {
+        const char* name = D <= 64 ? "gh_pf_attn_d1_k"
+                           : D <= 128 ? "gh_pf_attn_d2_k"
+                           : D <= 256 ? "gh_pf_attn_d4_k" : "gh_pf_attn_d8_k";
+        if ((st = ctx->launch(name, dim3(a.nkv, T), dim3(256), 0, args)) != GH_OK) return st;
+      }
     }
     // 4. o = W_o . attn
     if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.o), nullptr, m->pf_attn,

@@ -124,10 +124,15 @@ def ring_lists(ring, clocks):
     return slots, actives
 
 
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
-def test_model_prefill_matches_sequential_oracle(gpu, mode):
-    # 12 prompt tokens (4 anchors, then the window), one batch, then two decode
-    # steps through the per-token graph on the caches the prefill wrote
+@pytest.mark.parametrize("mode,T,dup", [(gh.QUANT_Q4, 12, False), (gh.QUANT_Q8, 12, False),
+                                        (gh.QUANT_Q4, 11, False), (gh.QUANT_Q8, 9, True)])
+def test_model_prefill_matches_sequential_oracle(gpu, mode, T, dup):
+    # T prompt tokens (4 anchors, then the window), one batch, then decode
+    # steps through the per-token graph on the caches the prefill wrote.  T
+    # not a multiple of 4 leaves a partial token group in the grouped
+    # attention; dup names one slot twice in the last token's list (counted
+    # twice, as the reference's loop over the list does), which keeps the
+    # batch on the per-token attention kernel
     cfg = tiny_cfg()
     m = gh.Model(gpu, cfg, mode=mode, seed=11)
     try:
@@ -135,8 +140,9 @@ def test_model_prefill_matches_sequential_oracle(gpu, mode):
         ring = gh.Ring(cfg.num_hidden_layers, 4, 16, 4)
         tokens = np.random.default_rng(5).integers(0, cfg.vocab_size, 14)
         xs = np.stack([m.embed(int(t)) for t in tokens])
-        T = 12
         slots, actives = ring_lists(ring, range(T))
+        if dup:
+            actives[-1] = np.append(actives[-1], actives[-1][0])
         tok = m.prefill(xs[:T], np.arange(T), slots, actives, True)
         for c in range(T):
             rtok, _, rlog = om.forward(xs[c], c, slots[c], actives[c], c == T - 1, NT)
@@ -159,7 +165,8 @@ def test_model_prefill_matches_sequential_oracle(gpu, mode):
         m.close()
 
 
-def test_model_prefill_equals_per_token_path(gpu):
+@pytest.mark.parametrize("T", [40, 37])
+def test_model_prefill_equals_per_token_path(gpu, T):
     # the batched prefill and T per-token calls leave the same caches (to
     # tolerance) and pick the same final token on a 12B-width layer pair
     cfg = gh.model_config(vocab=4096, hidden=3840, intermediate=15360, layers=2, heads=16,
@@ -168,13 +175,13 @@ def test_model_prefill_equals_per_token_path(gpu):
     b = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=3)
     try:
         ring_a, ring_b = gh.Ring(2, 8, 48, 8), gh.Ring(2, 8, 48, 8)
-        tokens = np.random.default_rng(9).integers(0, cfg.vocab_size, 40)
+        tokens = np.random.default_rng(9).integers(0, cfg.vocab_size, T)
         xs = np.stack([a.embed(int(t)) for t in tokens])
-        slots, actives = ring_lists(ring_a, range(40))
-        a.prefill(xs, np.arange(40), slots, actives, True)
-        for c in range(40):
+        slots, actives = ring_lists(ring_a, range(T))
+        a.prefill(xs, np.arange(T), slots, actives, True)
+        for c in range(T):
             slot = ring_b.activate_slot(0, c)
-            b.forward(xs[c], c, slot, ring_b.active_slots(0, c), c == 39)
+            b.forward(xs[c], c, slot, ring_b.active_slots(0, c), c == T - 1)
         assert_close(a.read(-1, gh.T_LOGITS, np.float32), b.read(-1, gh.T_LOGITS, np.float32),
                      what="prefill vs per-token logits")
         for l in range(2):

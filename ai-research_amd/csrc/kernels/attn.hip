@@ -413,7 +413,8 @@ __device__ __forceinline__ float wave_allsum_swap(float v) {
 // active lists once (entries: slot | token mask << 24, built on the host),
 // so each K/V row it loads serves all PF_GT tokens x G query heads; a token
 // skips the slots its mask bit does not cover.  Requires G <= 2 and D <= 256;
-// the online softmax, wave merge and output follow attn_split.
+// the online softmax, wave merge and output follow attn_split.  The list
+// holds (slot, token mask) pairs; the staging packs each into one word.
 #define PF_GT 4
 #define PF_QN (PF_GT * 2)  // query vectors per workgroup: tokens x heads (G <= 2)
 #define PF_MAXD 256
@@ -433,7 +434,7 @@ __device__ __forceinline__ void attn_pf_group(const AttnArgs& a) {
   const uint32_t S = a.n_active[grp];
   const uint32_t* list = a.active + (size_t)grp * a.active_stride;
   const uint32_t n0 = min(S, (uint32_t)ATT_CHUNK);
-  const uint32_t idx0 = tid < n0 ? list[tid] : 0u;  // ATT_CHUNK == ATT_NT
+  const uint32_t idx0 = tid < n0 ? list[2 * tid] | list[2 * tid + 1] << 24 : 0u;
 
   // 1. the group's query vectors (token i, head g at qs[i * G + g]) into LDS
   for (uint32_t i = tid; i < qn_used * D; i += ATT_NT) {
@@ -465,7 +466,8 @@ __device__ __forceinline__ void attn_pf_group(const AttnArgs& a) {
     const uint32_t n = min(S - r0, (uint32_t)ATT_CHUNK);
     if (r0 != 0) {
       __syncthreads();
-      for (uint32_t t = tid; t < n; t += ATT_NT) sidx[t] = list[r0 + t];
+      for (uint32_t t = tid; t < n; t += ATT_NT)
+        sidx[t] = list[2 * (r0 + t)] | list[2 * (r0 + t) + 1] << 24;
       __syncthreads();
     }
     for (uint32_t base = wave * TT; base < n; base += ATT_WAVES * TT) {
@@ -655,5 +657,225 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a)
     r.z = ((a0.z + a1.z) + (a2.z + a3.z)) * inv;
     r.w = ((a0.w + a1.w) + (a2.w + a3.w)) * inv;
     *reinterpret_cast<float4*>(a.out + (size_t)h * D + col * 4) = r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Matrix-core batched prefill attention, head_dim 256, fp32 throughout.
+//
+// Grid (kv heads, token groups), group ngroups-1-blockIdx.y first.  A group
+// is 16 / G consecutive tokens, so its query vectors form 16 columns (column
+// c: token c / G, head c % G); the host's union list holds (slot, token mask)
+// pairs.  The four waves take the union's 16-slot tiles in turn, and per tile
+//   S^T (16 slots x 16 columns) = K . Q^T      64 x v_mfma_f32_16x16x4_f32
+//   O^T (256 dims x 16 columns) += V^T . P^T   64 x v_mfma_f32_16x16x4_f32
+// with the online softmax in between.  Operand mapping (lane l, column
+// l % 16, lane group l / 16):
+//   K . Q^T: the k index of step (j, c) is dim (l/16)*64 + 4j + c, so a lane
+//     loads 64 contiguous floats of its K row (slot l % 16 of the tile) and
+//     reads the same dims of column l % 16's query from LDS.  The result
+//     lands as S[column l % 16][slot 4*(l/16) + r], r = 0..3 --
+//   which is the B operand of V^T . P^T when the k index of step r is slot
+//     4*(l/16) + r: the probabilities feed the second product without a
+//     shuffle.  Its A operand row i of output tile t is dim 16 i + t, so a
+//     lane loads 16 contiguous floats (dims 16*(l%16) ..) of each of its 4
+//     V rows; the result O[column l%16][16*(4*(l/16) + r) + t] sits in o[t][r].
+// The row max and row sum of the softmax reduce over r in the lane and over
+// the 4 lane groups with lane swaps, so every lane of a column holds the same
+// (m, l).  The waves merge through LDS in wave order and write each token's
+// output rows.  Products and sums are fp32; only the summation order differs
+// from the per-token kernel.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma_f32_4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float swap16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float swap32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+#define PFM_D 256
+struct PfmEntries {
+  uint32_t kslot;     // K row: slot of tile entry l % 16
+  uint32_t vslot[4];  // V rows / scores: tile entries 4*(l/16) + r
+  uint32_t vmask[4];  // their token masks (0 past the end of the list)
+};
+__device__ __forceinline__ void pfm_entries(const uint32_t* list, uint32_t S, uint32_t tile,
+                                            uint32_t col, uint32_t quad, PfmEntries& e) {
+  const uint32_t e0 = tile * 16;
+  e.kslot = list[2 * min(e0 + col, S - 1)];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t i = e0 + 4 * quad + r, ic = min(i, S - 1);
+    e.vslot[r] = list[2 * ic];
+    e.vmask[r] = i < S ? list[2 * ic + 1] : 0u;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(ATT_NT, 2) void gh_pf_attn_m_k(AttnArgs a) {
+  // 64 KB: the query operand (16 steps x 64 lanes of float4) during the
+  // loop, then the waves' o registers ([wave][64 regs][64 lanes]) for the merge
+  __shared__ float4 smem4[ATT_WAVES * 64 * 64 / 4];
+  __shared__ float wm[ATT_WAVES][16], wl[ATT_WAVES][16];
+  float4* qs4 = smem4;
+  float* wo = reinterpret_cast<float*>(smem4);
+
+  const uint32_t G = a.nq / a.nkv;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t col = lane & 15, quad = lane >> 4;
+  const size_t kv_dim = (size_t)a.nkv * PFM_D;
+  const uint32_t kvh = blockIdx.x, grp = gridDim.y - 1 - blockIdx.y;
+  const uint32_t t0 = grp * (16 / G);
+  const uint32_t S = a.n_active[grp];
+  const uint32_t* list = a.active + (size_t)grp * a.active_stride;
+  const uint32_t ntiles = (S + 15) / 16;
+
+  // 1. query columns into LDS in operand order: qs4[j * 64 + l] = dims
+  //    (l/16)*64 + 4j .. +4 of column l % 16 (zeros past the last token)
+  for (uint32_t i = tid; i < 16 * 64; i += ATT_NT) {
+    const uint32_t j = i >> 6, ln = i & 63, c = ln & 15;
+    const uint32_t t = t0 + c / G, g = c % G;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < a.n_tokens)
+      v = *reinterpret_cast<const float4*>(a.q + (size_t)t * a.q_stride +
+                                           (size_t)(kvh * G + g) * PFM_D + (ln >> 4) * 64 + 4 * j);
+    qs4[i] = v;
+  }
+  // entries of this wave's first two tiles (indices clamped into the list, so
+  // every load below is unconditional and in bounds, and masks past the end
+  // are zero)
+  PfmEntries cur, nxt;
+  pfm_entries(list, S, wave, col, quad, cur);
+  pfm_entries(list, S, wave + ATT_WAVES, col, quad, nxt);
+  __syncthreads();
+
+  // 2. the wave's tiles: scores, online softmax, weighted V
+  const uint32_t bit = col / G;  // this column's token within the group
+  f32x4 o[16];
+#pragma unroll
+  for (int t = 0; t < 16; t++) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  const float* kb = a.k_cache + (size_t)kvh * PFM_D + quad * 64;
+  const float* vb = a.v_cache + (size_t)kvh * PFM_D + col * 16;
+  // The first half of tile i + 4's K rows loads while tile i's V . P
+  // products run, the second half at the top of its iteration, and its V
+  // rows once the first half's score products have freed their registers.
+  // This keeps a wave within 256 registers (two waves per SIMD).
+  float4 kr[16], vr[4][4];
+  {
+    const float4* kp = reinterpret_cast<const float4*>(kb + (size_t)cur.kslot * kv_dim);
+#pragma unroll
+    for (int j = 0; j < 8; j++) kr[j] = kp[j];
+  }
+  for (uint32_t tile = wave; tile < ntiles; tile += ATT_WAVES) {
+    {
+      const float4* kp = reinterpret_cast<const float4*>(kb + (size_t)cur.kslot * kv_dim);
+#pragma unroll
+      for (int j = 8; j < 16; j++) kr[j] = kp[j];
+    }
+
+    // four independent accumulation chains (one per float4 component)
+    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0, s2 = s0, s3 = s0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      if (j == 8) {  // the first half's K registers are free: V rows load now
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float4* vp = reinterpret_cast<const float4*>(vb + (size_t)cur.vslot[r] * kv_dim);
+#pragma unroll
+          for (int i = 0; i < 4; i++) vr[r][i] = vp[i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float4 q4 = qs4[j * 64 + lane];
+      s0 = mfma_f32_4(kr[j].x, q4.x, s0);
+      s1 = mfma_f32_4(kr[j].y, q4.y, s1);
+      s2 = mfma_f32_4(kr[j].z, q4.z, s2);
+      s3 = mfma_f32_4(kr[j].w, q4.w, s3);
+    }
+    const f32x4 s = (s0 + s1) + (s2 + s3);
+    __builtin_amdgcn_sched_barrier(0);  // K registers are free from here on
+    {
+      const float4* kp = reinterpret_cast<const float4*>(kb + (size_t)nxt.kslot * kv_dim);
+#pragma unroll
+      for (int j = 0; j < 8; j++) kr[j] = kp[j];
+    }
+    uint32_t vmask[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) vmask[r] = cur.vmask[r];
+    cur = nxt;
+    pfm_entries(list, S, tile + 2 * ATT_WAVES, col, quad, nxt);
+    float sv[4], mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      sv[r] = s[r] * a.scale;
+      if ((vmask[r] >> bit) & 1u) mx = fmaxf(mx, sv[r]);
+    }
+    mx = swap32_max(swap16_max(mx));
+    const float mt = fmaxf(m, mx);
+    const float corr = mt == -INFINITY ? 1.f : __expf(m - mt);  // m = -inf, mt finite: 0
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      p[r] = (vmask[r] >> bit) & 1u ? __expf(sv[r] - mt) : 0.f;
+      ps += p[r];
+    }
+    ps = swap32_add(swap16_add(ps));
+    l = l * corr + ps;
+    m = mt;
+#pragma unroll
+    for (int t = 0; t < 16; t++) o[t] *= corr;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+#pragma unroll
+      for (int t = 0; t < 16; t++) {  // consecutive products into different tiles
+        const float4 v4 = vr[r][t >> 2];
+        const float v = (t & 3) == 0 ? v4.x : (t & 3) == 1 ? v4.y : (t & 3) == 2 ? v4.z : v4.w;
+        o[t] = mfma_f32_4(v, p[r], o[t]);
+      }
+    }
+  }
+
+  // 3. merge the four waves (wave order) and write the output rows
+  __syncthreads();  // every wave is done with the query operand (aliased below)
+#pragma unroll
+  for (int t = 0; t < 16; t++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) wo[(wave * 64 + t * 4 + r) * 64 + lane] = o[t][r];
+  }
+  if (quad == 0) {
+    wm[wave][col] = m;
+    wl[wave][col] = l;
+  }
+  __syncthreads();
+  const uint32_t c = tid >> 4, i = tid & 15;  // output column, dims 16 i .. 16 i + 15
+  const uint32_t t = t0 + c / G, g = c % G;
+  if (t < a.n_tokens) {
+    float M = -INFINITY;
+    for (int w = 0; w < ATT_WAVES; w++) M = fmaxf(M, wm[w][c]);
+    float cw[ATT_WAVES], L = 0.f;
+    for (int w = 0; w < ATT_WAVES; w++) {
+      cw[w] = wm[w][c] == -INFINITY ? 0.f : __expf(wm[w][c] - M);
+      L += wl[w][c] * cw[w];
+    }
+    const uint32_t ln = (i >> 2) * 16 + c, r = i & 3;
+    float res[16];
+#pragma unroll
+    for (int d = 0; d < 16; d++) {
+      float O = 0.f;
+      for (int w = 0; w < ATT_WAVES; w++) O += wo[(w * 64 + d * 4 + r) * 64 + ln] * cw[w];
+      res[d] = L > 0.f ? O / L : 0.f;
+    }
+    float4* dst = reinterpret_cast<float4*>(a.out_rows + (size_t)t * a.out_stride +
+                                            (size_t)(kvh * G + g) * PFM_D + i * 16);
+#pragma unroll
+    for (int j = 0; j < 4; j++) dst[j] = make_float4(res[4 * j], res[4 * j + 1], res[4 * j + 2], res[4 * j + 3]);
   }
 }

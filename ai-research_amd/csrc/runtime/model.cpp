@@ -39,7 +39,7 @@ struct Layer {
 };
 
 constexpr size_t kNone = ~(size_t)0;
-constexpr uint32_t kPfGroup = 4;  // tokens per grouped prefill attention workgroup (PF_GT in attn.hip)
+constexpr uint32_t kPfGroup = 4;  // tokens per gh_pf_attn_g_* workgroup (PF_GT in attn.hip)
 
 }  // namespace
 
@@ -70,11 +70,11 @@ struct gh_model {
   float *pf_xn = nullptr, *pf_attn = nullptr, *pf_act = nullptr;
   float* pf_rs = nullptr;  // row scales of the normed rows (pf_xn holds their fp16 hi/lo planes)
   uint32_t *pf_meta = nullptr, *pf_active = nullptr;
-  // grouped prefill attention: per group of PF_GROUP consecutive tokens, the
-  // union of their active lists (slot | token mask << 24) and its length
+  // grouped prefill attention: per group of pf_gtok consecutive tokens, the
+  // union of their active lists as (slot, token mask) pairs, and its length
   uint32_t *pf_union = nullptr, *pf_ucount = nullptr;
-  uint32_t pf_ustride = 0;
-  bool pf_grouped = false;  // this call's unions are valid
+  uint32_t pf_ustride = 0, pf_gtok = 0;
+  uint32_t pf_gkind = 0;  // this call: 0 per-token kernel, 1 gh_pf_attn_g_*, 2 gh_pf_attn_m_k
 
   template <typename T>
   T* at(size_t off) const {
@@ -663,41 +663,74 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   hipError_t e = hipMemcpyAsync(m->pf_x, x, (size_t)T * c.hidden_size * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(m->pf_meta, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(m->pf_active, act.data(), act.size() * 4, hipMemcpyHostToDevice, s);
-  // union lists of each group of kPfGroup consecutive tokens, in order of
-  // first appearance; a list that names one slot twice keeps every layer on
-  // the per-token kernel (a union entry counts a slot once per token)
-  const uint32_t groups = (T + kPfGroup - 1) / kPfGroup;
-  std::vector<uint32_t> uni((size_t)groups * m->pf_ustride), ucount(groups);
-  m->pf_grouped = c.max_slots <= (1u << 24);
+  // Grouped attention: the matrix-core kernel when every layer has head_dim
+  // 256 and one G = nq / nkv dividing 16 (16 / G tokens per group), else the
+  // 4-token kernel when every layer has G <= 2 and head_dim <= 256, else the
+  // per-token kernel.  The union of a group's lists keeps the order of first
+  // appearance; a list that names one slot twice keeps the per-token kernel
+  // (a union entry counts a slot once per token).
+  uint32_t gkind = 0, gtok = 0;
   {
+    bool all256 = true, small = true, sameG = true;
+    uint32_t G0 = 0;
+    for (auto& L : m->layers) {
+      const uint32_t G = c.num_attention_heads / L.nkv;
+      if (G0 == 0) G0 = G;
+      sameG = sameG && G == G0;
+      all256 = all256 && L.head_dim == 256;
+      small = small && G <= 2 && L.head_dim <= 256;
+    }
+    if (all256 && sameG && G0 >= 1 && G0 <= 16 && 16 % G0 == 0) {
+      gkind = 2;
+      gtok = 16 / G0;
+    } else if (small && c.max_slots <= (1u << 24)) {
+      gkind = 1;
+      gtok = kPfGroup;
+    }
+  }
+  m->pf_gkind = 0;
+  std::vector<uint32_t> uni, ucount;
+  if (gkind) {
+    const uint32_t groups = (T + gtok - 1) / gtok;
+    const uint32_t ustride = std::min(gtok * m->pf_stride, c.max_slots);
+    uni.assign((size_t)groups * ustride * 2, 0u);
+    ucount.assign(groups, 0u);
     std::vector<uint32_t> stamp(c.max_slots, 0u), pos(c.max_slots);
-    for (uint32_t g = 0; g < groups && m->pf_grouped; g++) {
-      uint32_t* u = &uni[(size_t)g * m->pf_ustride];
+    bool ok = true;
+    for (uint32_t g = 0; g < groups && ok; g++) {
+      uint32_t* u = &uni[(size_t)g * ustride * 2];
       uint32_t n = 0;
-      for (uint32_t i = 0; i < kPfGroup && g * kPfGroup + i < T && m->pf_grouped; i++) {
-        const uint32_t t = g * kPfGroup + i;
+      for (uint32_t i = 0; i < gtok && g * gtok + i < T && ok; i++) {
+        const uint32_t t = g * gtok + i;
         const uint32_t* row = active + (size_t)t * active_stride;
         for (uint32_t k = 0; k < n_active[t]; k++) {
           const uint32_t slot = row[k];
           if (stamp[slot] != g + 1) {
             stamp[slot] = g + 1;
             pos[slot] = n;
-            u[n++] = slot | (1u << (24 + i));
-          } else if (u[pos[slot]] & (1u << (24 + i))) {
-            m->pf_grouped = false;
+            u[2 * n] = slot;
+            u[2 * n + 1] = 1u << i;
+            n++;
+          } else if ((u[2 * pos[slot] + 1] >> i) & 1u) {
+            ok = false;
             break;
           } else {
-            u[pos[slot]] |= 1u << (24 + i);
+            u[2 * pos[slot] + 1] |= 1u << i;
           }
         }
       }
       ucount[g] = n;
     }
+    if (ok) {
+      m->pf_gkind = gkind;
+      m->pf_gtok = gtok;
+      m->pf_ustride = ustride;
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(m->pf_union, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, s);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(m->pf_ucount, ucount.data(), ucount.size() * 4, hipMemcpyHostToDevice, s);
+    }
   }
-  if (m->pf_grouped && e == hipSuccess)
-    e = hipMemcpyAsync(m->pf_union, uni.data(), uni.size() * 4, hipMemcpyHostToDevice, s);
-  if (m->pf_grouped && e == hipSuccess)
-    e = hipMemcpyAsync(m->pf_ucount, ucount.data(), ucount.size() * 4, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: input copies");
   if ((st = prefill_forward(m, T, want_logits != 0)) != GH_OK) return st;
   if (want_logits) {
@@ -752,9 +785,8 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   const size_t o_xn = take((size_t)T * H * 4), o_attn = take((size_t)T * m->max_q * 4);
   const size_t o_act = take((size_t)T * I * 4), o_meta = take((size_t)3 * T * 4);
   const size_t o_active = take((size_t)T * stride * 4), o_rs = take((size_t)T * 4);
-  const uint32_t groups = (T + kPfGroup - 1) / kPfGroup;
-  const uint32_t ustride = std::min(kPfGroup * stride, c.max_slots);
-  const size_t o_union = take((size_t)groups * ustride * 4), o_ucount = take((size_t)groups * 4);
+  // unions: at most ceil(T / g) groups of min(g * stride, max_slots) pairs, g <= 16
+  const size_t o_union = take((size_t)(T + 15) * stride * 8), o_ucount = take((size_t)T * 4);
   if (m->pf_arena) {
     hipStreamSynchronize(m->ctx->stream);
     hipFree(m->pf_arena);
@@ -777,7 +809,6 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   m->pf_rs = f32(o_rs);
   m->pf_union = u32(o_union);
   m->pf_ucount = u32(o_ucount);
-  m->pf_ustride = ustride;
   m->pf_cap = T;
   m->pf_stride = stride;
   return GH_OK;
@@ -850,17 +881,19 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
         return st;
     }
     {
-      const uint32_t D = L.head_dim, G = a.nq / a.nkv;
+      const uint32_t D = L.head_dim;
       void* args[] = {&a};
-      if (m->pf_grouped && G <= 2 && D <= 256) {
-        // one workgroup per (kv head, group of kPfGroup tokens) over the union list
+      if (m->pf_gkind != 0) {
+        // one workgroup per (kv head, group of pf_gtok tokens) over the union list
         a.active = m->pf_union;
         a.n_active = m->pf_ucount;
-        a.active_stride = m->pf_ustride;
+        a.active_stride = 2 * m->pf_ustride;
         a.n_tokens = T;
-        const char* name = D <= 64 ? "gh_pf_attn_g_d1_k" : D <= 128 ? "gh_pf_attn_g_d2_k"
-                                                                    : "gh_pf_attn_g_d4_k";
-        const uint32_t groups = (T + kPfGroup - 1) / kPfGroup;
+        const char* name = m->pf_gkind == 2 ? "gh_pf_attn_m_k"
+                           : D <= 64        ? "gh_pf_attn_g_d1_k"
+                           : D <= 128       ? "gh_pf_attn_g_d2_k"
+                                            : "gh_pf_attn_g_d4_k";
+        const uint32_t groups = (T + m->pf_gtok - 1) / m->pf_gtok;
         if ((st = ctx->launch(name, dim3(a.nkv, groups), dim3(256), 0, args)) != GH_OK) return st;
       } else {
         const char* name = D <= 64 ? "gh_pf_attn_d1_k"

@@ -663,7 +663,7 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a)
 // ---------------------------------------------------------------------------
 // Matrix-core batched prefill attention, head_dim 256, fp32 throughout.
 //
-// Grid (kv heads, token groups), group ngroups-1-blockIdx.y first.  A group
+// Grid (kv heads, token groups), long and short groups paired.  A group
 // is 16 / G consecutive tokens, so its query vectors form 16 columns (column
 // c: token c / G, head c % G); the host's union list holds (slot, token mask)
 // pairs.  The four waves take the union's 16-slot tiles in turn, and per tile
@@ -730,7 +730,11 @@ extern "C" __global__ __launch_bounds__(ATT_NT, 2) void gh_pf_attn_m_k(AttnArgs 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t col = lane & 15, quad = lane >> 4;
   const size_t kv_dim = (size_t)a.nkv * PFM_D;
-  const uint32_t kvh = blockIdx.x, grp = gridDim.y - 1 - blockIdx.y;
+  // group order: the first half of blockIdx.y runs the longest groups in
+  // descending order, the second half the shortest in ascending order, so the
+  // workgroups y and y + half that share a CU sum to about the same work
+  const uint32_t gy = gridDim.y, half = (gy + 1) / 2, y = blockIdx.y;
+  const uint32_t kvh = blockIdx.x, grp = y < half ? gy - 1 - y : y - half;
   const uint32_t t0 = grp * (16 / G);
   const uint32_t S = a.n_active[grp];
   const uint32_t* list = a.active + (size_t)grp * a.active_stride;

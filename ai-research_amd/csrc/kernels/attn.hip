@@ -19,6 +19,13 @@
 // once per tile.  Waves merge through LDS; each split writes (o, m, l); the
 // merge kernel combines the splits in split order, so the result does not
 // depend on scheduling.
+//
+// Batched prefill: gh_pf_qkv_rope_k (norm + RoPE + cache write for T tokens),
+// then one of three attention kernels, chosen by the host: gh_pf_attn_m_k
+// (matrix cores, head_dim 256: 16 query columns of consecutive tokens per
+// workgroup over the union of their active lists), gh_pf_attn_g_d*_k (4
+// tokens per workgroup on the vector ALUs), gh_pf_attn_d*_k (one token per
+// workgroup, attn_split over its own list).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

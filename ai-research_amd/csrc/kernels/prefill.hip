@@ -441,6 +441,8 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 //   mode 1: xn = RMSNorm(x) * w
 //   mode 2: x <- (x + RMSNorm(r) * wr) * s  (r as given when wr is null),
 //           stored back as the residual stream; xn = RMSNorm(x) * w
+// In mode 2, r may arrive as rz unsummed K-split planes of a GEMM ([rz][T][H]);
+// they are added in plane order, as gh_pf_splitk_k adds them.
 // One workgroup per token row.
 // ---------------------------------------------------------------------------
 template <int NT>
@@ -480,7 +482,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 
 extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     float* X, const float* R, const float* wr, const float* w, _Float16* Xa,
-    float* rs, uint32_t H, float s, float eps, uint32_t mode, uint32_t perm) {
+    float* rs, uint32_t H, float s, float eps, uint32_t mode, uint32_t perm, uint32_t rz) {
   __shared__ float red[PF_NORM_NT / 64];
   // thread t owns the 8-element group t of the row (H <= 8 * PF_NORM_NT)
   const uint32_t t = blockIdx.x, tid = threadIdx.x, n8 = H / 8;
@@ -501,6 +503,13 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
   load8(w, wv);
   load8(wrp, wrv);
   if (add) {
+    const size_t plane = (size_t)gridDim.x * H;
+    for (uint32_t z = 1; z < rz; z++) {
+      float pv[8];
+      load8(r + z * plane, pv);
+#pragma unroll
+      for (int k = 0; k < 8; k++) rv[k] += pv[k];
+    }
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k++) ss += rv[k] * rv[k];

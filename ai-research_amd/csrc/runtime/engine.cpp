@@ -315,7 +315,8 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
 
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
                                     const void* W1, const void* Ax, const float* rs, float* C,
-                                    uint32_t T, uint32_t N, uint32_t K) {
+                                    uint32_t T, uint32_t N, uint32_t K, const float** planes,
+                                    uint32_t* nplanes) {
   if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
     return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4 or Q8");
   if (!W0 || !Ax || !rs || !C || T == 0 || N == 0 || K == 0)
@@ -326,6 +327,7 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
       (W1 && (reinterpret_cast<uintptr_t>(W1) & 3)))
     return fail(GH_ERR_INVALID, "prefill GEMM: A halves must be 16-byte and W 4-byte aligned");
   const bool pair = W1 != nullptr;
+  if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
   // products of at least 128 tokens) when splitting K lifts it to that
@@ -371,7 +373,11 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                     &out, &T, &N, &K};
     st = ctx->launch(name, grid, dim3(256), 0, args);
   }
-  if (st != GH_OK || nz == 1) return st;
+  if (planes) {
+    *planes = nz > 1 ? out : C;
+    *nplanes = nz;
+  }
+  if (st != GH_OK || nz == 1 || planes) return st;
   const uint64_t tn = (uint64_t)T * N;
   const unsigned rgrid = (unsigned)std::min<uint64_t>((tn + 255) / 256, 4ull * cus);
   void* rargs[] = {&out, &C, &T, &N, &nz, const_cast<uint32_t*>(&nmat)};
@@ -382,7 +388,8 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
 // (gh_pf_halves_k, once per row rather than in every tile that reads it),
 // then the GEMM.
 gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
-                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K) {
+                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K,
+                              const float** planes, uint32_t* nplanes) {
   if (!A || T == 0 || K == 0 || K % 32 != 0) return fail(GH_ERR_INVALID, "prefill GEMM: bad A");
   if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
   if (reinterpret_cast<uintptr_t>(A) & 15) return fail(GH_ERR_INVALID, "prefill GEMM: A must be 16-byte aligned");
@@ -396,7 +403,7 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   uint32_t perm = mode == GH_QUANT_Q4 ? 1u : 0u;  // K order of the Q4 unpacking
   void* args[] = {const_cast<float**>(&A), &Ax, &rs, &K, &perm};
   if ((st = ctx->launch("gh_pf_halves_k", dim3(T), dim3(1024), 0, args)) != GH_OK) return st;
-  return launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, T, N, K);
+  return launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes);
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {

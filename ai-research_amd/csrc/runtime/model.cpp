@@ -814,9 +814,10 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   return GH_OK;
 }
 
-// gh_pf_norm_k over T rows (mode 1: RMSNorm; mode 2: residual add + RMSNorm).
+// gh_pf_norm_k over T rows (mode 1: RMSNorm; mode 2: residual add + RMSNorm,
+// the residual R given as rz unsummed K-split planes [rz][T][H]).
 gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* wr,
-                         const float* w, float s, uint32_t mode) {
+                         const float* w, float s, uint32_t mode, uint32_t rz = 1) {
   uint32_t H = m->cfg.hidden_size;
   float eps = m->cfg.rms_norm_eps;
   float* X = m->pf_x;
@@ -825,7 +826,7 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   float* rs = m->pf_rs;
   uint32_t perm = m->mode == GH_QUANT_Q4 ? 1u : 0u;  // K order of the Q4 unpacking
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
-                  &Xa, &rs, &H, &s, &eps, &mode, &perm};
+                  &Xa, &rs, &H, &s, &eps, &mode, &perm, &rz};
   return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
 }
 
@@ -837,6 +838,10 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
   uint32_t* clocks = m->pf_meta;
   uint32_t* slots = m->pf_meta + T;
   uint32_t* nact = m->pf_meta + 2 * T;
+  // the down projection's output as the next layer's norm reads it: its
+  // K-split planes, summed by that norm (the last layer's is summed in place)
+  const float* m_planes = m->pf_m;
+  uint32_t m_nz = 1;
   for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& L = m->layers[l];
     // 1. xn = norm(x) (layer 0: RMSNorm; later: post-FFN add + layer scalar + norm)
@@ -844,8 +849,8 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
       st = launch_pf_norm(m, T, nullptr, nullptr, m->at<float>(L.input_norm), 1.0f, 1);
     } else {
       const Layer& P = m->layers[l - 1];
-      st = launch_pf_norm(m, T, m->pf_m, P.post_ffn == kNone ? nullptr : m->at<float>(P.post_ffn),
-                          m->at<float>(L.input_norm), P.scalar, 2);
+      st = launch_pf_norm(m, T, m_planes, P.post_ffn == kNone ? nullptr : m->at<float>(P.post_ffn),
+                          m->at<float>(L.input_norm), P.scalar, 2, m_nz);
     }
     if (st != GH_OK) return st;
     // 2. [q|k|v] rows of every token
@@ -902,22 +907,29 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
         if ((st = ctx->launch(name, dim3(a.nkv, T), dim3(256), 0, args)) != GH_OK) return st;
       }
     }
-    // 4. o = W_o . attn
+    // 4. o = W_o . attn (a K split stays unsummed: the norm below adds the planes)
+    const float* o_planes = nullptr;
+    uint32_t o_nz = 1;
     if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.o), nullptr, m->pf_attn,
-                                      m->pf_o, T, H, L.q_dim)) != GH_OK)
+                                      m->pf_o, T, H, L.q_dim, &o_planes, &o_nz)) != GH_OK)
       return st;
     // 5. x += post_attn_norm(o); act = geglu(W_gate, W_up . pre_ffn_norm(x))
-    if ((st = launch_pf_norm(m, T, m->pf_o,
+    if ((st = launch_pf_norm(m, T, o_planes,
                              L.post_attn == kNone ? nullptr : m->at<float>(L.post_attn),
-                             m->at<float>(L.pre_ffn), 1.0f, 2)) != GH_OK)
+                             m->at<float>(L.pre_ffn), 1.0f, 2, o_nz)) != GH_OK)
       return st;
     if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.gate),
                                             m->at<uint8_t>(L.up), xh, m->pf_rs, m->pf_act, T,
                                             I, H)) != GH_OK)
       return st;
-    // 6. m = W_down . act
+    // 6. m = W_down . act (unsummed planes for the next layer's norm; the last
+    //    layer's m is summed into pf_m for the LM-head prologue)
+    const bool last = l + 1 == c.num_hidden_layers;
+    m_planes = m->pf_m;
+    m_nz = 1;
     if ((st = gh::launch_prefill_gemm(ctx, m->mode, m->at<uint8_t>(L.down), nullptr, m->pf_act,
-                                      m->pf_m, T, H, I)) != GH_OK)
+                                      m->pf_m, T, H, I, last ? nullptr : &m_planes,
+                                      last ? nullptr : &m_nz)) != GH_OK)
       return st;
   }
   if (want_logits) {

@@ -78,14 +78,20 @@ gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
 // Prefill MFMA GEMM (prefill.hip): C [T][N] = A [T][K] . deq(W0)^T, or with
 // W1, C = gelu_tanh(A . deq(W0)^T) * (A . deq(W1)^T); A and C f32.
+// A single product (W1 null) may leave a K split unsummed: with planes
+// given, *planes/*nplanes receive the partial planes ([nplanes][T][N] f32, in
+// the context's GEMM scratch, valid until the next split GEMM) and C is not
+// written; an unsplit product writes C and returns (C, 1).
 gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W0, const void* W1,
-                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K);
+                              const float* A, float* C, uint32_t T, uint32_t N, uint32_t K,
+                              const float** planes = nullptr, uint32_t* nplanes = nullptr);
 // The same with A given as its fp16 hi/lo halves Ax ([T][2K], the hi and lo
 // halves of each 32-element block side by side) and row scales rs
 // (A = rs[t] (hi + lo)), as gh_pf_norm_k / gh_pf_halves_k write them.
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
                                     const void* W1, const void* Ax, const float* rs, float* C,
-                                    uint32_t T, uint32_t N, uint32_t K);
+                                    uint32_t T, uint32_t N, uint32_t K,
+                                    const float** planes = nullptr, uint32_t* nplanes = nullptr);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);
 }  // namespace gh

@@ -590,6 +590,67 @@ extern "C" __global__ __launch_bounds__(64) void gh_pf_qkv_rope_k(AttnArgs a,
   for (uint32_t d = lane; d < D; d += 64) vc[d] = vin[d] * vinv;
 }
 
+// The same for head_dim 256, one workgroup per token (grid (tokens), 256
+// threads): a token's head rows are jobs -- query heads [0, nq), key heads
+// [nq, nq + nkv), value heads after them -- and wave w takes jobs w, w + 4, ...
+// Every job's row (4 floats per lane) loads before any is used, the RoPE
+// angles are computed once per wave rather than once per head, and each head
+// is normalised in registers, rotated through the wave's LDS row
+// (rope_lds), and stored: q in place, k and v into the caches at slots[t].
+#define PFR_JOBS 16  // jobs per wave: nq + 2 nkv <= 64
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs a,
+                                                                      const uint32_t* clocks,
+                                                                      const uint32_t* slots) {
+  __shared__ float hb[ATT_WAVES][256];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t clock = clocks[t], slot = slots[t];
+  float* row = const_cast<float*>(a.q) + (size_t)t * a.q_stride;
+  const uint32_t nq = a.nq, nkv = a.nkv, njobs = nq + 2 * nkv;
+  const uint32_t per = (njobs + ATT_WAVES - 1) / ATT_WAVES;  // the same for every wave
+  const size_t q_dim = (size_t)nq * 256, kv_dim = (size_t)nkv * 256;
+  auto src = [&](uint32_t j) -> const float* {
+    if (j < nq) return row + (size_t)j * 256;
+    if (j < nq + nkv) return row + q_dim + (size_t)(j - nq) * 256;
+    return (a.k_eq_v ? row + q_dim : row + q_dim + kv_dim) + (size_t)(j - nq - nkv) * 256;
+  };
+  const uint32_t d0 = lane * 4;
+  float4 v[PFR_JOBS];
+#pragma unroll
+  for (int i = 0; i < PFR_JOBS; i++) {
+    const uint32_t j = min(wave + ATT_WAVES * (uint32_t)i, njobs - 1);
+    v[i] = *reinterpret_cast<const float4*>(src(j) + d0);
+  }
+  const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);  // a missing norm weight
+  const float4 wq = a.q_norm ? *reinterpret_cast<const float4*>(a.q_norm + d0) : one;
+  const float4 wk = a.k_norm ? *reinterpret_cast<const float4*>(a.k_norm + d0) : one;
+  float rc[ROPE_K], rsn[ROPE_K];
+  rope_angles(a.rot, a.theta, clock, lane, rc, rsn);
+  float* h = hb[wave];
+#pragma unroll
+  for (int i = 0; i < PFR_JOBS; i++) {
+    if ((uint32_t)i < per) {  // per is the same for the whole workgroup
+      const uint32_t j = wave + ATT_WAVES * (uint32_t)i;
+      const bool isq = j < nq, isk = !isq && j < nq + nkv;
+      const float4 x = v[i];
+      const float ss = wave_allsum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
+      const float inv = 1.0f / sqrtf(ss / 256.0f + a.eps);
+      const float4 w = isq ? wq : isk ? wk : one;
+      *reinterpret_cast<float4*>(h + d0) =
+          make_float4(x.x * inv * w.x, x.y * inv * w.y, x.z * inv * w.z, x.w * inv * w.w);
+      __syncthreads();
+      if (isq || isk) rope_lds(h, a.rot, rc, rsn, lane);
+      __syncthreads();
+      const float4 y = *reinterpret_cast<const float4*>(h + d0);
+      if (j < njobs) {
+        float* dst = isq ? row + (size_t)j * 256
+                     : isk ? a.k_cache + (size_t)slot * kv_dim + (size_t)(j - nq) * 256
+                           : a.v_cache + (size_t)slot * kv_dim + (size_t)(j - nq - nkv) * 256;
+        *reinterpret_cast<float4*>(dst + d0) = y;
+      }
+    }
+  }
+}
+
 // Combine the split partials of one query head:
 // out = sum_s exp(m_s - M) o_s / sum_s exp(m_s - M) l_s.  One workgroup of
 // 256 threads per query head; wave w takes splits w, w + 4, ...  Every load

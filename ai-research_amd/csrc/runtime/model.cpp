@@ -882,8 +882,12 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     a.out_stride = L.q_dim;
     {
       void* args[] = {&a, &clocks, &slots};
-      if ((st = ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args)) != GH_OK)
-        return st;
+      // head_dim 256: one workgroup per token (angles once per wave); else one
+      // wavefront per (head, token)
+      st = L.head_dim == 256 && a.nq + 2 * a.nkv <= 64
+               ? ctx->launch("gh_pf_qkv_rope4_k", dim3(T), dim3(256), 0, args)
+               : ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args);
+      if (st != GH_OK) return st;
     }
     {
       const uint32_t D = L.head_dim;

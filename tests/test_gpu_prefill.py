@@ -194,6 +194,44 @@ def test_model_prefill_equals_per_token_path(gpu, T):
         b.close()
 
 
+@pytest.mark.parametrize("shape", ["12b", "tiny"])
+def test_model_prefill_windowed_lists(gpu, shape):
+    # explicit lists with a sliding window (slot 0 as an anchor plus the last
+    # 10 slots): within a token group the later tokens drop slots the earlier
+    # ones still attend to, so the grouped attention's token masks decide which
+    # union entries each token uses; checked against T per-token calls with the
+    # same lists, at 12B width (head_dim 256: the matrix-core kernel) and on the
+    # tiny model (head_dim 64/128: the 4-token vector-ALU kernel)
+    if shape == "12b":
+        cfg = gh.model_config(vocab=4096, hidden=3840, intermediate=15360, layers=1, heads=16,
+                              kv_heads=8, head_dim=256, max_slots=64, full_layers=())
+        T = 29
+    else:
+        cfg = tiny_cfg()
+        T = 21
+    a = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=4)
+    b = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=4)
+    try:
+        tokens = np.random.default_rng(13).integers(0, cfg.vocab_size, T)
+        xs = np.stack([a.embed(int(t)) for t in tokens])
+        slots = list(range(T))
+        actives = [np.array(sorted({0} | set(range(max(0, t - 9), t + 1))), np.uint32)
+                   for t in range(T)]
+        a.prefill(xs, np.arange(T), slots, actives, True)
+        for c in range(T):
+            b.forward(xs[c], c, slots[c], actives[c], c == T - 1)
+        assert_close(a.read(-1, gh.T_LOGITS, np.float32), b.read(-1, gh.T_LOGITS, np.float32),
+                     what="windowed prefill vs per-token logits")
+        for l in range(cfg.num_hidden_layers):
+            for t in (gh.T_K_CACHE, gh.T_V_CACHE):
+                ka = a.read(l, t, np.float32).reshape(cfg.max_slots, -1)[slots]
+                kb = b.read(l, t, np.float32).reshape(cfg.max_slots, -1)[slots]
+                assert_close(ka, kb, what="windowed prefill vs per-token cache %d/%d" % (l, t))
+    finally:
+        a.close()
+        b.close()
+
+
 def test_model_prefill_rejects_slot_reuse(gpu):
     cfg = tiny_cfg(layers=1, full_layers=())
     m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=2)

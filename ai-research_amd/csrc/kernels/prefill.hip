@@ -317,8 +317,10 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
 #define GH_PF_OCC_64
 #define GH_GEMM_ALL                                                       \
   GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, 1, false, )             \
+  GH_GEMM(gh_pf_gemm_q4_m128_n64, Q4W, 128, 64, 1, false, )               \
   GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, 1, false, )                 \
   GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, 1, false, )             \
+  GH_GEMM(gh_pf_gemm_q8_m128_n64, Q8W, 128, 64, 1, false, )               \
   GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, false, )                 \
   GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, 1, false, )        \
   GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, false, )          \

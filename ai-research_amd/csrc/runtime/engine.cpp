@@ -336,7 +336,12 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   const bool big_split = !pair && T >= 128 && tiles_big < cus && 4 * tiles_big >= cus &&
                          getenv("GH_PF_NO_BIG_SPLIT") == nullptr;
   const bool big = tiles_big >= cus || big_split;
-  const uint32_t bm = big ? 128 : 64, bn = big ? bn_big : 64;
+  // a plain product whose 128x128 tiles give each CU only one workgroup (the
+  // QKV projection of 512 tokens: 256 tiles) takes 128x64 tiles, two per CU
+  const uint32_t tiles_n64 = ((N + 63) / 64) * ((T + 127) / 128);
+  const bool narrow = !pair && big && !big_split && tiles_big < 2 * cus && tiles_n64 >= 2 * cus &&
+                      getenv("GH_PF_NO_N64") == nullptr;
+  const uint32_t bm = big ? 128 : 64, bn = big ? (narrow ? 64 : bn_big) : 64;
   std::string name = std::string(pair ? "gh_pf_gateup_" : "gh_pf_gemm_") +
                      (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
                      std::to_string(bn) + "_k1";

@@ -352,7 +352,8 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   const uint32_t tiles = grid.x * grid.y, nsteps = K / 32;
   uint32_t nz = 1;
   if (!big && tiles < cus) nz = std::min<uint32_t>((2 * cus + tiles - 1) / tiles, std::max(1u, nsteps / 8));
-  if (big_split) nz = std::min<uint32_t>((cus + tiles - 1) / tiles, std::max(1u, nsteps / 8));
+  // large tiles: as many splits as keep every workgroup resident (two per CU)
+  if (big_split) nz = std::min<uint32_t>(std::max(1u, 2 * cus / tiles), std::max(1u, nsteps / 8));
   if (const char* env = getenv("GH_PF_SPLIT")) {
     const int v = atoi(env);
     if (v >= 1 && (!big || big_split)) nz = std::min<uint32_t>((uint32_t)v, nsteps);

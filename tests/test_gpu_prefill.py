@@ -195,15 +195,22 @@ def test_model_prefill_equals_per_token_path(gpu, T):
         b.close()
 
 
-@pytest.mark.parametrize("shape", ["12b", "tiny"])
+@pytest.mark.parametrize("shape", ["12b", "tiny", "g4", "g1"])
 def test_model_prefill_windowed_lists(gpu, shape):
     # explicit lists with a sliding window (slot 0 as an anchor plus the last
     # 10 slots): within a token group the later tokens drop slots the earlier
     # ones still attend to, so the grouped attention's token masks decide which
     # union entries each token uses; checked against T per-token calls with the
     # same lists, at 12B width (head_dim 256: the matrix-core kernel) and on the
-    # tiny model (head_dim 64/128: the 4-token vector-ALU kernel)
-    if shape == "12b":
+    # tiny model (head_dim 64/128: the 4-token vector-ALU kernel); g4 and g1
+    # are head_dim-256 models with 4 and 1 query heads per kv head, so the
+    # matrix-core kernel's 16 columns are 4 tokens x 4 heads and 16 tokens x 1
+    if shape == "g4" or shape == "g1":
+        cfg = gh.model_config(vocab=1024, hidden=1024, intermediate=2048, layers=1,
+                              heads=8 if shape == "g4" else 4, kv_heads=2 if shape == "g4" else 4,
+                              head_dim=256, max_slots=64, full_layers=())
+        T = 37
+    elif shape == "12b":
         cfg = gh.model_config(vocab=4096, hidden=3840, intermediate=15360, layers=1, heads=16,
                               kv_heads=8, head_dim=256, max_slots=64, full_layers=())
         T = 29

@@ -282,3 +282,124 @@ def test_qkv_norm_rope_composition():
     _, _, v3 = orc.qkv_norm_rope(q, k, v, qn, kn, nq, nkv, hd, rot, True, 1e4, 1e-6, 37)
     kh = k[:hd].astype(np.float64)
     assert np.allclose(v3[:hd], kh / np.sqrt(np.mean(kh ** 2) + 1e-6), atol=1e-5)
+
+
+# ------------------------------------------------- MLP, embedding, forward ----
+def test_gate_up_and_gated_mlp_fp64():
+    # kernels.zig:94-129: act = gelu_tanh(Wg x) * (Wu x), out = Wd act
+    rng = np.random.default_rng(21)
+    H, I = 256, 384
+    wg, wu, wd = (nr.quantize_q4(nr.bf16_rne(rng.standard_normal(s).astype(np.float32) * 0.05))
+                  for s in ((I, H), (I, H), (H, I)))
+    x = rng.standard_normal(H).astype(np.float32)
+    act = orc.gate_up_geglu_q4(x, wg, wu, 3)
+    g64 = nr.dequant_q4(wg, H) @ x.astype(np.float64)
+    u64 = nr.dequant_q4(wu, H) @ x.astype(np.float64)
+    ref = nr.gelu64(g64) * u64
+    assert np.max(np.abs(act - ref)) / np.max(np.abs(ref)) < 1e-5
+    swapped = nr.gelu64(u64) * g64  # the roles of gate and up matter
+    assert np.max(np.abs(act - swapped)) / np.max(np.abs(ref)) > 1e-2
+    out, act2 = orc.gated_mlp_q4(x, wg, wu, wd, 4)
+    assert np.array_equal(act, act2)
+    ref_out = nr.dequant_q4(wd, I) @ ref
+    assert np.max(np.abs(out - ref_out)) / np.max(np.abs(ref_out)) < 1e-5
+
+
+def test_embed_bits():
+    # forward.zig:33-37: x = bf16(E[token]) * sqrt(f32(H)), one f32 multiply
+    rng = np.random.default_rng(5)
+    V, H = 64, 3840
+    e = nr.bf16_rne(rng.standard_normal((V, H)).astype(np.float32) * 0.02)
+    for t in (0, 17, V - 1):
+        want = nr.bf16_to_f32(e[t]) * np.sqrt(np.float32(H))
+        assert want.dtype == np.float32
+        got = orc.embed(e, t, H)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert not np.array_equal(orc.embed(e, 1, H), orc.embed(e, 2, H))
+
+
+def _tiny_forward_model(mode):
+    """Three layers covering the shape rules: a sliding layer with v_proj, a
+    full-attention layer with attention_k_eq_v (its own head_dim, rotary_dim
+    head_dim / 4, one kv head, no post-attention norm, layer_scalar 0.7) and
+    a sliding layer without v_proj (the key serves as value) with
+    layer_scalar 0.5."""
+    rng = np.random.default_rng(99)
+    H, I, V, nq, slots = 256, 512, 512, 4, 24
+    quant = nr.quantize_q8 if mode == "q8" else nr.quantize_q4
+    mat = lambda r, c: quant(nr.bf16_rne(rng.standard_normal((r, c)).astype(np.float32) * 0.05))  # noqa: E731
+    vec = lambda n: nr.bf16_to_f32(nr.bf16_rne((1 + 0.1 * rng.standard_normal(n)).astype(np.float32)))  # noqa: E731
+    specs = [dict(full=False, head_dim=64, num_kv_heads=2, k_eq_v=False, scalar=1.0, post_attn=True),
+             dict(full=True, head_dim=128, num_kv_heads=1, k_eq_v=True, scalar=0.7, post_attn=False),
+             dict(full=False, head_dim=64, num_kv_heads=2, k_eq_v=True, scalar=0.5, post_attn=True)]
+    layers = []
+    for s in specs:
+        hd, nkv = s["head_dim"], s["num_kv_heads"]
+        qd, kvd = nq * hd, nkv * hd
+        d = dict(full=s["full"], head_dim=hd, rotary_dim=hd // 4 if s["full"] else hd,
+                 num_kv_heads=nkv, k_eq_v=s["k_eq_v"], layer_scalar=s["scalar"],
+                 wq=mat(qd, H), wk=mat(kvd, H), wo=mat(H, qd), wg=mat(I, H), wu=mat(I, H),
+                 wd=mat(H, I), input_norm=vec(H), q_norm=vec(hd), k_norm=vec(hd),
+                 post_attn_norm=vec(H) if s["post_attn"] else None, pre_ffn_norm=vec(H),
+                 post_ffn_norm=vec(H))
+        d["wv"] = d["wk"] if s["k_eq_v"] else mat(kvd, H)
+        k = rng.standard_normal((slots, kvd)).astype(np.float32)
+        v = rng.standard_normal((slots, kvd)).astype(np.float32)
+        v /= np.sqrt(np.mean(v.reshape(slots, nkv, hd) ** 2, axis=2, keepdims=True) + 1e-6).repeat(hd, 2).reshape(slots, kvd)
+        d["k_cache"], d["v_cache"] = k, v
+        layers.append(d)
+    head = nr.quantize_q8(nr.bf16_rne(rng.standard_normal((V, H)).astype(np.float32) * 0.05))
+    fnorm = vec(H)
+    return H, I, V, nq, layers, head, fnorm, rng
+
+
+def _copy_layers(layers):
+    return [dict(d, k_cache=d["k_cache"].copy(), v_cache=d["v_cache"].copy()) for d in layers]
+
+
+@pytest.mark.parametrize("mode", ["q4", "q8"])
+def test_forward_token_matches_fp64_restatement(mode):
+    # orc_forward_token against tests/numpy_ref.forward64, written separately
+    # from forward.zig / model_dispatch.zig: layer order, norm placement, the
+    # layer scalar, gate/up roles, k_eq_v / missing v_proj, partial RoPE per
+    # layer type, the cache write before attention and the Q8 head.
+    H, I, V, nq, layers, head, fnorm, rng = _tiny_forward_model(mode)
+    om = orc.Model(H, I, V, nq, layers, head, fnorm,
+                   layer_mode=orc.QUANT_Q8 if mode == "q8" else orc.QUANT_Q4)
+    ref_layers = _copy_layers(layers)
+    for clock in (3, 4, 9, 17):
+        slot = clock % 24
+        active = np.unique(np.concatenate([[slot], rng.choice(24, 10, replace=False)])).astype(np.uint32)
+        x = rng.standard_normal(H).astype(np.float32) * 3
+        tok, xo, logits = om.forward(x, clock, slot, active, True, 2)
+        rtok, rx, rlog = nr.forward64(ref_layers, x, clock, slot, active, head, fnorm, nq, mode=mode)
+        assert np.max(np.abs(logits - rlog)) / np.max(np.abs(rlog)) < 1e-5
+        assert np.max(np.abs(xo - rx)) / np.max(np.abs(rx)) < 1e-5
+        srt = np.sort(rlog)
+        if srt[-1] - srt[-2] > 1e-4 * np.max(np.abs(rlog)):
+            assert tok == rtok
+        for d, r in zip(layers, ref_layers):
+            assert np.max(np.abs(d["k_cache"] - r["k_cache"])) < 1e-5
+            assert np.max(np.abs(d["v_cache"] - r["v_cache"])) < 1e-5
+    # the prefill graph (no logits) leaves the same residual stream
+    x = rng.standard_normal(H).astype(np.float32)
+    tok, xo, _ = om.forward(x, 20, 20, np.arange(21, dtype=np.uint32) % 24, False, 1)
+    _, rx, _ = nr.forward64(ref_layers, x, 20, 20, np.arange(21) % 24, head, fnorm, nq, mode=mode,
+                            want_logits=False)
+    assert tok == 0 and np.max(np.abs(xo - rx)) / np.max(np.abs(rx)) < 1e-5
+
+
+@pytest.mark.parametrize("mistake", ["scalar_both_adds", "swap_gate_up", "skip_post_attn", "rope_v",
+                                     "normed_k_as_v", "theta_swap", "attn_scale",
+                                     "write_after_attn", "scalar_before_ffn"])
+def test_forward_restatement_catches_planted_mistakes(mistake):
+    # The comparison above has teeth: each planted mistake in the fp64
+    # restatement moves the logits far beyond its 1e-5 bar.
+    H, I, V, nq, layers, head, fnorm, rng = _tiny_forward_model("q4")
+    om = orc.Model(H, I, V, nq, layers, head, fnorm)
+    bad = _copy_layers(layers)
+    active = np.array([0, 2, 5, 7, 9, 11], np.uint32)
+    x = rng.standard_normal(H).astype(np.float32) * 3
+    _, _, logits = om.forward(x, 7, 7, active, True, 1)
+    _, _, blog = nr.forward64(bad, x, 7, 7, active, head, fnorm, nq, mistake=mistake)
+    assert np.max(np.abs(logits - blog)) / np.max(np.abs(blog)) > 1e-3

@@ -109,3 +109,79 @@ extern "C" __global__ __launch_bounds__(256) void gh_fill_u32_k(uint32_t* dst, u
        i += (uint64_t)gridDim.x * blockDim.x)
     dst[i] = value;
 }
+
+extern "C" __global__ __launch_bounds__(256) void gh_copy_u32_k(uint32_t* dst, const uint32_t* src,
+                                                                uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+// Device-resident ring bookkeeping for one decode token (the layer-0 state of
+// DynamicRingBuffer, src/ring_buffer.zig:56-136, as src/model/forward.zig:42-43
+// uses it).  step = {clock, slot_idx, S, mode}: with mode 1 the kernel
+// activates the clock's slot (activateSlot: clocks[slot] = clock, flag set)
+// and writes slot_idx, S and the active list (getActiveSlots); any other mode
+// leaves the host's slot_idx, S and list, and only records the activation of
+// slot_idx, so that the device state follows host-driven steps too.  The list is the slot-order
+// compaction of one predicate, because the three tiers are contiguous and
+// each tier is listed in slot order:
+//   anchors  s < min(clock + 1, A) and active
+//   window   clock >= A, active, and its clock in [clock - W + 1 (or A), clock]
+//   recall   active and its clock <= clock
+// One workgroup of 1024 threads; slots are taken 1024 at a time, with a
+// ballot prefix per wavefront and the wavefront counts scanned in LDS.
+extern "C" __global__ __launch_bounds__(1024) void gh_ring_step_k(
+    uint32_t* ring_clock, uint32_t* ring_flag, uint32_t* step, uint32_t* active, uint32_t A,
+    uint32_t W, uint32_t R) {
+  __shared__ uint32_t wave_n[16];
+  __shared__ uint32_t base_n;
+  if (step[3] != 1u) {
+    if (threadIdx.x == 0 && step[1] < A + W + R) {
+      ring_clock[step[1]] = step[0];
+      ring_flag[step[1]] = 1u;
+    }
+    return;
+  }
+  const uint32_t c = step[0];
+  const uint32_t slot = c < A ? c : A + (c - A) % W;
+  const uint32_t total = A + W + R;
+  const uint32_t alim = c + 1u < A ? c + 1u : A;
+  const uint32_t minc = c >= W ? c - W + 1u : A;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  if (tid == 0) base_n = 0;
+  __syncthreads();
+  for (uint32_t s0 = 0; s0 < total; s0 += 1024u) {
+    const uint32_t s = s0 + tid;
+    bool on = false;
+    if (s < total) {
+      const bool act = s == slot || ring_flag[s] != 0u;
+      const uint32_t clk = s == slot ? c : ring_clock[s];
+      if (s < A)
+        on = s < alim && act;
+      else if (s < A + W)
+        on = c >= A && act && clk >= minc && clk <= c;
+      else
+        on = act && clk <= c;
+    }
+    const uint64_t mask = __ballot(on);
+    if (lane == 0) wave_n[wave] = (uint32_t)__popcll(mask);
+    __syncthreads();
+    uint32_t off = base_n;
+    for (uint32_t w = 0; w < wave; w++) off += wave_n[w];
+    if (on) active[off + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull))] = s;
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t n = 0;
+      for (uint32_t w = 0; w < 16u; w++) n += wave_n[w];
+      base_n += n;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    ring_clock[slot] = c;
+    ring_flag[slot] = 1u;
+    step[1] = slot;
+    step[2] = base_n;
+  }
+}

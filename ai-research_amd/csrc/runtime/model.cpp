@@ -53,16 +53,29 @@ struct gh_model {
   size_t lm_head = 0, final_norm = 0;
   size_t x0 = 0, x1 = 0, qkv_out = 0, attn_out = 0, o_out = 0, act = 0, m_out = 0, logits = 0;
   size_t token = 0, step = 0, active = 0, attn_part = 0, amax = 0;
+  // The per-token inputs sit in one region, [x0: hidden f32 | step: 4 u32 |
+  // active list], so that one host->device copy carries them (x alone and the
+  // step record when the device ring computes the list).
+  size_t io = 0, io_bytes = 0;
+  // device-resident ring bookkeeping (layer 0): clock and active flag per slot
+  size_t ring_clock = 0, ring_flag = 0;
+  uint32_t ring_a = 0, ring_w = 0, ring_r = 0;
+  gh_ring* ring = nullptr;  // host mirror of the same state (batched prefill lists)
   uint32_t nsplit = 1, max_q = 0, max_kv = 0;
-  size_t hidden_final = 0;       // which x buffer holds the residual stream after a step
+  size_t hidden_decode = 0;      // where the decode graph leaves the final residual
+  size_t hidden_final = 0;       // where the last call left it (kNone: not computed)
   uint16_t* embed_dev = nullptr; // synthetic models only
-  // pinned host staging for the per-token copies
+  // pinned host staging of the io region and the token read-back
+  uint8_t* h_io = nullptr;
   float* h_x = nullptr;
   uint32_t* h_active = nullptr;
   uint32_t* h_step = nullptr;
   uint32_t* h_token = nullptr;
   void* graph_decode = nullptr;
   void* graph_prefill = nullptr;
+  // per-layer residual trace: row l = layer l's input, row L = the final residual
+  float* trace = nullptr;
+  bool trace_on = false;
   // batched prefill buffers (gh_model_prefill), sized for pf_cap tokens
   uint32_t pf_cap = 0, pf_stride = 0;
   uint8_t* pf_arena = nullptr;
@@ -98,10 +111,10 @@ gh_model::~gh_model() {
   if (arena) hipFree(arena);
   if (pf_arena) hipFree(pf_arena);
   if (embed_dev) hipFree(embed_dev);
-  if (h_x) hipHostFree(h_x);
-  if (h_active) hipHostFree(h_active);
-  if (h_step) hipHostFree(h_step);
+  if (trace) hipFree(trace);
+  if (h_io) hipHostFree(h_io);
   if (h_token) hipHostFree(h_token);
+  if (ring) gh_ring_destroy(ring);
 }
 
 namespace {
@@ -172,8 +185,14 @@ gh_status plan(gh_model* m) {
   }
   m->lm_head = take((size_t)V * (H / 32) * 36);
   m->final_norm = take(H * 4);
-  m->x0 = take(H * 4);
+  m->io_bytes = align_up((size_t)H * 4, 256) + 64 + (size_t)c.max_slots * 4;
+  m->io = take(m->io_bytes);
+  m->x0 = m->io;
+  m->step = m->io + align_up((size_t)H * 4, 256);
+  m->active = m->step + 64;
   m->x1 = take(H * 4);
+  m->ring_clock = take((size_t)c.max_slots * 4);
+  m->ring_flag = take((size_t)c.max_slots * 4);
   uint32_t max_qkv = 0;
   for (auto& L : m->layers) max_qkv = std::max(max_qkv, L.qkv_rows);
   m->qkv_out = take((size_t)max_qkv * 4);
@@ -183,8 +202,6 @@ gh_status plan(gh_model* m) {
   m->m_out = take(H * 4);
   m->logits = take((size_t)V * 4);
   m->token = take(64);
-  m->step = take(64);
-  m->active = take((size_t)c.max_slots * 4);
   uint32_t max_nkv = 0, max_g = 1, max_d = 0;
   for (auto& L : m->layers) {
     max_nkv = std::max(max_nkv, L.nkv);
@@ -203,13 +220,14 @@ gh_status alloc_all(gh_model* m) {
   if (e != hipSuccess)
     return fail(GH_ERR_ALLOC, "model arena (" + std::to_string(m->arena_bytes >> 20) +
                                   " MiB): " + hipGetErrorString(e));
-  e = hipHostMalloc(&m->h_x, m->cfg.hidden_size * 4);
-  if (e == hipSuccess) e = hipHostMalloc(&m->h_active, (size_t)m->cfg.max_slots * 4);
-  if (e == hipSuccess) e = hipHostMalloc(&m->h_step, 64);
+  e = hipHostMalloc(&m->h_io, m->io_bytes);
   if (e == hipSuccess) e = hipHostMalloc(&m->h_token, 64);
   if (e != hipSuccess) return fail(GH_ERR_ALLOC, std::string("pinned staging: ") + hipGetErrorString(e));
-  memset(m->h_step, 0, 64);
+  memset(m->h_io, 0, m->io_bytes);
   memset(m->h_token, 0, 64);
+  m->h_x = reinterpret_cast<float*>(m->h_io);
+  m->h_step = reinterpret_cast<uint32_t*>(m->h_io + (m->step - m->io));
+  m->h_active = reinterpret_cast<uint32_t*>(m->h_io + (m->active - m->io));
   // caches, activations and scratch start at zero (counters must)
   uint64_t words = m->arena_bytes / 4;
   uint32_t zero = 0;
@@ -256,25 +274,35 @@ XPro pro_plain(const float* x) {
   return p;
 }
 
-// Records one forward pass (all layers; with the LM head when logits).
+// dst[0..n) = src[0..n) (u32 words) on the context stream.
+gh_status copy_words(gh_model* m, void* dst, const void* src, uint64_t n) {
+  void* args[] = {&dst, const_cast<void**>(&src), &n};
+  const unsigned grid = (unsigned)std::min<uint64_t>((n + 255) / 256, 64);
+  return m->ctx->launch("gh_copy_u32_k", dim3(grid), dim3(256), 0, args);
+}
+
+// Records one forward pass (all layers; with the LM head when logits).  The
+// graph holds kernels only: the caller copies the io region in before the
+// replay and the token out after it.
 gh_status record_forward(gh_model* m, bool logits) {
   gh_context* ctx = m->ctx;
   const gh_model_config& c = m->cfg;
   const uint32_t H = c.hidden_size, I = c.intermediate_size;
   const char* gemv = m->mode == GH_QUANT_Q8 ? "gh_gemv_q8" : "gh_gemv_q4";
   const char* gateup = m->mode == GH_QUANT_Q8 ? "gh_gateup_q8" : "gh_gateup_q4";
-  hipError_t e;
-  // host -> device: x, active list, step params (pinned staging)
-  e = hipMemcpyAsync(m->at<float>(m->x0), m->h_x, H * 4, hipMemcpyHostToDevice, ctx->stream);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(m->at<uint32_t>(m->active), m->h_active, (size_t)c.max_slots * 4,
-                       hipMemcpyHostToDevice, ctx->stream);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(m->at<uint32_t>(m->step), m->h_step, 16, hipMemcpyHostToDevice, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "record: input copies");
+  gh_status st;
+  {  // device ring: slot_idx, S and the active list from the clock (step mode 1)
+    uint32_t* rc = m->at<uint32_t>(m->ring_clock);
+    uint32_t* rf = m->at<uint32_t>(m->ring_flag);
+    uint32_t* sp = m->at<uint32_t>(m->step);
+    uint32_t* al = m->at<uint32_t>(m->active);
+    uint32_t A = m->ring_a, W = std::max(1u, m->ring_w), R = m->ring_r;
+    void* args[] = {&rc, &rf, &sp, &al, &A, &W, &R};
+    if ((st = ctx->launch("gh_ring_step_k", dim3(1), dim3(1024), 0, args)) != GH_OK) return st;
+  }
+  if (m->trace_on && (st = copy_words(m, m->trace, m->at<float>(m->x0), H)) != GH_OK) return st;
 
   size_t xcur = m->x0, xoth = m->x1;
-  gh_status st;
   for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& L = m->layers[l];
     // 1. [q|k|v] = W_qkv . norm(x)  (layer 0: RMSNorm; later: post-FFN add + norm)
@@ -296,6 +324,9 @@ gh_status record_forward(gh_model* m, bool logits) {
     }
     Q4Args qa{m->at<uint8_t>(L.qkv), m->at<float>(m->qkv_out)};
     if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H)) != GH_OK) return st;
+    if (m->trace_on && l > 0 &&
+        (st = copy_words(m, m->trace + (size_t)l * H, m->at<float>(xcur), H)) != GH_OK)
+      return st;
     // 2. q/k norm + RoPE + cache write + split-K attention
     gh::AttnLaunch A{};
     AttnArgs& a = A.args;
@@ -357,14 +388,15 @@ gh_status record_forward(gh_model* m, bool logits) {
     p.s = P.scalar;
     p.eps = c.rms_norm_eps;
     p.mode = 2;
-    m->hidden_final = xoth;
+    m->hidden_decode = xoth;
     ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
     if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
         GH_OK)
       return st;
-    e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost,
-                       ctx->stream);
-    if (e != hipSuccess) return hip_fail(e, "record: token copy");
+    if (m->trace_on &&
+        (st = copy_words(m, m->trace + (size_t)c.num_hidden_layers * H, m->at<float>(xoth), H)) !=
+            GH_OK)
+      return st;
   }
   return GH_OK;
 }
@@ -398,6 +430,44 @@ gh_status finish_init(gh_model* m, gh_model** out) {
     return hip_fail(e, "model init");
   }
   *out = m;
+  return GH_OK;
+}
+
+// Sends the host mirror's layer-0 ring state to the device arrays the ring
+// kernel reads.
+gh_status ring_upload(gh_model* m) {
+  const uint32_t n = m->cfg.max_slots;
+  std::vector<uint32_t> st(2 * (size_t)n, 0u);
+  if (m->ring) gh::ring_state(m->ring, 0, st.data(), st.data() + n, n);
+  gh_status s = gh_buffer_write(m->ctx, m->at<uint32_t>(m->ring_clock), st.data(), (size_t)n * 4);
+  if (s == GH_OK) s = gh_buffer_write(m->ctx, m->at<uint32_t>(m->ring_flag), st.data() + n, (size_t)n * 4);
+  return s;
+}
+
+gh_status rerecord(gh_model* m) {
+  hipStreamSynchronize(m->ctx->stream);
+  if (m->graph_decode) gh_graph_destroy(m->graph_decode);
+  if (m->graph_prefill) gh_graph_destroy(m->graph_prefill);
+  m->graph_decode = m->graph_prefill = nullptr;
+  return record_graphs(m);
+}
+
+// One token: the first `bytes` of the io region go up, the graph replays, and
+// with logits the token comes back.
+gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_token) {
+  hipStream_t s = m->ctx->stream;
+  hipError_t e = hipMemcpyAsync(m->arena + m->io, m->h_io, bytes, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "forward: input copy");
+  gh_status st = gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
+  if (st != GH_OK) return st;
+  if (want_logits) {
+    e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return hip_fail(e, "forward: token copy");
+  }
+  e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "forward");
+  m->hidden_final = want_logits ? m->hidden_decode : kNone;
+  if (want_logits) *out_token = m->h_token[0];
   return GH_OK;
 }
 
@@ -605,13 +675,120 @@ gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits
   m->h_step[0] = (uint32_t)clock;
   m->h_step[1] = slot_idx;
   m->h_step[2] = n_active;
-  m->h_step[3] = 0;
-  gh_status st = gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
+  m->h_step[3] = 0;  // the list comes from the host
+  if (m->ring) {  // keep the ring state in step (the ring kernel records the activation)
+    if (slot_idx != gh_ring_slot_index(m->ring, clock))
+      return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: slot_idx is not the ring's slot "
+                                  "for this clock");
+    gh_ring_activate_slot(m->ring, 0, clock);
+  }
+  return run_token(m, want_logits != 0, (m->active - m->io) + (size_t)n_active * 4, out_token);
+}
+
+gh_status gh_model_ring_init(gh_model* m, uint32_t num_anchors, uint32_t window_size,
+                             uint32_t num_recall) {
+  if (!m) return fail(GH_ERR_INVALID, "gh_model_ring_init: null model");
+  if (window_size == 0 || (uint64_t)num_anchors + window_size + num_recall > m->cfg.max_slots)
+    return fail(GH_ERR_INVALID, "gh_model_ring_init: need window > 0 and anchors + window + "
+                                "recall <= max_slots");
+  gh_ring* r = nullptr;
+  gh_status st = gh_ring_create(1, num_anchors, window_size, num_recall, &r);
   if (st != GH_OK) return st;
-  hipError_t e = hipStreamSynchronize(m->ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "gh_dispatch_forward_token");
-  if (want_logits) *out_token = m->h_token[0];
+  if (m->ring) gh_ring_destroy(m->ring);
+  m->ring = r;
+  const bool reshape = m->ring_a != num_anchors || m->ring_w != window_size || m->ring_r != num_recall;
+  m->ring_a = num_anchors;
+  m->ring_w = window_size;
+  m->ring_r = num_recall;
+  if ((st = ring_upload(m)) != GH_OK) return st;
+  // the ring kernel takes the tier sizes as arguments: record again
+  if (reshape && (st = rerecord(m)) != GH_OK) return st;
   return GH_OK;
+}
+
+gh_status gh_model_forward_clock(gh_model* m, const float* x, int want_logits, uint64_t clock,
+                                 uint32_t* out_token) {
+  if (!m || !x || !out_token) return fail(GH_ERR_INVALID, "gh_model_forward_clock: null argument");
+  *out_token = 0;
+  if (!m->ring) return fail(GH_ERR_INVALID, "gh_model_forward_clock: gh_model_ring_init first");
+  if (clock > 0xFFFFFFFFull) return fail(GH_ERR_INVALID, "gh_model_forward_clock: clock > 2^32");
+  memcpy(m->h_x, x, (size_t)m->cfg.hidden_size * 4);
+  m->h_step[0] = (uint32_t)clock;
+  m->h_step[1] = m->h_step[2] = 0;
+  m->h_step[3] = 1;  // the ring kernel activates the slot and builds the list
+  gh_ring_activate_slot(m->ring, 0, clock);
+  return run_token(m, want_logits != 0, (m->step - m->io) + 16, out_token);
+}
+
+gh_status gh_model_ring_clear_recall(gh_model* m) {
+  if (!m || !m->ring) return fail(GH_ERR_INVALID, "gh_model_ring_clear_recall: no device ring");
+  gh_ring_clear_recall(m->ring);
+  return ring_upload(m);
+}
+
+gh_status gh_model_write_recall_kv(gh_model* m, uint32_t layer, uint32_t rank, const float* k,
+                                   const float* v, uint64_t clock) {
+  if (!m || !k || !v) return fail(GH_ERR_INVALID, "gh_model_write_recall_kv: null argument");
+  if (!m->ring) return fail(GH_ERR_INVALID, "gh_model_write_recall_kv: gh_model_ring_init first");
+  if (layer >= m->layers.size() || rank >= m->ring_r || clock > 0xFFFFFFFFull)
+    return fail(GH_ERR_INVALID, "gh_model_write_recall_kv: layer, rank or clock out of range");
+  const Layer& L = m->layers[layer];
+  const size_t slot = (size_t)m->ring_a + m->ring_w + rank;
+  gh_status st = gh_buffer_write(m->ctx, m->at<float>(L.k_cache) + slot * L.kv_dim, k, L.kv_dim * 4);
+  if (st == GH_OK)
+    st = gh_buffer_write(m->ctx, m->at<float>(L.v_cache) + slot * L.kv_dim, v, L.kv_dim * 4);
+  if (st != GH_OK) return st;
+  // writeRecallKV's bookkeeping; the device path lists layer 0's ring
+  // (src/model/forward.zig:42-43), so layer 0 activates the slot
+  if (layer == 0) {
+    gh_ring_activate_recall(m->ring, 0, rank, clock);
+    return ring_upload(m);
+  }
+  return GH_OK;
+}
+
+gh_status gh_model_ring_prefill(gh_model* m, const float* x, uint32_t T, uint64_t first_clock,
+                                int want_logits, uint32_t* out_token) {
+  if (!m || !x || !out_token) return fail(GH_ERR_INVALID, "gh_model_ring_prefill: null argument");
+  *out_token = 0;
+  if (!m->ring) return fail(GH_ERR_INVALID, "gh_model_ring_prefill: gh_model_ring_init first");
+  if (T == 0 || first_clock + T - 1 > 0xFFFFFFFFull)
+    return fail(GH_ERR_INVALID, "gh_model_ring_prefill: T is zero or a clock exceeds 2^32");
+  const uint32_t total = gh_ring_total_slots(m->ring);
+  std::vector<uint64_t> clocks(T);
+  std::vector<uint32_t> slots(T), n(T), lists((size_t)T * total);
+  // the lists as the per-token calls would see them: slot activations of the
+  // earlier tokens of the batch included, later ones not; on a refused batch
+  // the ring keeps its state
+  gh_ring* r = gh::ring_clone(m->ring);
+  if (!r) return fail(GH_ERR_ALLOC, "gh_model_ring_prefill: ring copy");
+  for (uint32_t t = 0; t < T; t++) {
+    clocks[t] = first_clock + t;
+    slots[t] = gh_ring_activate_slot(r, 0, clocks[t]);
+    n[t] = gh_ring_active_slots(r, 0, clocks[t], &lists[(size_t)t * total], total);
+  }
+  gh_status st = gh_model_prefill(m, x, T, clocks.data(), slots.data(), lists.data(), total,
+                                  n.data(), want_logits, out_token);
+  if (st != GH_OK) {
+    gh_ring_destroy(r);
+    return st;
+  }
+  gh_ring_destroy(m->ring);
+  m->ring = r;
+  return ring_upload(m);
+}
+
+gh_status gh_model_set_trace(gh_model* m, int enable) {
+  if (!m) return fail(GH_ERR_INVALID, "gh_model_set_trace: null model");
+  if ((enable != 0) == m->trace_on) return GH_OK;
+  if (enable && !m->trace) {
+    const size_t bytes = (size_t)(m->cfg.num_hidden_layers + 1) * m->cfg.hidden_size * 4;
+    hipError_t e = hipMalloc(&m->trace, bytes);
+    if (e != hipSuccess) return fail(GH_ERR_ALLOC, std::string("trace buffer: ") + hipGetErrorString(e));
+    if (hipMemset(m->trace, 0, bytes) != hipSuccess) return fail(GH_ERR_HIP, "trace buffer clear");
+  }
+  m->trace_on = enable != 0;
+  return rerecord(m);
 }
 
 gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64_t* clocks,
@@ -648,6 +825,10 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
                     "gh_model_prefill: a token attends to a slot a later token of the batch writes");
     }
   }
+  if (m->ring)
+    for (uint32_t t = 0; t < T; t++)
+      if (slot_idx[t] != gh_ring_slot_index(m->ring, clocks[t]))
+        return fail(GH_ERR_INVALID, "gh_model_prefill: a slot is not the ring's slot for its clock");
   gh_status st = ensure_prefill(m, T, active_stride);
   if (st != GH_OK) return st;
   hipStream_t s = m->ctx->stream;
@@ -739,7 +920,12 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   }
   e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_fail(e, "gh_model_prefill");
+  m->hidden_final = want_logits ? m->x1 : kNone;
   if (want_logits) *out_token = m->h_token[0];
+  if (m->ring) {
+    for (uint32_t t = 0; t < T; t++) gh_ring_activate_slot(m->ring, 0, clocks[t]);
+    return ring_upload(m);
+  }
   return GH_OK;
 }
 
@@ -948,7 +1134,6 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     p.s = P.scalar;
     p.eps = c.rms_norm_eps;
     p.mode = 2;
-    m->hidden_final = m->x1;
     ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
     if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
         GH_OK)
@@ -970,10 +1155,23 @@ std::pair<uint8_t*, size_t> tensor_ref(const gh_model* m, int layer, gh_tensor t
       return {reinterpret_cast<uint8_t*>(m->embed_dev), m->embed_dev ? (size_t)V * H * 2 : 0};
     case GH_T_LOGITS:
       return {m->arena + m->logits, (size_t)V * 4};
-    case GH_T_HIDDEN:
-      return {m->arena + (m->hidden_final ? m->hidden_final : m->x1), (size_t)H * 4};
+    case GH_T_HIDDEN:  // the final residual of the last call that computed logits
+      if (m->hidden_final == kNone || m->hidden_final == 0) return {nullptr, 0};
+      return {m->arena + m->hidden_final, (size_t)H * 4};
+    case GH_T_STEP:
+      return {m->arena + m->step, 16};
+    case GH_T_ACTIVE:
+      return {m->arena + m->active, (size_t)c.max_slots * 4};
+    case GH_T_RING_CLOCKS:
+      return {m->arena + m->ring_clock, (size_t)c.max_slots * 4};
+    case GH_T_RING_FLAGS:
+      return {m->arena + m->ring_flag, (size_t)c.max_slots * 4};
     default:
       break;
+  }
+  if (t == GH_T_TRACE) {  // row `layer` of the residual trace, 0..num_layers
+    if (!m->trace || layer < 0 || layer > (int)m->layers.size()) return {nullptr, 0};
+    return {reinterpret_cast<uint8_t*>(m->trace + (size_t)layer * H), (size_t)H * 4};
   }
   if (layer < 0 || layer >= (int)m->layers.size()) return {nullptr, 0};
   const Layer& L = m->layers[layer];

@@ -103,3 +103,20 @@ uint32_t gh_ring_active_slots(const gh_ring* r, uint32_t layer, uint64_t clock, 
 }
 
 }  // extern "C"
+
+namespace gh {
+
+gh_ring* ring_clone(const gh_ring* r) { return r ? new gh_ring(*r) : nullptr; }
+
+// Layer `layer`'s clocks (as u32) and active flags of the first n slots; slots
+// beyond the ring read as inactive.
+void ring_state(const gh_ring* r, uint32_t layer, uint32_t* clocks, uint32_t* flags, uint32_t n) {
+  const size_t base = (size_t)layer * r->total_slots;
+  for (uint32_t s = 0; s < n; s++) {
+    const bool in = s < r->total_slots;
+    clocks[s] = in ? (uint32_t)r->clocks[base + s] : 0u;
+    flags[s] = in ? r->active[base + s] : 0u;
+  }
+}
+
+}  // namespace gh

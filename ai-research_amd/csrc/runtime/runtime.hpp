@@ -92,6 +92,9 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                     const void* W1, const void* Ax, const float* rs, float* C,
                                     uint32_t T, uint32_t N, uint32_t K,
                                     const float** planes = nullptr, uint32_t* nplanes = nullptr);
+// Internal helpers of the host ring (ring.cpp).
+gh_ring* ring_clone(const gh_ring* r);
+void ring_state(const gh_ring* r, uint32_t layer, uint32_t* clocks, uint32_t* flags, uint32_t n);
 gh_status fail(gh_status st, const std::string& msg);
 gh_status hip_fail(hipError_t e, const char* what);
 }  // namespace gh

@@ -67,6 +67,7 @@ _SIGS = {
                          _u32, _f32, _f32]),
     "gh_decode_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _u32]),
     "gh_argmax": (_i, [_vp, _vp, _vp, _u32]),
+    "gh_qkv_rope_attn": (_i, [_vp] * 11 + [_u32] * 5 + [_f32, _f32, _u32]),
     "gh_prefill_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _u32, _u32, _u32]),
     "gh_prefill_gate_up_geglu": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
 }
@@ -118,6 +119,12 @@ _SIGS.update({
     "gh_dispatch_forward_token": (_i, [_vp, _vp, _i, _u64, _u32, _vp, _u32, C.POINTER(_u32)]),
     "gh_model_prefill": (_i, [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _vp, _i, C.POINTER(_u32)]),
     "gh_model_embed": (_i, [_vp, _u32, _vp]),
+    "gh_model_ring_init": (_i, [_vp, _u32, _u32, _u32]),
+    "gh_model_forward_clock": (_i, [_vp, _vp, _i, _u64, C.POINTER(_u32)]),
+    "gh_model_ring_prefill": (_i, [_vp, _vp, _u32, _u64, _i, C.POINTER(_u32)]),
+    "gh_model_ring_clear_recall": (_i, [_vp]),
+    "gh_model_write_recall_kv": (_i, [_vp, _u32, _u32, _vp, _vp, _u64]),
+    "gh_model_set_trace": (_i, [_vp, _i]),
     "gh_model_tensor_bytes": (_sz, [_vp, _i, _i]),
     "gh_model_read_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
     "gh_model_write_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
@@ -127,6 +134,7 @@ _SIGS.update({
 (T_QKV, T_O_PROJ, T_GATE, T_UP, T_DOWN, T_INPUT_NORM, T_Q_NORM, T_K_NORM, T_POST_ATTN_NORM,
  T_PRE_FFN_NORM, T_POST_FFN_NORM, T_K_CACHE, T_V_CACHE) = range(13)
 T_LM_HEAD, T_FINAL_NORM, T_EMBED, T_LOGITS, T_HIDDEN = 20, 21, 22, 23, 24
+T_STEP, T_ACTIVE, T_RING_CLOCKS, T_RING_FLAGS, T_TRACE = 25, 26, 27, 28, 29
 
 _lib = None
 
@@ -358,6 +366,13 @@ class Context:
                                     _addr(active), _addr(out), _addr(step), head_dim, kv_dim,
                                     gqa_ratio, inv_sqrt_dim, num_q_heads), "gh_decode_attn")
 
+    def qkv_rope_attn(self, Q, K, V, Qn, Kn, K_cache, V_cache, active, step, out, num_q, num_kv,
+                      head_dim, rot, k_eq_v, theta, eps=1e-6, max_slots=640):
+        _check(lib().gh_qkv_rope_attn(self.h, _addr(Q), _addr(K), _addr(V), _addr(Qn), _addr(Kn),
+                                      _addr(K_cache), _addr(V_cache), _addr(active), _addr(step),
+                                      _addr(out), num_q, num_kv, head_dim, rot, int(k_eq_v),
+                                      theta, eps, max_slots), "gh_qkv_rope_attn")
+
     def argmax(self, logits, out_token, vocab):
         _check(lib().gh_argmax(self.h, _addr(logits), _addr(out_token), vocab), "gh_argmax")
 
@@ -488,6 +503,36 @@ class Model:
                                       stride, _ptr(n_act), int(want_logits), C.byref(tok)),
                "gh_model_prefill")
         return tok.value
+
+    # ---- device-resident ring (gh_model_ring_*) ----
+    def ring_init(self, anchors, window, recall):
+        _check(lib().gh_model_ring_init(self.h, anchors, window, recall), "gh_model_ring_init")
+
+    def forward_clock(self, x, clock, want_logits=True):
+        x = np.ascontiguousarray(x, np.float32)
+        tok = _u32()
+        _check(lib().gh_model_forward_clock(self.h, _ptr(x), int(want_logits), clock, C.byref(tok)),
+               "gh_model_forward_clock")
+        return tok.value
+
+    def ring_prefill(self, x, first_clock, want_logits=True):
+        x = np.ascontiguousarray(x, np.float32)
+        tok = _u32()
+        _check(lib().gh_model_ring_prefill(self.h, _ptr(x), x.shape[0], first_clock,
+                                           int(want_logits), C.byref(tok)), "gh_model_ring_prefill")
+        return tok.value
+
+    def ring_clear_recall(self):
+        _check(lib().gh_model_ring_clear_recall(self.h), "gh_model_ring_clear_recall")
+
+    def write_recall_kv(self, layer, rank, k, v, clock):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        _check(lib().gh_model_write_recall_kv(self.h, layer, rank, _ptr(k), _ptr(v), clock),
+               "gh_model_write_recall_kv")
+
+    def set_trace(self, enable):
+        _check(lib().gh_model_set_trace(self.h, int(enable)), "gh_model_set_trace")
 
     def embed(self, token):
         x = np.empty(self.cfg.hidden_size, np.float32)

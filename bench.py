@@ -151,7 +151,129 @@ def bench_gemv(ctx, reps=256):
     return nbytes / (ms * 1e-3) / 1e9, ms * 1e3
 
 
-def bench_decode(ctx, n_prompt=512, n_decode=128):
+def timed_graph(ctx, launch, reps):
+    """Average ms of one launch: `reps` launches recorded once as a graph,
+    replayed once untimed, then timed with HIP events on the context stream."""
+    ctx.graph_begin()
+    for i in range(reps):
+        launch(i)
+    g = ctx.graph_end()
+    ctx.graph_launch(g)
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0)
+    ctx.graph_launch(g)
+    ctx.record(e1)
+    ctx.sync()
+    ms = ctx.elapsed_ms(e0, e1) / reps
+    ctx.graph_destroy(g)
+    ctx.destroy_event(e0)
+    ctx.destroy_event(e1)
+    return ms
+
+
+def bench_attention(ctx, reps=96):
+    """The decode graph's per-layer attention step (q/k norm + RoPE, the cache
+    write, split-K attention and the split merge; gh_qkv_rope_attn): 16 query /
+    8 kv heads of 256, 48 rotated per-layer 640-slot caches (503 MB, beyond
+    the Infinity Cache), S = 544 (the steady decode context) and 640 (the
+    whole ring).  Algorithmic bytes: K + V rows of the S slots, q, the new
+    k/v, the output and the list."""
+    nq, nkv, D, slots, nl = 16, 8, 256, 640, 48
+    caches = []
+    for l in range(nl):
+        kc, vc = ctx.alloc(slots * nkv * D * 4), ctx.alloc(slots * nkv * D * 4)
+        ctx.synth_normal_dev(kc, slots * nkv * D, 7, 2 * l, 0.0, 1.0)
+        ctx.synth_normal_dev(vc, slots * nkv * D, 7, 2 * l + 1, 0.0, 1.0)
+        caches.append((kc, vc))
+    q, k, v = (ctx.upload(gh.synth_normal(n, 7, 200 + i, 0.0, 1.0))
+               for i, n in enumerate((nq * D, nkv * D, nkv * D)))
+    qn = ctx.upload(gh.synth_normal(D, 7, 210, 1.0, 0.1))
+    kn = ctx.upload(gh.synth_normal(D, 7, 211, 1.0, 0.1))
+    out = ctx.alloc(nq * D * 4)
+    res = {}
+    for S, clock in ((544, 600), (640, 639)):
+        slot = 32 + (clock - 32) % 512
+        act = ctx.upload(np.arange(S, dtype=np.uint32))
+        st = ctx.upload(np.array([clock, slot, S, 0], np.uint32))
+
+        def launch(i):
+            kc, vc = caches[i % nl]
+            ctx.qkv_rope_attn(q, k, v, qn, kn, kc, vc, act, st, out, nq, nkv, D, 256, False, 1e4)
+
+        ms = timed_graph(ctx, launch, reps)
+        nbytes = S * nkv * D * 4 * 2 + 2 * nq * D * 4 + 2 * nkv * D * 4 + S * 4
+        res["S%d" % S] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
+                          "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                          "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    for kc, vc in caches:
+        kc.free()
+        vc.free()
+    return res
+
+
+def bench_lm_head(ctx, reps=20):
+    """Final norm -> Q8_0 LM head 262144 x 3840 -> greedy argmax (one fused
+    stream plus the partial reduction), the decode step's tail.  1.13 GB of
+    weights: one copy already exceeds the Infinity Cache."""
+    V = 262144
+    staging = ctx.alloc(V * H * 2)
+    ctx.synth_normal_dev(staging, V * H, 0, 999, 0.0, 0.02, bf16=True)
+    W = ctx.alloc(V * (H // 32) * 36)
+    ctx.quantize_dev(W, staging, V, H, gh.QUANT_Q8)
+    staging.free()
+    X = ctx.upload(gh.synth_normal(H, 0, 4, 0.0, 1.0))
+    NW = ctx.upload(gh.synth_normal(H, 0, 5, 1.0, 0.1))
+    L, TOK = ctx.alloc(V * 4), ctx.alloc(4)
+    pro = ctx.prologue(X, mode=1, norm=NW)
+    ms = timed_graph(ctx, lambda i: ctx.norm_gemv_argmax_q8(W, L, TOK, V, H, pro), reps)
+    W.free()
+    nbytes = V * (H // 32) * 36 + 2 * H * 4 + V * 4 + 4
+    return {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def decode_step_bytes(S):
+    """Algorithmic HBM bytes of one 12B-shaped decode step at S active slots:
+    layer weights, the Q8 LM head, K/V rows of the S slots in 48 layers, the
+    f32 norms and the 1 MiB of logits."""
+    layers = 48 * (8192 * Q4_ROW(H) + H * Q4_ROW(4096) + 2 * I * Q4_ROW(H) + H * Q4_ROW(I))
+    head = 262144 * (H // 32) * 36
+    kv = S * 8 * 256 * 4 * 2 * 48
+    norms = 48 * (4 * H + 2 * 256) * 4 + H * 4
+    return layers + head + kv + norms + 262144 * 4
+
+
+def cpu_decode_baseline(m, cfg, clock, nt, steps=2):
+    """The oracle's restatement of the reference CPU forward
+    (src/model/forward.zig:49-70, quantized weights as the GPU graph runs
+    them) for whole 12B decode steps on this host: weights and caches read
+    back from the device, `steps` timed steps after one untimed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from model_ref import oracle_model
+
+    om, _ = oracle_model(m, cfg)
+    ring = gh.Ring(1, 32, 512, 96)
+    for c in range(clock):
+        ring.activate_slot(0, c)
+    x = gh.synth_normal(H, 0, 6, 0.0, 1.0)
+    times = []
+    for i in range(steps + 1):
+        c = clock + i
+        slot = ring.activate_slot(0, c)
+        act = ring.active_slots(0, c)
+        t0 = time.perf_counter()
+        om.forward(x, c, slot, act, True, nt)
+        times.append(time.perf_counter() - t0)
+    dt = sum(times[1:]) / steps
+    return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": nt,
+            "host_cpus": os.cpu_count(), "kind": "port",
+            "sample": "%d full 12B decode steps (48 layers + Q8 head, S = %d) after one untimed, "
+                      "%.2f s each" % (steps, len(act), dt)}
+
+
+def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
     """12B-shaped decode: 48 layers (global iff (l+1) % 6 == 0), hidden 3840,
     16/8 heads of 256, intermediate 15360, vocab 262144, Q4_0 layers and Q8_0
     tied head, 640-slot ring (32 anchors, 512 window, 96 recall).  A prompt of
@@ -171,46 +293,66 @@ def bench_decode(ctx, n_prompt=512, n_decode=128):
     def emb(t):  # src/model/forward.zig:33-37
         return (embed[t].astype(np.uint32) << 16).view(np.float32) * scale
 
-    ring = gh.Ring(48, 32, 512, 96)
+    m.ring_init(32, 512, 96)  # device-resident ring: a token uploads x and its clock
+    ring = gh.Ring(1, 32, 512, 96)  # host ring, for the host-list steps at the end
     prompt = gh.synth_uniform_u32(n_prompt, 1, 0, cfg.vocab_size)
     xs = np.stack([emb(int(t)) for t in prompt])
-    slots, actives = [], []
-    for c in range(n_prompt):
-        slots.append(ring.activate_slot(0, c))
-        actives.append(np.array(ring.active_slots(0, c), np.uint32))
-    clocks = np.arange(n_prompt)
     # Two untimed calls (the first allocates the prefill buffers; the GPU comes
     # up to clock after the idle embedding read), then the median of three
     # timed calls, each rewriting the same K/V.
     for _ in range(2):
-        m.prefill(xs, clocks, slots, actives, True)
+        m.ring_prefill(xs, 0, True)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        tok = m.prefill(xs, clocks, slots, actives, True)
+        tok = m.ring_prefill(xs, 0, True)
         times.append(time.perf_counter() - t0)
     prefill_s = sorted(times)[1]
+    for c in range(n_prompt):
+        ring.activate_slot(0, c)
     toks = []
     t0 = time.perf_counter()
     for i in range(n_decode):
         c = n_prompt + i
-        slot = ring.activate_slot(0, c)
-        tok = m.forward(emb(tok), c, slot, ring.active_slots(0, c), True)
+        tok = m.forward_clock(emb(tok), c, True)
         toks.append(tok)
     decode_s = time.perf_counter() - t0
+    for i in range(n_decode):
+        ring.activate_slot(0, n_prompt + i)
+    # the same per-token work with the host's slot bookkeeping and list upload
+    # (gpuDispatchForwardToken's interface): 32 more steps
+    n_host = 32
+    t0 = time.perf_counter()
+    for i in range(n_host):
+        c = n_prompt + n_decode + i
+        slot = ring.activate_slot(0, c)
+        tok = m.forward(emb(tok), c, slot, ring.active_slots(0, c), True)
+    host_s = time.perf_counter() - t0
+    cpu_dec = None
+    if cpu:
+        cpu_dec = cpu_decode_baseline(m, cfg, n_prompt + n_decode + n_host,
+                                      max(1, min(16, os.cpu_count() or 1)))
     m.close()
+    clocks = range(n_prompt, n_prompt + n_decode)
+    ideal_s = sum(decode_step_bytes(min(c + 1, 544)) for c in clocks) / (HBM_PEAK_GBS * 1e9)
     step_bytes = (48 * (8192 * Q4_ROW(H) + H * Q4_ROW(4096) + 2 * I * Q4_ROW(H) + H * Q4_ROW(I))
                   + 262144 * (H // 32) * 36)
     gemm_flop = 2 * n_prompt * 48 * (8192 * H + H * 4096 + 2 * I * H + H * I)
     return {"decode_tok_s": round(n_decode / decode_s, 2),
             "decode_ms_per_token": round(decode_s / n_decode * 1e3, 3),
             "decode_weight_gbs": round(step_bytes * n_decode / decode_s / 1e9, 1),
+            "decode_roofline_ms_per_token": round(ideal_s / n_decode * 1e3, 4),
+            "decode_roofline_frac": round(ideal_s / decode_s, 4),
+            "decode_path": "device ring (gh_model_forward_clock): x and the clock go up, the "
+                           "token comes back, one host round trip per token",
+            "decode_tok_s_host_lists": round(n_host / host_s, 2),
             "prefill_tok_s": round(n_prompt / prefill_s, 1),
             "prefill_ms": round(prefill_s * 1e3, 2),
             "prefill_path": "batched (MFMA Q4 dequant GEMM), one call; median of 3 after 2 warm-up calls",
             "prefill_gemm_tflops": round(gemm_flop / prefill_s / 1e12, 1),
             "model_init_s": round(init_s, 2),
-            "decode_tokens_head": [int(t) for t in toks[:8]]}
+            "decode_tokens_head": [int(t) for t in toks[:8]],
+            "cpu_decode_baseline": cpu_dec}
 
 
 def cpu_baseline(x, host_w, budget_s=10.0, threads=None):
@@ -262,7 +404,9 @@ def main():
     value = step_bytes * args.steps / wall / 1e9
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
     gemv_gbs, gemv_us = bench_gemv(ctx)
-    dec = bench_decode(ctx, args.prompt, args.decode) if not args.no_decode else None
+    attn = bench_attention(ctx)
+    head = bench_lm_head(ctx)
+    dec = bench_decode(ctx, args.prompt, args.decode, cpu=not args.no_cpu) if not args.no_decode else None
     if dec:
         log("decode %.1f tok/s (%.3f ms/token), prefill %.1f tok/s"
             % (dec["decode_tok_s"], dec["decode_ms_per_token"], dec["prefill_tok_s"]))
@@ -279,7 +423,7 @@ def main():
     if not args.no_cpu:
         n, dt, nt = cpu_baseline(x, host_w)
         cpu = {"value": round(step_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": nt,
-               "kind": "port",
+               "host_cpus": os.cpu_count(), "kind": "port",
                "sample": "%d full MLP steps (3840/15360 Q4_0, copy 0 of the weights) in %.1f s "
                          "with the oracle's 16-way row split" % (n, dt)}
         n1, dt1, _ = cpu_baseline(x, host_w, budget_s=4.0, threads=1)
@@ -314,6 +458,12 @@ def main():
                   "down_proj_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
                   "gemv_q4_8192x2048_gbs": round(gemv_gbs, 1),
                   "gemv_q4_8192x2048_us": round(gemv_us, 3),
+                  "gemv_q4_8192x2048_roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1),
+                                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                 "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                                                 "bytes": 10526720},
+                  "attention_640_slots": attn,
+                  "lm_head_q8_argmax": head,
                   "cpu_baseline_1thread": cpu1,
                   "decode_12b": dec},
     }

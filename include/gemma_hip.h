@@ -191,6 +191,22 @@ gh_status gh_decode_attn(gh_context *ctx, const float *Q, const float *K_cache,
                          const float *V_cache, const uint32_t *active_slots, float *out,
                          const uint32_t *step_params, uint32_t head_dim, uint32_t kv_dim,
                          uint32_t gqa_ratio, float inv_sqrt_dim, uint32_t num_q_heads);
+/* recordQkvRope + recordDecodeAttn (kernels.zig:116-129) as the decode graph
+ * runs them back to back (model_dispatch.zig:22-25), in one split-K launch
+ * plus the split merge: per-head RMSNorm(q_norm) + RoPE of the query heads,
+ * RMSNorm(k_norm) + RoPE of the key heads and unit-RMS of the value heads
+ * (the raw key heads when k_eq_v) written to K_cache / V_cache at row
+ * step_params[1], then attention of every query head (kv head h / (num_q /
+ * num_kv), scale 1.0, model/forward.zig:80) over the step_params[2] active
+ * slots into out [num_q][head_dim].  Q_in is left unchanged.  max_slots sets
+ * the split count as the model's ring does.  The first call allocates the
+ * context's split scratch (not inside graph capture). */
+gh_status gh_qkv_rope_attn(gh_context *ctx, const float *Q_in, const float *K_in,
+                           const float *V_in, const float *Q_norm, const float *K_norm,
+                           float *K_cache, float *V_cache, const uint32_t *active_slots,
+                           const uint32_t *step_params, float *out, uint32_t num_q,
+                           uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
+                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots);
 /* recordArgmax (kernels.zig:139-142), shaders/argmax.wgsl, with the CPU
  * path's tie rule (sampleArgmax, src/kernels.zig:164-174): the lowest index
  * of the largest value.  out_token is a device u32. */
@@ -258,7 +274,7 @@ typedef struct gh_model_config {
 /* LayerWeights (src/model/types.zig:13-41): borrowed bf16 host pointers,
  * row-major [out][in]; v_proj, post_* and k_norm may be null (k_norm null =
  * ones, v_proj null = the key projection is used as value, as
- * src/gpu/model_gpu.zig:267-278 does). */
+ * src/gpu/model_gpu.zig:124 does). */
 typedef struct gh_layer_weights {
   const uint16_t *input_layernorm, *q_proj, *k_proj, *v_proj, *o_proj, *q_norm, *k_norm;
   const uint16_t *post_attention_layernorm, *pre_feedforward_layernorm;
@@ -291,7 +307,10 @@ void gh_model_deinit(gh_model *m);
  * and the active slots from ring.getActiveSlots (u32, host).  When want_logits
  * the decode graph runs and *out_token receives the greedy token; otherwise
  * the prefill graph (no LM head) runs and *out_token is 0.  Every layer writes
- * this token's K/V into its cache at slot_idx. */
+ * this token's K/V into its cache at slot_idx.  x, the step record and the
+ * list go up in one copy before the graph replays (the graph holds kernels
+ * only).  After gh_model_ring_init, slot_idx must be the ring's slot for the
+ * clock, and the call also records the activation in the device ring. */
 gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits, uint64_t clock,
                                     uint32_t slot_idx, const uint32_t *active_slots,
                                     uint32_t n_active, uint32_t *out_token);
@@ -315,6 +334,48 @@ gh_status gh_model_prefill(gh_model *m, const float *x, uint32_t T, const uint64
  * synthetic model, whose bf16 embedding lives on the device. */
 gh_status gh_model_embed(gh_model *m, uint32_t token, float *x_host);
 
+/* ---- device-resident ring bookkeeping ------------------------------------
+ * The model keeps layer 0's DynamicRingBuffer state (src/ring_buffer.zig:
+ * 7-147: a clock and an active flag per slot) in HBM, plus a host mirror.  A
+ * token then needs only x and its clock: the decode graph's first kernel
+ * activates the clock's slot (activateSlot, ring_buffer.zig:61-68) and builds
+ * slot_idx, S and the active list (getSlotIndex / getActiveSlots,
+ * ring_buffer.zig:56-59,101-136), which the host computes per token in the
+ * reference (src/model/forward.zig:42-43, src/gpu/model_dispatch.zig:136-142).
+ * DynamicRingBuffer.init for the device state (ring_buffer.zig:19-36): A
+ * anchors, W window slots (> 0), R recall slots, A + W + R <= max_slots; all
+ * slots start inactive. */
+gh_status gh_model_ring_init(gh_model *m, uint32_t num_anchors, uint32_t window_size,
+                             uint32_t num_recall);
+/* forwardToken's GPU branch (src/model/forward.zig:41-45) with the ring on
+ * the device: only x (host) and the clock go up. */
+gh_status gh_model_forward_clock(gh_model *m, const float *x, int want_logits, uint64_t clock,
+                                 uint32_t *out_token);
+/* T prompt tokens at clocks first_clock .. first_clock + T - 1 through the
+ * batched prefill, their slots and lists taken from the device ring (as T
+ * calls of gh_model_forward_clock would see them).  A batch the prefill
+ * refuses (it would write one slot twice) leaves the ring unchanged. */
+gh_status gh_model_ring_prefill(gh_model *m, const float *x, uint32_t T, uint64_t first_clock,
+                                int want_logits, uint32_t *out_token);
+/* clearRecall (ring_buffer.zig:82-88) on the device ring. */
+gh_status gh_model_ring_clear_recall(gh_model *m);
+/* writeRecallKV (ring_buffer.zig:90-99) into the device caches: layer's
+ * [kv_dim] key and value rows (host f32) go to recall slot A + W + rank; for
+ * layer 0 the slot becomes active with `clock`, the bookkeeping the device
+ * path lists every layer by (forward.zig:42-43).  The reference's GPU path
+ * activates recall slots without uploading their K/V
+ * (src/model/memory_inject.zig:38-45 writes the host ring only); this call
+ * uploads both. */
+gh_status gh_model_write_recall_kv(gh_model *m, uint32_t layer, uint32_t rank, const float *k,
+                                   const float *v, uint64_t clock);
+
+/* Per-layer residual trace (no reference counterpart; for checking): when
+ * enabled, every forward call also copies the residual stream at each
+ * layer's input into row l of a [num_layers + 1][hidden] buffer, and with
+ * logits the final residual into row num_layers (GH_T_TRACE).  Enabling or
+ * disabling records the graphs again. */
+gh_status gh_model_set_trace(gh_model *m, int enable);
+
 /* Tensor access for checking and cache set-up (no reference counterpart). */
 typedef enum gh_tensor {
   GH_T_QKV = 0,        /* layer: [q_dim + kv_dim (+ kv_dim)] quantized rows */
@@ -334,7 +395,13 @@ typedef enum gh_tensor {
   GH_T_FINAL_NORM = 21,
   GH_T_EMBED = 22,     /* synthetic models: bf16 [vocab][hidden] */
   GH_T_LOGITS = 23,    /* f32 [vocab] of the last decode step */
-  GH_T_HIDDEN = 24     /* f32 [hidden]: the residual stream after the last step */
+  GH_T_HIDDEN = 24,    /* f32 [hidden]: the final residual of the last call that
+                          computed logits (absent after a call without logits) */
+  GH_T_STEP = 25,      /* u32 [4]: {clock, slot_idx, S, mode} of the last step */
+  GH_T_ACTIVE = 26,    /* u32 [max_slots]: the last step's active list (S entries) */
+  GH_T_RING_CLOCKS = 27, /* u32 [max_slots]: device ring clock per slot */
+  GH_T_RING_FLAGS = 28,  /* u32 [max_slots]: device ring active flag per slot */
+  GH_T_TRACE = 29      /* f32 [hidden]: trace row `layer` (0 .. num_layers) */
 } gh_tensor;
 /* Byte size of a tensor (0 when it does not exist). */
 size_t gh_model_tensor_bytes(const gh_model *m, int layer, gh_tensor t);

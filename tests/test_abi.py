@@ -30,6 +30,27 @@ def test_library_exports_every_declared_function():
     assert sorted(gh.exported_symbols()) == names
 
 
+def header_arities():
+    """Parameter count of every function the header declares."""
+    txt = open(os.path.join(ROOT, "include", "gemma_hip.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(gh_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", txt):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_arity_matches_header():
+    # the ctypes table passes exactly the header's parameters
+    L = gh.lib()
+    ar = header_arities()
+    assert len(ar) == len(header_functions())
+    bad = {n: (k, len(getattr(L, n).argtypes)) for n, k in ar.items()
+           if len(getattr(L, n).argtypes) != k}
+    assert not bad, bad
+
+
 def test_device_count_without_gpu_is_not_an_error():
     assert gh.device_count() >= 0
 

@@ -151,6 +151,44 @@ def test_decode_attention_closed_forms(gpu):
     assert np.allclose(out[5], vc[17].reshape(nkv, D)[2], atol=1e-6)
 
 
+@pytest.mark.parametrize("k_eq_v", [False, True])
+@pytest.mark.parametrize("clock,S", [(600, 544), (639, 640), (5, 6)])
+def test_qkv_rope_attn_fused(gpu, clock, S, k_eq_v):
+    # the decode graph's per-layer attention step: q/k norm + RoPE, the cache
+    # write at slot_idx, and attention over the active list that includes it
+    nq, nkv, D, slots, rot, theta = 16, 8, 256, 640, 64, 1e6
+    kc, vc = make_cache(slots, nkv, D, 11)
+    qraw = gh.synth_normal(nq * D, clock, 86, 0.0, 1.0)
+    kraw = gh.synth_normal(nkv * D, clock, 87, 0.0, 1.0)
+    vraw = gh.synth_normal(nkv * D, clock, 88, 0.0, 1.0)
+    qn = bf16_round(gh.synth_normal(D, 11, 89, 1.0, 0.1))
+    kn = bf16_round(gh.synth_normal(D, 11, 90, 1.0, 0.1))
+    ring = orc.Ring(1, nkv * D, 32, 512, 96)
+    slot = ring.slot_index(clock)
+    active = np.random.default_rng(S).permutation(slots)[:S].astype(np.uint32)
+    if slot not in active:
+        active[S // 2] = slot
+    step = np.array([clock, slot, S, 0], np.uint32)
+    bufs = [gpu.upload(a) for a in (qraw, kraw, vraw, qn, kn, kc, vc, active, step)]
+    O = gpu.alloc(nq * D * 4)
+    Q, K, V, QN, KN, KC, VC, A, ST = bufs
+    gpu.qkv_rope_attn(Q, K, 0 if k_eq_v else V, QN, KN, KC, VC, A, ST, O, nq, nkv, D, rot,
+                      k_eq_v, theta)
+    q2, k2, v2 = orc.qkv_norm_rope(qraw, kraw, vraw, qn, kn, nq, nkv, D, rot, k_eq_v, theta,
+                                   1e-6, clock)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[slot], vc2[slot] = k2, v2
+    ref = orc.attention(q2, kc2, vc2, active, nq, nkv, D)
+    assert_close(O.read(np.float32, nq * D), ref, what="fused attention S=%d" % S)
+    got_k = KC.read(np.float32).reshape(slots, -1)
+    got_v = VC.read(np.float32).reshape(slots, -1)
+    assert_close(got_k[slot], k2, what="K row")
+    assert_close(got_v[slot], v2, what="V row")
+    others = np.arange(slots) != slot
+    assert np.array_equal(got_k[others], kc[others]) and np.array_equal(got_v[others], vc[others])
+    assert np.array_equal(Q.read(np.float32, nq * D), qraw)
+
+
 # ---------------------------------------------------------------- argmax ----
 def test_argmax_bit_exact(gpu):
     V = 262144

@@ -10,7 +10,7 @@ import gemma_hip as gh
 import numpy_ref as nr
 import oracle as orc
 from model_ref import layer_dims, oracle_model
-from tol import assert_close, errors
+from tol import assert_close
 
 pytestmark = pytest.mark.gpu
 NT = min(16, os.cpu_count() or 1)
@@ -25,20 +25,35 @@ def tiny_cfg(**kw):
     return gh.model_config(**args)
 
 
-def check_token(m, ref_logits, tok, what):
+def check_token(m, ref_logits, tok, rtok, what):
+    """Logits within the bar, the fused argmax bit-exact on the device's own
+    logits, and the greedy token equal to the oracle's.  The one allowed
+    exception is stated and asserted: a near-tie, where the oracle's gap
+    between its token and the device's is within the measured logit error."""
     logits = m.read(-1, gh.T_LOGITS, np.float32)
     assert_close(logits, ref_logits, what=what)
-    assert tok == orc.argmax(logits)  # the fused argmax is bit-exact on its own logits
-    top = float(np.max(ref_logits))
-    assert ref_logits[tok] >= top - 2e-3 * np.max(np.abs(ref_logits))
+    assert tok == orc.argmax(logits)
+    if tok != rtok:
+        err = float(np.max(np.abs(logits.astype(np.float64) - ref_logits)))
+        gap = float(ref_logits[rtok]) - float(ref_logits[tok])
+        assert 0.0 <= gap <= 2.0 * err, "%s: token %d vs oracle %d (gap %.3g, logit error %.3g)" % (
+            what, tok, rtok, gap, err)
+    return logits
 
 
+@pytest.mark.parametrize("k_eq_v", [False, True])
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
-def test_tiny_model_decode_sequence(gpu, mode):
-    cfg = tiny_cfg()
+def test_tiny_model_decode_sequence(gpu, mode, k_eq_v):
+    # k_eq_v: attention_k_eq_v = 1, so the full-attention layer (layer 2) has
+    # no v rows and its values are the raw keys (src/model/loader.zig:36-42,
+    # src/model/forward.zig:125)
+    cfg = tiny_cfg(k_eq_v=k_eq_v)
     m = gh.Model(gpu, cfg, mode=mode, seed=7)
     try:
         om, layers = oracle_model(m, cfg, mode)
+        assert layers[2]["k_eq_v"] == k_eq_v and not layers[0]["k_eq_v"]
+        qkv_rows = m.read(2, gh.T_QKV, np.uint32).size // ((cfg.hidden_size // 32) * (9 if mode == gh.QUANT_Q8 else 5))
+        assert qkv_rows == 4 * 128 + 2 * 128 * (1 if k_eq_v else 2)
         embed = m.read(-1, gh.T_EMBED, np.uint16).reshape(cfg.vocab_size, cfg.hidden_size)
         ring = gh.Ring(cfg.num_hidden_layers, 4, 16, 4)
         tokens = np.random.default_rng(1).integers(0, cfg.vocab_size, 40)
@@ -49,11 +64,13 @@ def test_tiny_model_decode_sequence(gpu, mode):
             active = ring.active_slots(0, clock)
             want = clock % 3 != 1  # interleave the prefill (no-logits) graph
             tok = m.forward(x, clock, slot, active, want)
-            rtok, _, rlog = om.forward(x, clock, slot, active, want, NT)
+            rtok, rx, rlog = om.forward(x, clock, slot, active, want, NT)
             if want:
-                check_token(m, rlog, tok, "tiny step %d" % clock)
+                check_token(m, rlog, tok, rtok, "tiny step %d" % clock)
+                assert_close(m.read(-1, gh.T_HIDDEN, np.float32), rx, what="final residual")
             else:
                 assert tok == 0
+                assert m.tensor_bytes(-1, gh.T_HIDDEN) == 0  # not computed without logits
         for l, d in enumerate(layers):
             kvd = d["num_kv_heads"] * d["head_dim"]
             kc = m.read(l, gh.T_K_CACHE, np.float32).reshape(cfg.max_slots, kvd)
@@ -104,8 +121,8 @@ def test_model_init_from_host_bf16(gpu):
             slot = ring.activate_slot(0, clock)
             active = ring.active_slots(0, clock)
             tok = m.forward(x, clock, slot, active)
-            _, _, rlog = om.forward(x, clock, slot, active, True, NT)
-            check_token(m, rlog, tok, "host-weights step %d" % clock)
+            rtok, _, rlog = om.forward(x, clock, slot, active, True, NT)
+            check_token(m, rlog, tok, rtok, "host-weights step %d" % clock)
     finally:
         m.close()
 
@@ -147,8 +164,7 @@ def test_12b_width_two_layers_strict(gpu):
         x = m.embed(4242)
         tok = m.forward(x, clock, slot, active)
         rtok, _, rlog = om.forward(x, clock, slot, active, True, NT)
-        check_token(m, rlog, tok, "12B-width 2 layers")
-        assert tok == rtok
+        check_token(m, rlog, tok, rtok, "12B-width 2 layers")
         for l in (0, 1):
             kc = m.read(l, gh.T_K_CACHE, np.float32).reshape(640, -1)
             assert_close(kc[slot], layers[l]["k_cache"][slot], what="K row layer %d" % l)
@@ -157,31 +173,47 @@ def test_12b_width_two_layers_strict(gpu):
 
 
 def test_12b_shaped_decode_step(gpu):
-    # The full 12B shape: 48 layers (global iff (l+1) % 6 == 0).  A random-init
-    # 48-layer stack amplifies rounding differences about 1.2x per layer: the
-    # oracle's own logits move by ~3% normwise when its input is perturbed by
-    # 1e-6, so the bound here is the greedy token bit-exact and the logit error
-    # within 3x that measured sensitivity (the 2e-3 bar is met at 1-2 layers,
-    # test above).
-    m, om, layers, clock, slot, active = _populated_step(
-        gpu, _12b(48, [l for l in range(48) if (l + 1) % 6 == 0]))
+    # The full 12B shape: 48 layers (global iff (l + 1) % 6 == 0), 544 active
+    # slots.  Every layer is held to the 2e-3 bar from the device's own layer
+    # input (the residual trace): the oracle runs layer l on the device's x_l
+    # and its x_(l+1) and K/V row must match the device's; the LM head is
+    # checked the same way from the device's final residual, and the greedy
+    # token of the whole step against the oracle's own 48-layer forward.  (A
+    # random-init 48-layer stack amplifies rounding differences about 1.2x per
+    # layer, so the end-to-end logits are not a 2e-3 quantity; each layer is.)
+    cfg = _12b(48, [l for l in range(48) if (l + 1) % 6 == 0])
+    m, om, layers, clock, slot, active = _populated_step(gpu, cfg)
     try:
         caches = [(d["k_cache"].copy(), d["v_cache"].copy()) for d in layers]
+        m.set_trace(True)
         x = m.embed(123456)
         tok = m.forward(x, clock, slot, active)
         logits = m.read(-1, gh.T_LOGITS, np.float32)
-        rtok, _, rlog = om.forward(x, clock, slot, active, True, NT)
-        row_ref = layers[0]["k_cache"][slot].copy()
+        trace = [m.read(l, gh.T_TRACE, np.float32) for l in range(49)]
+        assert np.array_equal(trace[0], x)
+        assert np.array_equal(trace[48], m.read(-1, gh.T_HIDDEN, np.float32))
+        H, nq = cfg.hidden_size, cfg.num_attention_heads
+        head = m.read(-1, gh.T_LM_HEAD, np.uint32).reshape(cfg.vocab_size, -1)
+        fn = m.read(-1, gh.T_FINAL_NORM, np.float32)
+        for l in range(48):
+            d = dict(layers[l], k_cache=caches[l][0].copy(), v_cache=caches[l][1].copy())
+            one = orc.Model(H, cfg.intermediate_size, cfg.vocab_size, nq, [d], head, fn)
+            _, xo, _ = one.forward(trace[l], clock, slot, active, False, NT)
+            assert_close(trace[l + 1], xo, what="layer %d output" % l)
+            kc = m.read(l, gh.T_K_CACHE, np.float32).reshape(640, -1)
+            vc = m.read(l, gh.T_V_CACHE, np.float32).reshape(640, -1)
+            assert_close(kc[slot], d["k_cache"][slot], what="K row layer %d" % l)
+            assert_close(vc[slot], d["v_cache"][slot], what="V row layer %d" % l)
+        tail = orc.Model(H, cfg.intermediate_size, cfg.vocab_size, nq, [], head, fn)
+        htok, _, hlog = tail.forward(trace[48], clock, slot, active, True, NT)
+        check_token(m, hlog, tok, htok, "LM head from the device's final residual")
+        # the whole step end to end: the greedy token
         for d, (kc, vc) in zip(layers, caches):
             d["k_cache"][:] = kc
             d["v_cache"][:] = vc
-        xp = (x * (1 + 1e-6 * np.sign(np.sin(np.arange(x.size))))).astype(np.float32)
-        _, _, rlog_p = om.forward(xp, clock, slot, active, True, NT)
-        sens = errors(rlog_p, rlog)[0]
-        err = errors(logits, rlog)[0]
-        assert tok == rtok and tok == orc.argmax(logits)
-        assert err <= max(2e-3, 3 * sens), (err, sens)
-        kc = m.read(0, gh.T_K_CACHE, np.float32).reshape(640, -1)
-        assert_close(kc[slot], row_ref, what="K row layer 0")
+        rtok, _, rlog = om.forward(x, clock, slot, active, True, NT)
+        if tok != rtok:
+            err = float(np.max(np.abs(logits.astype(np.float64) - rlog)))
+            assert 0.0 <= float(rlog[rtok] - rlog[tok]) <= 2.0 * err
     finally:
         m.close()

@@ -56,6 +56,28 @@ def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     assert_close(got, ref, what="prefill GeGLU")
 
 
+# The 128x64 gate/up tile (gh_pf_gateup_q{4,8}_m128_n64_k1) runs when
+# ceil(N / 64) * ceil(T / 128) reaches the CU count (256): the 12B gate/up of
+# a 512-token prompt (960 tiles) and a ragged 129-token batch of exactly 256
+# tiles (its second 128-row tile holds one token).
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("T,N,K", [(512, 15360, 3840), (129, 8192, 512)])
+def test_prefill_gate_up_large_tiles(gpu, mode, T, N, K):
+    assert -(-N // 64) * -(-T // 128) >= 256
+    gq, gdeq = quantized(N, K, mode, 340)
+    uq, udeq = quantized(N, K, mode, 341)
+    a = gh.synth_normal(T * K, 1, 342, 0.0, 1.0).reshape(T, K)
+    Wg, Wu, A, act = gpu.upload(gq), gpu.upload(uq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gate_up_geglu(mode, Wg, Wu, A, act, T, N, K)
+    got = act.read(np.float32, T * N).reshape(T, N)
+    a64 = np.asarray(a, np.float64)
+    ref = nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T)
+    del gdeq, udeq
+    assert_close(got, ref, what="prefill GeGLU, 128x64 tiles")
+    for t in (0, T - 1):  # first and last rows, one of them alone in its tile
+        assert_close(got[t], ref[t], what="prefill GeGLU row %d" % t)
+
+
 def test_prefill_gemm_row_range(gpu):
     # rows far outside fp16 range (1e6, 1e-7), a zero row and mixed magnitudes
     # within a row: the per-row power-of-two scale keeps every row exact to

@@ -9,6 +9,7 @@
 // norm and the activations.  The per-token graph (5 kernels a layer + the LM
 // head) is captured once into a HIP graph with the small host->device copies
 // of x, the active list and the step parameters, and replayed per token.
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -76,6 +77,9 @@ struct gh_model {
   // per-layer residual trace: row l = layer l's input, row L = the final residual
   float* trace = nullptr;
   bool trace_on = false;
+  // GH_EAGER_DECODE=1 (read at init): each token launches its kernels
+  // directly instead of replaying the recorded graph (for kernel tracing).
+  bool eager = false;
   // batched prefill buffers (gh_model_prefill), sized for pf_cap tokens
   uint32_t pf_cap = 0, pf_stride = 0;
   uint8_t* pf_arena = nullptr;
@@ -419,6 +423,8 @@ gh_status record_graphs(gh_model* m) {
 }
 
 gh_status finish_init(gh_model* m, gh_model** out) {
+  const char* eager = getenv("GH_EAGER_DECODE");
+  m->eager = eager && eager[0] == '1';
   gh_status st = record_graphs(m);
   if (st != GH_OK) {
     delete m;
@@ -458,7 +464,8 @@ gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_t
   hipStream_t s = m->ctx->stream;
   hipError_t e = hipMemcpyAsync(m->arena + m->io, m->h_io, bytes, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "forward: input copy");
-  gh_status st = gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
+  gh_status st = m->eager ? record_forward(m, want_logits)
+                          : gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
   if (st != GH_OK) return st;
   if (want_logits) {
     e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost, s);

@@ -153,7 +153,11 @@ def bench_gemv(ctx, reps=256):
 
 def timed_graph(ctx, launch, reps):
     """Average ms of one launch: `reps` launches recorded once as a graph,
-    replayed once untimed, then timed with HIP events on the context stream."""
+    replayed once untimed, then timed with HIP events on the context stream.
+    One eager launch first: an entry point's first call may allocate its
+    scratch, which a capture refuses."""
+    launch(0)
+    ctx.sync()
     ctx.graph_begin()
     for i in range(reps):
         launch(i)

@@ -217,3 +217,25 @@ def test_12b_shaped_decode_step(gpu):
             assert 0.0 <= float(rlog[rtok] - rlog[tok]) <= 2.0 * err
     finally:
         m.close()
+
+
+def test_eager_decode_matches_graph(gpu, monkeypatch):
+    # GH_EAGER_DECODE=1 launches each token's kernels directly (for kernel
+    # tracing): the same kernels on the same inputs give the same bits
+    cfg = tiny_cfg()
+    mg = gh.Model(gpu, cfg, seed=9)
+    monkeypatch.setenv("GH_EAGER_DECODE", "1")
+    me = gh.Model(gpu, cfg, seed=9)
+    try:
+        for m in (mg, me):
+            m.ring_init(4, 16, 4)
+        for c in range(30):
+            x = mg.embed(c * 7 % cfg.vocab_size)
+            want = c % 2 == 0
+            assert mg.forward_clock(x, c, want) == me.forward_clock(x, c, want)
+            if want:
+                assert np.array_equal(mg.read(-1, gh.T_LOGITS, np.float32),
+                                      me.read(-1, gh.T_LOGITS, np.float32))
+    finally:
+        mg.close()
+        me.close()

@@ -30,6 +30,7 @@ KERNEL_FAMILIES = ["gemv", "gemv_norm", "util", "attn", "norm", "prefill"]
 FAMILY_FLAGS = {"prefill": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 HOST_SOURCES = ["runtime.cpp", "engine.cpp", "model.cpp", "ring.cpp"]
+HIP_HOST_SOURCES = ["noalloc.hip"]
 HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-pthread", "-ffp-contract=off",
               "-Wall", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
               "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
@@ -63,8 +64,21 @@ def build_kernels():
 def build_host():
     srcs = [os.path.join(CSRC, "runtime", s) for s in HOST_SOURCES
             if os.path.exists(os.path.join(CSRC, "runtime", s))]
+    # Host sources with device variables of their own (the allocation-free
+    # entry point's scratch array) go through hipcc, which embeds their gfx950
+    # code object in the library.
+    objs = []
+    bdir = os.path.join(PKG, "_build")
+    os.makedirs(bdir, exist_ok=True)
+    for src in HIP_HOST_SOURCES:
+        obj = os.path.join(bdir, os.path.splitext(src)[0] + ".o")
+        _run([HIPCC, "-c", "-fPIC", "-O2", "-std=c++17", "--offload-arch=gfx950",
+              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+              "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+              os.path.join(CSRC, "runtime", src), "-o", obj])
+        objs.append(obj)
     tmp = LIB_PATH + ".tmp"
-    _run(["g++"] + HOST_FLAGS + srcs + ["-o", tmp] + HOST_LIBS)
+    _run(["g++"] + HOST_FLAGS + srcs + objs + ["-o", tmp] + HOST_LIBS)
     os.replace(tmp, LIB_PATH)
 
 

@@ -412,6 +412,44 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   return launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes);
 }
 
+gh_status fused_attn_args(gh_context* ctx, const float* Q_in, const float* K_in,
+                          const float* V_in, const float* Q_norm, const float* K_norm,
+                          float* K_cache, float* V_cache, const uint32_t* active_slots,
+                          const uint32_t* step_params, float* out, uint32_t num_q,
+                          uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
+                          uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
+                          const char* who, AttnLaunch* L, size_t* part_bytes) {
+  if (!ctx || !Q_in || !K_in || (!V_in && !k_eq_v) || !Q_norm || !K_norm || !K_cache ||
+      !V_cache || !active_slots || !step_params || !out)
+    return fail(GH_ERR_INVALID, std::string(who) + ": null pointer");
+  if (num_kv == 0 || num_q % num_kv || rotary_dim > head_dim || rotary_dim % 2 || max_slots == 0)
+    return fail(GH_ERR_INVALID, std::string(who) + ": bad head shape");
+  *L = AttnLaunch{};
+  AttnArgs& a = L->args;
+  a.q = Q_in;
+  a.k_in = K_in;
+  a.v_in = V_in ? V_in : K_in;
+  a.q_norm = Q_norm;
+  a.k_norm = K_norm;
+  a.k_cache = K_cache;
+  a.v_cache = V_cache;
+  a.active = active_slots;
+  a.step = step_params;
+  a.out = out;
+  a.nq = num_q;
+  a.nkv = num_kv;
+  a.D = head_dim;
+  a.rot = rotary_dim;
+  a.k_eq_v = k_eq_v ? 1 : 0;
+  a.fuse = 1;
+  a.theta = theta;
+  a.eps = eps;
+  a.scale = 1.0f;  // inv_sqrt_dim = 1.0 (src/model/forward.zig:80)
+  a.nsplit = attention_splits(ctx, num_kv, max_slots);
+  *part_bytes = (size_t)num_kv * a.nsplit * (num_q / num_kv) * (head_dim + 4) * 4;
+  return GH_OK;
+}
+
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {
   // about 32 slots per split (8 per wave), at most ~one workgroup per CU
   uint32_t ns = std::max<uint32_t>(1u, (max_slots + 31) / 32);
@@ -464,37 +502,16 @@ gh_status gh_qkv_rope_attn(gh_context* ctx, const float* Q_in, const float* K_in
                            const uint32_t* step_params, float* out, uint32_t num_q,
                            uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
                            uint32_t k_eq_v, float theta, float eps, uint32_t max_slots) {
-  if (!ctx || !Q_in || !K_in || (!V_in && !k_eq_v) || !Q_norm || !K_norm || !K_cache ||
-      !V_cache || !active_slots || !step_params || !out)
-    return fail(GH_ERR_INVALID, "gh_qkv_rope_attn: null pointer");
-  if (num_kv == 0 || num_q % num_kv || rotary_dim > head_dim || rotary_dim % 2 || max_slots == 0)
-    return fail(GH_ERR_INVALID, "gh_qkv_rope_attn: bad head shape");
   gh::AttnLaunch L{};
-  AttnArgs& a = L.args;
-  a.q = Q_in;
-  a.k_in = K_in;
-  a.v_in = V_in ? V_in : K_in;
-  a.q_norm = Q_norm;
-  a.k_norm = K_norm;
-  a.k_cache = K_cache;
-  a.v_cache = V_cache;
-  a.active = active_slots;
-  a.step = step_params;
-  a.out = out;
-  a.nq = num_q;
-  a.nkv = num_kv;
-  a.D = head_dim;
-  a.rot = rotary_dim;
-  a.k_eq_v = k_eq_v ? 1 : 0;
-  a.fuse = 1;
-  a.theta = theta;
-  a.eps = eps;
-  a.scale = 1.0f;  // inv_sqrt_dim = 1.0 (src/model/forward.zig:80)
-  a.nsplit = gh::attention_splits(ctx, num_kv, max_slots);
-  const size_t part_bytes = (size_t)num_kv * a.nsplit * (num_q / num_kv) * (head_dim + 4) * 4;
-  gh_status st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes, part_bytes);
+  size_t part_bytes = 0;
+  gh_status st = gh::fused_attn_args(ctx, Q_in, K_in, V_in, Q_norm, K_norm, K_cache, V_cache,
+                                     active_slots, step_params, out, num_q, num_kv, head_dim,
+                                     rotary_dim, k_eq_v, theta, eps, max_slots, "gh_qkv_rope_attn",
+                                     &L, &part_bytes);
   if (st != GH_OK) return st;
-  a.part = static_cast<float*>(ctx->attn_scratch);
+  st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes, part_bytes);
+  if (st != GH_OK) return st;
+  L.args.part = static_cast<float*>(ctx->attn_scratch);
   return gh::launch_attention(ctx, L);
 }
 

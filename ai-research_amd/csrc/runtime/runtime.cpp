@@ -203,6 +203,9 @@ gh_status gh_context_init(const char* code_object_dir, gh_context** out) {
     delete ctx;
     return st;
   }
+  // the allocation-free entry point's scratch address on this device; a
+  // failure is reported by that entry point, the rest of the library works
+  gh::noalloc_setup(ctx->device);
   *out = ctx;
   return GH_OK;
 }

@@ -76,6 +76,16 @@ struct StreamShape {
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out);
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
+// Argument checks and the launch block of the fused q/k norm + RoPE + cache
+// write + split-K attention (gh_qkv_rope_attn and its allocation-free
+// variant); the caller supplies the split partials (*part_bytes bytes).
+gh_status fused_attn_args(gh_context* ctx, const float* Q_in, const float* K_in,
+                          const float* V_in, const float* Q_norm, const float* K_norm,
+                          float* K_cache, float* V_cache, const uint32_t* active_slots,
+                          const uint32_t* step_params, float* out, uint32_t num_q,
+                          uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
+                          uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
+                          const char* who, AttnLaunch* L, size_t* part_bytes);
 // Prefill MFMA GEMM (prefill.hip): C [T][N] = A [T][K] . deq(W0)^T, or with
 // W1, C = gelu_tanh(A . deq(W0)^T) * (A . deq(W1)^T); A and C f32.
 // A single product (W1 null) may leave a K split unsummed: with planes
@@ -92,6 +102,9 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                     const void* W1, const void* Ax, const float* rs, float* C,
                                     uint32_t T, uint32_t N, uint32_t K,
                                     const float** planes = nullptr, uint32_t* nplanes = nullptr);
+// Resolves the allocation-free entry point's device scratch for `device`
+// (noalloc.hip); called by gh_context_init with that device current.
+gh_status noalloc_setup(int device);
 // Internal helpers of the host ring (ring.cpp).
 gh_ring* ring_clone(const gh_ring* r);
 void ring_state(const gh_ring* r, uint32_t layer, uint32_t* clocks, uint32_t* flags, uint32_t n);

@@ -207,6 +207,22 @@ gh_status gh_qkv_rope_attn(gh_context *ctx, const float *Q_in, const float *K_in
                            const uint32_t *step_params, float *out, uint32_t num_q,
                            uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
                            uint32_t k_eq_v, float theta, float eps, uint32_t max_slots);
+/* gh_qkv_rope_attn without any allocation (no reference counterpart: it is
+ * for callers that cannot allocate -- code under HIP graph capture, serving
+ * loops or harnesses that forbid hipMalloc).  Same arguments, kernels and
+ * results; the split partials live in a fixed 1 MiB device array of this
+ * library (one per GPU, held until the process ends) instead of context
+ * scratch that the first call allocates.  Shapes whose partials need more
+ * (num_kv * splits * (num_q / num_kv) * (head_dim + 4) * 4 bytes; 332,800
+ * for 8 kv heads of 256 with 2 query heads each at 640 slots) are refused
+ * with GH_ERR_UNSUPPORTED.  All calls on one GPU share the array: calls that
+ * overlap on one GPU (other streams or threads) race. */
+gh_status gh_qkv_rope_attn_noalloc(gh_context *ctx, const float *Q_in, const float *K_in,
+                                   const float *V_in, const float *Q_norm, const float *K_norm,
+                                   float *K_cache, float *V_cache, const uint32_t *active_slots,
+                                   const uint32_t *step_params, float *out, uint32_t num_q,
+                                   uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
+                                   uint32_t k_eq_v, float theta, float eps, uint32_t max_slots);
 /* recordArgmax (kernels.zig:139-142), shaders/argmax.wgsl, with the CPU
  * path's tie rule (sampleArgmax, src/kernels.zig:164-174): the lowest index
  * of the largest value.  out_token is a device u32. */

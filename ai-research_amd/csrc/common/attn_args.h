@@ -26,4 +26,10 @@ struct AttnArgs {
   // grouped prefill (gh_pf_attn_g_*): tokens in the batch; active/n_active
   // then hold one union list per group of consecutive tokens
   uint32_t n_tokens;
+  // decode: *flags bit 1 (value 2) set means the active list is 0 .. S-1, so
+  // slot i is i and the list need not be read (null: read the list)
+  const uint32_t* flags;
+  // decode, fused: cos[ROPE_TAB_HALF] then sin[ROPE_TAB_HALF] of this
+  // token's angles for this layer's (rot, theta) (null: computed in-kernel)
+  const float* rope_tab;
 };

@@ -29,6 +29,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../common/rope.h"
+
 #define ATT_NT 256
 #define ATT_WAVES (ATT_NT / 64)
 #define MAX_D 512
@@ -174,13 +176,24 @@ __device__ __forceinline__ void rope_angles(uint32_t rot, float theta, uint32_t 
     const uint32_t i = lane + 64 * k;
     c[k] = 1.f;
     s[k] = 0.f;
-    if (i < rot / 2) {
-      const float freq = 1.0f / powf(theta, (2.0f * (float)i) / (float)rot);
-      const float ang = (float)clock * freq;
-      c[k] = cosf(ang);
-      s[k] = sinf(ang);
-    }
+    if (i < rot / 2) gh_rope_angle(i, rot, theta, clock, &c[k], &s[k]);
   }
+}
+
+// The same angles read from a per-token table (cos then sin, ROPE_TAB_HALF
+// each) that the step kernel wrote with gh_rope_angle.
+__device__ __forceinline__ void rope_angles_tab(const float* __restrict__ tab, uint32_t rot,
+                                                uint32_t lane, float* c, float* s) {
+#pragma unroll
+  for (int k = 0; k < ROPE_K; k++) {
+    // lanes past rot / 2 load a valid entry they never use (rope_lds reads
+    // the angles of pairs i < rot / 2 only): no branch, no select, so the
+    // loads stay in flight until the rotation needs them
+    const uint32_t ic = min(lane + 64u * k, (uint32_t)ROPE_TAB_HALF - 1u);
+    c[k] = tab[ic];
+    s[k] = tab[ROPE_TAB_HALF + ic];
+  }
+  (void)rot;
 }
 
 // Partial RoPE in place on an LDS head, one wavefront: pairs (i, i + rot/2)
@@ -383,10 +396,268 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { attn_split<1, 8, false>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_split<2, 8, false>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_split<4, 8, false>(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_split<8, 4, false>(a); }
+// ---------------------------------------------------------------------------
+// Decode attention, one workgroup per (kv head, split of the active list).
+// The same work as attn_split's decode form, ordered for latency: a kernel
+// this small is a chain of memory round trips, so every load that does not
+// depend on another goes out first.
+//  - Each wave reads its own tile's slot numbers (lanes 0..T-1, broadcast
+//    with readlane) instead of staging the split's list in LDS behind a
+//    barrier; when the step flags say the list is 0 .. S-1 it reads nothing.
+//  - Fused: each wave loads its prologue head rows (q heads, this token's k
+//    and v, their norm weights, the RoPE table) and then its first tile's
+//    K/V rows, and only then normalises; the K/V latency hides the prologue.
+//    Loads complete in order, so the prologue's waits do not wait for K/V.
+//  - RoPE angles come from the per-token table when one is given.
+// This token's own slot is served from LDS (its cache row is written by
+// split 0 in the same launch).  Waves merge through LDS and each split
+// writes (o, m, l) for gh_attn_merge_k, as attn_split does.
+// ---------------------------------------------------------------------------
+// A zero the compiler cannot see through, so a value derived from it counts
+// as per-lane: a slot number loaded with it stays in a vector register
+// instead of being moved to a scalar one (and waited for) right after its
+// load.
+__device__ __forceinline__ uint32_t opaque_zero() {
+  uint32_t z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
+struct DecodeSmem {
+  float qs[MAX_G][MAX_D];
+  float knew[MAX_D], vnew[MAX_D];
+  float wm[ATT_WAVES][MAX_G], wl[ATT_WAVES][MAX_G];
+  float wo[ATT_WAVES][MAX_G][MAX_D];
+};
+
+// DENSE: the list is 0 .. S-1 (step flags bit 1) and is not read.  The two
+// forms are separate straight-line bodies, so no load sits under a branch.
+template <int DPL, int T, bool DENSE>
+__device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
+  auto& qs = sm.qs;
+  auto& knew = sm.knew;
+  auto& vnew = sm.vnew;
+  auto& wm = sm.wm;
+  auto& wl = sm.wl;
+  auto& wo = sm.wo;
+
+  const uint32_t D = a.D, G = a.nq / a.nkv;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const size_t kv_dim = (size_t)a.nkv * D;
+  const uint32_t nsplit = a.nsplit;
+  const uint32_t kvh = blockIdx.x / nsplit, split = blockIdx.x % nsplit;
+  const uint32_t clock = a.step[0], cur_slot = a.step[1], S = a.step[2];
+  const bool fuse = a.fuse != 0;
+  const uint32_t per = (S + nsplit - 1) / nsplit;
+  const uint32_t s0 = min(S, split * per), s1 = min(S, s0 + per);
+  const uint32_t n = s1 - s0;
+  const uint32_t d0 = lane * DPL;
+  const bool dl = d0 < D;
+  const uint32_t dc = dl ? d0 : 0u;  // loads stay in bounds; lanes past D are ignored
+  const float* kbase = a.k_cache + (size_t)kvh * D + dc;
+  const float* vbase = a.v_cache + (size_t)kvh * D + dc;
+  const uint32_t last = S > 0u ? S - 1u : 0u;  // the last list position (S = 0: none read)
+
+  // Slot numbers of a tile starting at list position s0 + base, clamped to the
+  // split (the extra entries are masked in the softmax): scalar loads, so
+  // waiting for them never waits for a vector load.
+  // With S = 0 no list entry exists: position 0 of the step record stands in.
+  const uint32_t* lp = S > 0u ? a.active : a.step;
+  auto tile_slots = [&](uint32_t base, uint32_t* sl) {
+    const uint32_t z = DENSE ? 0u : opaque_zero();
+#pragma unroll
+    for (int j = 0; j < T; j++) {
+      const uint32_t pos = min(s0 + min(base + (uint32_t)j, n > 0u ? n - 1u : 0u), last);
+      if constexpr (DENSE)
+        sl[j] = pos;
+      else
+        sl[j] = lp[pos + z];  // with S = 0 the slot read is never used
+    }
+  };
+
+  // 1. this wave's first tile's slot numbers (the earliest loads)
+  const uint32_t base0 = wave * T;
+  uint32_t slot0[T];
+  tile_slots(base0, slot0);
+  // the scheduler keeps the phases in this order: slot numbers, prologue
+  // loads, K/V loads; the first wait (for the slot numbers) then leaves the
+  // prologue loads in flight
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. prologue loads: up to two head rows per wave (G query heads, then
+  //    this token's k and v), their norm weights, the RoPE angles.  Every
+  //    pointer is valid in every mode (the host passes real rows), so the
+  //    loads need no branch.
+  float hv[2][DPL], hw[2][DPL], rc[ROPE_K], rs[ROPE_K];
+  const uint32_t nheads = fuse ? G + 2 : G;
+  if (fuse && a.rope_tab) rope_angles_tab(a.rope_tab, a.rot, lane, rc, rs);
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const uint32_t g = min(wave + (uint32_t)h * ATT_WAVES, nheads - 1);
+    const float* src = g < G ? a.q + (size_t)(kvh * G + g) * D
+                       : g == G ? a.k_in + (size_t)kvh * D
+                                : (a.k_eq_v ? a.k_in : a.v_in) + (size_t)kvh * D;
+    load_row<DPL>(src + dc, hv[h]);
+    load_row<DPL>((g == G ? a.k_norm : a.q_norm) + dc, hw[h]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. the first tile's K/V rows (this token's own slot is replaced from LDS
+  //    after the prologue)
+  float kr[T][DPL], vr[T][DPL];
+#pragma unroll
+  for (int j = 0; j < T; j++) {
+    load_row<DPL>(kbase + (size_t)slot0[j] * kv_dim, kr[j]);
+    load_row<DPL>(vbase + (size_t)slot0[j] * kv_dim, vr[j]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. prologue compute: normalise (fused) or copy the heads into LDS
+  if (fuse && !a.rope_tab) rope_angles(a.rot, a.theta, clock, lane, rc, rs);
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const uint32_t g = wave + (uint32_t)h * ATT_WAVES;
+    if (g < nheads) {
+      float inv = 1.f;
+      if (fuse) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < DPL; j++) ss += dl ? hv[h][j] * hv[h][j] : 0.f;
+        inv = 1.0f / sqrtf(wave_allsum(ss) / (float)D + a.eps);
+      }
+      const bool weighted = fuse && g <= G;  // v is normalised to unit RMS only
+      float* out = g < G ? qs[g] : g == G ? knew : vnew;
+      if (dl) {
+#pragma unroll
+        for (int j = 0; j < DPL; j++)
+          out[d0 + j] = fuse ? hv[h][j] * inv * (weighted ? hw[h][j] : 1.0f) : hv[h][j];
+      }
+    }
+  }
+  __syncthreads();
+  if (fuse)
+    for (uint32_t g = wave; g < G + 1; g += ATT_WAVES) rope_lds(g < G ? qs[g] : knew, a.rot, rc, rs, lane);
+  __syncthreads();
+  if (fuse && split == 0) {  // ring_buffer.writeKV for this layer
+    float* kc = a.k_cache + (size_t)cur_slot * kv_dim + (size_t)kvh * D;
+    float* vc = a.v_cache + (size_t)cur_slot * kv_dim + (size_t)kvh * D;
+    for (uint32_t d = tid; d < D; d += ATT_NT) {
+      kc[d] = knew[d];
+      vc[d] = vnew[d];
+    }
+  }
+
+  // 5. online softmax over the wave's tiles
+  float q[MAX_G][DPL], o[MAX_G][DPL], m[MAX_G], l[MAX_G];
+#pragma unroll
+  for (int g = 0; g < MAX_G; g++) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; j++) {
+      q[g][j] = (g < (int)G && dl) ? qs[g][d0 + j] : 0.f;
+      o[g][j] = 0.f;
+    }
+  }
+  for (uint32_t base = base0; base < n; base += ATT_WAVES * T) {
+    if (base != base0) {  // later tiles: slot numbers, then the rows
+      tile_slots(base, slot0);
+#pragma unroll
+      for (int j = 0; j < T; j++) {
+        load_row<DPL>(kbase + (size_t)slot0[j] * kv_dim, kr[j]);
+        load_row<DPL>(vbase + (size_t)slot0[j] * kv_dim, vr[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < T; j++) {
+      if (fuse && slot0[j] == cur_slot) {  // this token's K/V: from LDS, not the cache
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+          kr[j][e] = dl ? knew[d0 + e] : 0.f;
+          vr[j][e] = dl ? vnew[d0 + e] : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < MAX_G; g++) {
+      if (g >= (int)G) break;
+      float sc[T];
+#pragma unroll
+      for (int j = 0; j < T; j++) {
+        float p = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) p += q[g][e] * kr[j][e];
+        sc[j] = p;
+      }
+#pragma unroll
+      for (int j = 0; j < T; j++) sc[j] = wave_allsum(sc[j]) * a.scale;
+      float mt = m[g];
+#pragma unroll
+      for (int j = 0; j < T; j++)
+        if (base + j < n) mt = fmaxf(mt, sc[j]);
+      const float corr = __expf(m[g] - mt);  // m = -inf, mt finite: 0
+      l[g] *= corr;
+#pragma unroll
+      for (int e = 0; e < DPL; e++) o[g][e] *= corr;
+#pragma unroll
+      for (int j = 0; j < T; j++) {
+        const float p = base + j < n ? __expf(sc[j] - mt) : 0.f;
+        l[g] += p;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) o[g][e] += p * vr[j][e];
+      }
+      m[g] = mt;
+    }
+  }
+
+  // 6. merge the waves (wave order), write the split partial (o, m, l)
+#pragma unroll
+  for (int g = 0; g < MAX_G; g++) {
+    if (g >= (int)G) break;
+    if (lane == 0) {
+      wm[wave][g] = m[g];
+      wl[wave][g] = l[g];
+    }
+    if (dl) {
+#pragma unroll
+      for (int e = 0; e < DPL; e++) wo[wave][g][d0 + e] = o[g][e];
+    }
+  }
+  __syncthreads();
+  const uint32_t PS = D + 4;
+  float* part = a.part + ((size_t)kvh * nsplit + split) * G * PS;
+  for (uint32_t i = tid; i < G * D; i += ATT_NT) {
+    const uint32_t g = i / D, d = i % D;
+    float M = -INFINITY;
+    for (int w = 0; w < ATT_WAVES; w++) M = fmaxf(M, wm[w][g]);
+    float L = 0.f, O = 0.f;
+    for (int w = 0; w < ATT_WAVES; w++) {
+      const float c = wm[w][g] == -INFINITY ? 0.f : __expf(wm[w][g] - M);
+      L += wl[w][g] * c;
+      O += wo[w][g][d] * c;
+    }
+    part[g * PS + d] = O;
+    if (d == 0) {
+      part[g * PS + D] = M;
+      part[g * PS + D + 1] = L;
+    }
+  }
+}
+
+template <int DPL, int T>
+__device__ __forceinline__ void attn_decode_k(const AttnArgs& a) {
+  __shared__ DecodeSmem sm;
+  if (a.flags != nullptr && (*a.flags & 2u) != 0u)
+    attn_decode<DPL, T, true>(a, sm);
+  else
+    attn_decode<DPL, T, false>(a, sm);
+}
+
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { attn_decode_k<1, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_decode_k<2, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_decode_k<4, 8>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_decode_k<8, 4>(a); }
 
 // Batched prefill: grid (kv heads, tokens); each workgroup runs token
 // blockIdx.y's whole active list (q already normalised and roped by

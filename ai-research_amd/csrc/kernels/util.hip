@@ -5,6 +5,7 @@
 
 #include "../common/quant_block.h"
 #include "../common/synth.h"
+#include "../common/rope.h"
 
 // 8 consecutive elements per thread: one 32-byte (f32: 2 x 16 B) store run.
 extern "C" __global__ __launch_bounds__(256) void gh_synth_normal_f32_k(
@@ -117,13 +118,21 @@ extern "C" __global__ __launch_bounds__(256) void gh_copy_u32_k(uint32_t* dst, c
     dst[i] = src[i];
 }
 
-// Device-resident ring bookkeeping for one decode token (the layer-0 state of
-// DynamicRingBuffer, src/ring_buffer.zig:56-136, as src/model/forward.zig:42-43
-// uses it).  step = {clock, slot_idx, S, mode}: with mode 1 the kernel
-// activates the clock's slot (activateSlot: clocks[slot] = clock, flag set)
-// and writes slot_idx, S and the active list (getActiveSlots); any other mode
-// leaves the host's slot_idx, S and list, and only records the activation of
-// slot_idx, so that the device state follows host-driven steps too.  The list is the slot-order
+// The per-token step kernel at the head of every decode graph.
+//
+// RoPE tables: for each of the model's two layer types (rot_t, theta_t; rot 0
+// = unused) it writes cos then sin of this clock's angles (gh_rope_angle, the
+// attention prologue's own definition) to rope_tab[t], so the 48 attention
+// launches of a token read angles instead of each recomputing powf/cosf/sinf.
+//
+// Ring bookkeeping: the layer-0 state of DynamicRingBuffer
+// (src/ring_buffer.zig:56-136, as src/model/forward.zig:42-43 drives it).
+// step = {clock, slot_idx, S, flags}.  flags bit 0 set: the kernel activates
+// the clock's slot (activateSlot: clocks[slot] = clock, flag set), writes
+// slot_idx, S and the active list (getActiveSlots), and sets flags bit 1
+// when the list is 0 .. S-1.  Bit 0 clear: the host wrote slot_idx, S, the
+// list and bit 1; the kernel only records the activation of slot_idx, so the
+// device state follows host-driven steps too.  The list is the slot-order
 // compaction of one predicate, because the three tiers are contiguous and
 // each tier is listed in slot order:
 //   anchors  s < min(clock + 1, A) and active
@@ -133,23 +142,38 @@ extern "C" __global__ __launch_bounds__(256) void gh_copy_u32_k(uint32_t* dst, c
 // ballot prefix per wavefront and the wavefront counts scanned in LDS.
 extern "C" __global__ __launch_bounds__(1024) void gh_ring_step_k(
     uint32_t* ring_clock, uint32_t* ring_flag, uint32_t* step, uint32_t* active, uint32_t A,
-    uint32_t W, uint32_t R) {
+    uint32_t W, uint32_t R, float* rope_tab, uint32_t rot0, float theta0, uint32_t rot1,
+    float theta1) {
   __shared__ uint32_t wave_n[16];
-  __shared__ uint32_t base_n;
-  if (step[3] != 1u) {
-    if (threadIdx.x == 0 && step[1] < A + W + R) {
-      ring_clock[step[1]] = step[0];
+  __shared__ uint32_t base_n, last_on;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t flags = step[3];
+  const uint32_t c = step[0];
+  {  // RoPE tables: threads [0, 512) type 0, [512, 1024) type 1
+    const uint32_t t = tid >> 9, i = tid & 511u;
+    const uint32_t rot = t ? rot1 : rot0;
+    if (i < rot / 2 && i < ROPE_TAB_HALF) {
+      float cs, sn;
+      gh_rope_angle(i, rot, t ? theta1 : theta0, c, &cs, &sn);
+      rope_tab[t * 2 * ROPE_TAB_HALF + i] = cs;
+      rope_tab[t * 2 * ROPE_TAB_HALF + ROPE_TAB_HALF + i] = sn;
+    }
+  }
+  if ((flags & 1u) == 0u) {
+    if (tid == 0 && step[1] < A + W + R) {
+      ring_clock[step[1]] = c;
       ring_flag[step[1]] = 1u;
     }
     return;
   }
-  const uint32_t c = step[0];
   const uint32_t slot = c < A ? c : A + (c - A) % W;
   const uint32_t total = A + W + R;
   const uint32_t alim = c + 1u < A ? c + 1u : A;
   const uint32_t minc = c >= W ? c - W + 1u : A;
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  if (tid == 0) base_n = 0;
+  if (tid == 0) {
+    base_n = 0;
+    last_on = 0;
+  }
   __syncthreads();
   for (uint32_t s0 = 0; s0 < total; s0 += 1024u) {
     const uint32_t s = s0 + tid;
@@ -166,6 +190,7 @@ extern "C" __global__ __launch_bounds__(1024) void gh_ring_step_k(
     }
     const uint64_t mask = __ballot(on);
     if (lane == 0) wave_n[wave] = (uint32_t)__popcll(mask);
+    if (on) atomicMax(&last_on, s);
     __syncthreads();
     uint32_t off = base_n;
     for (uint32_t w = 0; w < wave; w++) off += wave_n[w];
@@ -183,5 +208,21 @@ extern "C" __global__ __launch_bounds__(1024) void gh_ring_step_k(
     ring_flag[slot] = 1u;
     step[1] = slot;
     step[2] = base_n;
+    // the list is 0 .. S-1 exactly when its last (largest) slot is S - 1
+    step[3] = 1u | (base_n > 0u && last_on == base_n - 1u ? 2u : 0u);
+  }
+}
+
+// cos then sin of the RoPE angles at the clock step[0] for one (rot, theta):
+// the table the fused decode attention reads (gh_rope_table).
+extern "C" __global__ __launch_bounds__(256) void gh_rope_table_k(const uint32_t* step,
+                                                                  uint32_t rot, float theta,
+                                                                  float* tab) {
+  const uint32_t c = step[0];
+  for (uint32_t i = threadIdx.x; i < rot / 2 && i < ROPE_TAB_HALF; i += blockDim.x) {
+    float cs, sn;
+    gh_rope_angle(i, rot, theta, c, &cs, &sn);
+    tab[i] = cs;
+    tab[ROPE_TAB_HALF + i] = sn;
   }
 }

@@ -418,7 +418,8 @@ gh_status fused_attn_args(gh_context* ctx, const float* Q_in, const float* K_in,
                           const uint32_t* step_params, float* out, uint32_t num_q,
                           uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
-                          const char* who, AttnLaunch* L, size_t* part_bytes) {
+                          const float* rope_table, const char* who, AttnLaunch* L,
+                          size_t* part_bytes) {
   if (!ctx || !Q_in || !K_in || (!V_in && !k_eq_v) || !Q_norm || !K_norm || !K_cache ||
       !V_cache || !active_slots || !step_params || !out)
     return fail(GH_ERR_INVALID, std::string(who) + ": null pointer");
@@ -445,6 +446,8 @@ gh_status fused_attn_args(gh_context* ctx, const float* Q_in, const float* K_in,
   a.theta = theta;
   a.eps = eps;
   a.scale = 1.0f;  // inv_sqrt_dim = 1.0 (src/model/forward.zig:80)
+  a.flags = step_params + 3;  // bit 1: the list is 0 .. S-1
+  a.rope_tab = rope_table;
   a.nsplit = attention_splits(ctx, num_kv, max_slots);
   *part_bytes = (size_t)num_kv * a.nsplit * (num_q / num_kv) * (head_dim + 4) * 4;
   return GH_OK;
@@ -477,6 +480,9 @@ gh_status gh_decode_attn(gh_context* ctx, const float* Q, const float* K_cache,
   gh::AttnLaunch L{};
   AttnArgs& a = L.args;
   a.q = Q;
+  // unused without the fused prologue, but every row pointer the kernel
+  // loads through must be valid memory: the query rows stand in
+  a.k_in = a.v_in = a.q_norm = a.k_norm = Q;
   a.k_cache = const_cast<float*>(K_cache);
   a.v_cache = const_cast<float*>(V_cache);
   a.active = active_slots;
@@ -488,6 +494,7 @@ gh_status gh_decode_attn(gh_context* ctx, const float* Q, const float* K_cache,
   a.rot = 0;
   a.fuse = 0;
   a.scale = inv_sqrt_dim;
+  a.flags = step_params + 3;  // bit 1: the list is 0 .. S-1
   a.nsplit = gh::attention_splits(ctx, a.nkv, 1024);
   const size_t part_bytes = (size_t)a.nkv * a.nsplit * gqa_ratio * (head_dim + 4) * 4;
   gh_status st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes, part_bytes);
@@ -501,18 +508,28 @@ gh_status gh_qkv_rope_attn(gh_context* ctx, const float* Q_in, const float* K_in
                            float* K_cache, float* V_cache, const uint32_t* active_slots,
                            const uint32_t* step_params, float* out, uint32_t num_q,
                            uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
-                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots) {
+                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
+                           const float* rope_table) {
   gh::AttnLaunch L{};
   size_t part_bytes = 0;
   gh_status st = gh::fused_attn_args(ctx, Q_in, K_in, V_in, Q_norm, K_norm, K_cache, V_cache,
                                      active_slots, step_params, out, num_q, num_kv, head_dim,
-                                     rotary_dim, k_eq_v, theta, eps, max_slots, "gh_qkv_rope_attn",
-                                     &L, &part_bytes);
+                                     rotary_dim, k_eq_v, theta, eps, max_slots, rope_table,
+                                     "gh_qkv_rope_attn", &L, &part_bytes);
   if (st != GH_OK) return st;
   st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes, part_bytes);
   if (st != GH_OK) return st;
   L.args.part = static_cast<float*>(ctx->attn_scratch);
   return gh::launch_attention(ctx, L);
+}
+
+gh_status gh_rope_table(gh_context* ctx, const uint32_t* step_params, uint32_t rotary_dim,
+                        float theta, float* table) {
+  if (!ctx || !step_params || !table) return fail(GH_ERR_INVALID, "gh_rope_table: null pointer");
+  if (rotary_dim == 0 || rotary_dim % 2 || rotary_dim > 512)
+    return fail(GH_ERR_INVALID, "gh_rope_table: rotary_dim must be even, 2..512");
+  void* args[] = {const_cast<uint32_t**>(&step_params), &rotary_dim, &theta, &table};
+  return ctx->launch("gh_rope_table_k", dim3(1), dim3(256), 0, args);
 }
 
 gh_status gh_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W, const float* A,

@@ -60,6 +60,10 @@ struct gh_model {
   size_t io = 0, io_bytes = 0;
   // device-resident ring bookkeeping (layer 0): clock and active flag per slot
   size_t ring_clock = 0, ring_flag = 0;
+  // per-token RoPE tables (cos, sin) of the sliding (0) and full (1) layers
+  size_t rope_tab = 0;
+  uint32_t rope_rot[2] = {0, 0};
+  float rope_theta[2] = {0.f, 0.f};
   uint32_t ring_a = 0, ring_w = 0, ring_r = 0;
   gh_ring* ring = nullptr;  // host mirror of the same state (batched prefill lists)
   uint32_t nsplit = 1, max_q = 0, max_kv = 0;
@@ -197,6 +201,11 @@ gh_status plan(gh_model* m) {
   m->x1 = take(H * 4);
   m->ring_clock = take((size_t)c.max_slots * 4);
   m->ring_flag = take((size_t)c.max_slots * 4);
+  m->rope_tab = take(2 * 2 * 256 * 4);
+  for (auto& L : m->layers) {
+    m->rope_rot[L.full ? 1 : 0] = L.rot;
+    m->rope_theta[L.full ? 1 : 0] = L.theta;
+  }
   uint32_t max_qkv = 0;
   for (auto& L : m->layers) max_qkv = std::max(max_qkv, L.qkv_rows);
   m->qkv_out = take((size_t)max_qkv * 4);
@@ -301,7 +310,9 @@ gh_status record_forward(gh_model* m, bool logits) {
     uint32_t* sp = m->at<uint32_t>(m->step);
     uint32_t* al = m->at<uint32_t>(m->active);
     uint32_t A = m->ring_a, W = std::max(1u, m->ring_w), R = m->ring_r;
-    void* args[] = {&rc, &rf, &sp, &al, &A, &W, &R};
+    float* tab = m->at<float>(m->rope_tab);
+    void* args[] = {&rc, &rf, &sp, &al, &A, &W, &R, &tab, &m->rope_rot[0], &m->rope_theta[0],
+                    &m->rope_rot[1], &m->rope_theta[1]};
     if ((st = ctx->launch("gh_ring_step_k", dim3(1), dim3(1024), 0, args)) != GH_OK) return st;
   }
   if (m->trace_on && (st = copy_words(m, m->trace, m->at<float>(m->x0), H)) != GH_OK) return st;
@@ -344,6 +355,8 @@ gh_status record_forward(gh_model* m, bool logits) {
     a.v_cache = m->at<float>(L.v_cache);
     a.active = m->at<uint32_t>(m->active);
     a.step = m->at<uint32_t>(m->step);
+    a.flags = m->at<uint32_t>(m->step) + 3;
+    a.rope_tab = m->at<float>(m->rope_tab) + (L.full ? 2 * 256 : 0);
     a.part = m->at<float>(m->attn_part);
     a.out = m->at<float>(m->attn_out);
     a.nq = c.num_attention_heads;
@@ -682,7 +695,10 @@ gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits
   m->h_step[0] = (uint32_t)clock;
   m->h_step[1] = slot_idx;
   m->h_step[2] = n_active;
-  m->h_step[3] = 0;  // the list comes from the host
+  // the list comes from the host; bit 1 tells the attention when it is 0 .. S-1
+  bool dense = true;
+  for (uint32_t i = 0; i < n_active && dense; i++) dense = active_slots[i] == i;
+  m->h_step[3] = dense ? 2u : 0u;
   if (m->ring) {  // keep the ring state in step (the ring kernel records the activation)
     if (slot_idx != gh_ring_slot_index(m->ring, clock))
       return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: slot_idx is not the ring's slot "

@@ -54,12 +54,12 @@ extern "C" gh_status gh_qkv_rope_attn_noalloc(
     const float* Q_norm, const float* K_norm, float* K_cache, float* V_cache,
     const uint32_t* active_slots, const uint32_t* step_params, float* out, uint32_t num_q,
     uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim, uint32_t k_eq_v, float theta,
-    float eps, uint32_t max_slots) {
+    float eps, uint32_t max_slots, const float* rope_table) {
   gh::AttnLaunch L{};
   size_t part_bytes = 0;
   gh_status st = gh::fused_attn_args(ctx, Q_in, K_in, V_in, Q_norm, K_norm, K_cache, V_cache,
                                      active_slots, step_params, out, num_q, num_kv, head_dim,
-                                     rotary_dim, k_eq_v, theta, eps, max_slots,
+                                     rotary_dim, k_eq_v, theta, eps, max_slots, rope_table,
                                      "gh_qkv_rope_attn_noalloc", &L, &part_bytes);
   if (st != GH_OK) return st;
   if (part_bytes > kScratchFloats * sizeof(float))

@@ -85,7 +85,8 @@ gh_status fused_attn_args(gh_context* ctx, const float* Q_in, const float* K_in,
                           const uint32_t* step_params, float* out, uint32_t num_q,
                           uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
-                          const char* who, AttnLaunch* L, size_t* part_bytes);
+                          const float* rope_table, const char* who, AttnLaunch* L,
+                          size_t* part_bytes);
 // Prefill MFMA GEMM (prefill.hip): C [T][N] = A [T][K] . deq(W0)^T, or with
 // W1, C = gelu_tanh(A . deq(W0)^T) * (A . deq(W1)^T); A and C f32.
 // A single product (W1 null) may leave a K split unsummed: with planes

@@ -67,8 +67,9 @@ _SIGS = {
                          _u32, _f32, _f32]),
     "gh_decode_attn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _f32, _u32]),
     "gh_argmax": (_i, [_vp, _vp, _vp, _u32]),
-    "gh_qkv_rope_attn": (_i, [_vp] * 11 + [_u32] * 5 + [_f32, _f32, _u32]),
-    "gh_qkv_rope_attn_noalloc": (_i, [_vp] * 11 + [_u32] * 5 + [_f32, _f32, _u32]),
+    "gh_qkv_rope_attn": (_i, [_vp] * 11 + [_u32] * 5 + [_f32, _f32, _u32, _vp]),
+    "gh_qkv_rope_attn_noalloc": (_i, [_vp] * 11 + [_u32] * 5 + [_f32, _f32, _u32, _vp]),
+    "gh_rope_table": (_i, [_vp, _vp, _u32, _f32, _vp]),
     "gh_prefill_gemm": (_i, [_vp, _i, _vp, _vp, _vp, _u32, _u32, _u32]),
     "gh_prefill_gate_up_geglu": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _u32, _u32, _u32]),
 }
@@ -368,19 +369,26 @@ class Context:
                                     gqa_ratio, inv_sqrt_dim, num_q_heads), "gh_decode_attn")
 
     def qkv_rope_attn(self, Q, K, V, Qn, Kn, K_cache, V_cache, active, step, out, num_q, num_kv,
-                      head_dim, rot, k_eq_v, theta, eps=1e-6, max_slots=640):
+                      head_dim, rot, k_eq_v, theta, eps=1e-6, max_slots=640, table=None):
         _check(lib().gh_qkv_rope_attn(self.h, _addr(Q), _addr(K), _addr(V), _addr(Qn), _addr(Kn),
                                       _addr(K_cache), _addr(V_cache), _addr(active), _addr(step),
                                       _addr(out), num_q, num_kv, head_dim, rot, int(k_eq_v),
-                                      theta, eps, max_slots), "gh_qkv_rope_attn")
+                                      theta, eps, max_slots,
+                                      None if table is None else _addr(table)),
+               "gh_qkv_rope_attn")
 
     def qkv_rope_attn_noalloc(self, Q, K, V, Qn, Kn, K_cache, V_cache, active, step, out, num_q,
-                              num_kv, head_dim, rot, k_eq_v, theta, eps=1e-6, max_slots=640):
+                              num_kv, head_dim, rot, k_eq_v, theta, eps=1e-6, max_slots=640,
+                              table=None):
         _check(lib().gh_qkv_rope_attn_noalloc(self.h, _addr(Q), _addr(K), _addr(V), _addr(Qn),
                                               _addr(Kn), _addr(K_cache), _addr(V_cache),
                                               _addr(active), _addr(step), _addr(out), num_q,
                                               num_kv, head_dim, rot, int(k_eq_v), theta, eps,
-                                              max_slots), "gh_qkv_rope_attn_noalloc")
+                                              max_slots, None if table is None else _addr(table)),
+               "gh_qkv_rope_attn_noalloc")
+
+    def rope_table(self, step, rot, theta, table):
+        _check(lib().gh_rope_table(self.h, _addr(step), rot, theta, _addr(table)), "gh_rope_table")
 
     def argmax(self, logits, out_token, vocab):
         _check(lib().gh_argmax(self.h, _addr(logits), _addr(out_token), vocab), "gh_argmax")

@@ -184,7 +184,9 @@ gh_status gh_qkv_rope(gh_context *ctx, const float *Q_in, const float *K_in, con
  * every query head h (kv head h / gqa_ratio), softmax over the S =
  * step_params[2] active slots of inv_sqrt_dim * (Q[h] . K[slot]), then the
  * weighted sum of V[slot].  The reference passes inv_sqrt_dim = 1.0
- * (model/forward.zig:80).  kv_dim = (num_q_heads / gqa_ratio) * head_dim;
+ * (model/forward.zig:80).  step_params[3] bit 1 (value 2; the reference
+ * writes 0) declares the active list to be 0 .. S-1, which spares reading it.
+ * kv_dim = (num_q_heads / gqa_ratio) * head_dim;
  * head_dim % 4 == 0, <= 512; gqa_ratio <= 4.  The first call allocates the
  * context's split-K scratch (do not make that call inside graph capture). */
 gh_status gh_decode_attn(gh_context *ctx, const float *Q, const float *K_cache,
@@ -199,14 +201,26 @@ gh_status gh_decode_attn(gh_context *ctx, const float *Q, const float *K_cache,
  * step_params[1], then attention of every query head (kv head h / (num_q /
  * num_kv), scale 1.0, model/forward.zig:80) over the step_params[2] active
  * slots into out [num_q][head_dim].  Q_in is left unchanged.  max_slots sets
- * the split count as the model's ring does.  The first call allocates the
- * context's split scratch (not inside graph capture). */
+ * the split count as the model's ring does.  rope_table (nullable) holds the
+ * angles as gh_rope_table writes them; null computes them in the kernel.
+ * step_params[3] bit 1 (value 2) may declare the active list to be 0 .. S-1,
+ * which spares reading it.  The first call allocates the context's split
+ * scratch (not inside graph capture). */
 gh_status gh_qkv_rope_attn(gh_context *ctx, const float *Q_in, const float *K_in,
                            const float *V_in, const float *Q_norm, const float *K_norm,
                            float *K_cache, float *V_cache, const uint32_t *active_slots,
                            const uint32_t *step_params, float *out, uint32_t num_q,
                            uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
-                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots);
+                           uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
+                           const float *rope_table);
+/* The RoPE angles of the clock step_params[0] for one (rotary_dim, theta)
+ * into table (device, 512 floats: cos of pairs 0 .. rotary_dim/2 - 1 from
+ * index 0, their sin from index 256), computed as the attention prologue
+ * computes them (applyRopePartial, src/kernels.zig:132-150).  The decode
+ * graph builds the tables of both layer types once per token; passing one
+ * to gh_qkv_rope_attn spares each launch the powf/cosf/sinf work. */
+gh_status gh_rope_table(gh_context *ctx, const uint32_t *step_params, uint32_t rotary_dim,
+                        float theta, float *table);
 /* gh_qkv_rope_attn without any allocation (no reference counterpart: it is
  * for callers that cannot allocate -- code under HIP graph capture, serving
  * loops or harnesses that forbid hipMalloc).  Same arguments, kernels and
@@ -222,7 +236,8 @@ gh_status gh_qkv_rope_attn_noalloc(gh_context *ctx, const float *Q_in, const flo
                                    float *K_cache, float *V_cache, const uint32_t *active_slots,
                                    const uint32_t *step_params, float *out, uint32_t num_q,
                                    uint32_t num_kv, uint32_t head_dim, uint32_t rotary_dim,
-                                   uint32_t k_eq_v, float theta, float eps, uint32_t max_slots);
+                                   uint32_t k_eq_v, float theta, float eps, uint32_t max_slots,
+                                   const float *rope_table);
 /* recordArgmax (kernels.zig:139-142), shaders/argmax.wgsl, with the CPU
  * path's tie rule (sampleArgmax, src/kernels.zig:164-174): the lowest index
  * of the largest value.  out_token is a device u32. */

@@ -111,6 +111,11 @@ def test_decode_attention(gpu, S):
     out = O.read(np.float32, nq * D)
     ref = orc.attention(q, kc, vc, active, nq, nkv, D)
     assert_close(out, ref, what="attention S=%d" % S)
+    if S == slots:  # the list 0 .. S-1, declared in the step flags: same bits
+        ST2 = gpu.upload(np.array([700, 0, S, 2], np.uint32))
+        O2 = gpu.alloc(nq * D * 4)
+        gpu.decode_attn(Q, KC, VC, A, O2, ST2, D, nkv * D, nq // nkv, nq)
+        assert np.array_equal(O2.read(np.float32, nq * D), out)
     # a second launch reuses the self-reset split counters
     gpu.decode_attn(Q, KC, VC, A, O, ST, D, nkv * D, nq // nkv, nq)
     assert np.array_equal(O.read(np.float32, nq * D), out)
@@ -187,6 +192,58 @@ def test_qkv_rope_attn_fused(gpu, clock, S, k_eq_v):
     others = np.arange(slots) != slot
     assert np.array_equal(got_k[others], kc[others]) and np.array_equal(got_v[others], vc[others])
     assert np.array_equal(Q.read(np.float32, nq * D), qraw)
+
+
+@pytest.mark.parametrize("rot,theta", [(256, 1e4), (64, 1e6)])
+def test_qkv_rope_attn_table_and_dense_list(gpu, rot, theta):
+    # the decode graph's form: RoPE angles from the per-token table and the
+    # list declared 0 .. S-1 (step flags bit 1) give the same bits as angles
+    # computed in the kernel and the list read from memory
+    nq, nkv, D, slots, S, clock = 16, 8, 256, 640, 544, 600
+    kc, vc = make_cache(slots, nkv, D, 12)
+    raw = [gh.synth_normal(n, clock, 91 + i, 0.0, 1.0) for i, n in enumerate((nq * D, nkv * D, nkv * D))]
+    qn = bf16_round(gh.synth_normal(D, 12, 94, 1.0, 0.1))
+    kn = bf16_round(gh.synth_normal(D, 12, 95, 1.0, 0.1))
+    slot = 32 + (clock - 32) % 512
+    Q, K, V, QN, KN, A = (gpu.upload(a) for a in raw + [qn, kn, np.arange(S, dtype=np.uint32)])
+    outs = []
+    for flags, use_tab in ((0, False), (2, True), (2, False), (0, True)):
+        ST = gpu.upload(np.array([clock, slot, S, flags], np.uint32))
+        TAB = gpu.alloc(512 * 4)
+        if use_tab:
+            gpu.rope_table(ST, rot, theta, TAB)
+        KC, VC, O = gpu.upload(kc), gpu.upload(vc), gpu.alloc(nq * D * 4)
+        gpu.qkv_rope_attn(Q, K, V, QN, KN, KC, VC, A, ST, O, nq, nkv, D, rot, False, theta,
+                          table=TAB if use_tab else None)
+        outs.append((O.read(np.float32, nq * D), KC.read(np.float32), VC.read(np.float32)))
+    for o in outs[1:]:
+        for a, b in zip(o, outs[0]):
+            assert np.array_equal(a, b)
+    q2, k2, v2 = orc.qkv_norm_rope(*raw, qn, kn, nq, nkv, D, rot, False, theta, 1e-6, clock)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[slot], vc2[slot] = k2, v2
+    ref = orc.attention(q2, kc2, vc2, np.arange(S, dtype=np.uint32), nq, nkv, D)
+    assert_close(outs[0][0], ref, what="fused attention, table + dense list")
+
+
+def test_rope_table_matches_oracle(gpu):
+    # gh_rope_table's angles rotate like applyRopePartial (kernels.zig:132-150)
+    for rot, theta, clock in ((256, 1e4, 0), (256, 1e4, 639), (64, 1e6, 1000)):
+        ST = gpu.upload(np.array([clock, 0, 1, 0], np.uint32))
+        TAB = gpu.alloc(512 * 4)
+        gpu.rope_table(ST, rot, theta, TAB)
+        tab = TAB.read(np.float32)
+        i = np.arange(rot // 2)
+        ang = clock / np.float64(theta) ** (2.0 * i / rot)
+        assert np.max(np.abs(tab[:rot // 2] - np.cos(ang))) < 2e-4
+        assert np.max(np.abs(tab[256:256 + rot // 2] - np.sin(ang))) < 2e-4
+        v = np.ones(256, np.float32)
+        r = orc.rope_partial(v, clock, 256, rot, theta)
+        h = rot // 2
+        got = np.concatenate([tab[:h] - tab[256:256 + h], tab[256:256 + h] + tab[:h]])
+        # the f32 angle clock * freq: one ulp of powf (device vs the host libm)
+        # moves it by up to ~6e-8 * clock radians, ~6e-5 at clock 1000
+        assert np.max(np.abs(got - r[:rot])) < 1e-4
 
 
 # ---------------------------------------------------------------- argmax ----

@@ -32,4 +32,6 @@ struct AttnArgs {
   // decode, fused: cos[ROPE_TAB_HALF] then sin[ROPE_TAB_HALF] of this
   // token's angles for this layer's (rot, theta) (null: computed in-kernel)
   const float* rope_tab;
+  // layer gating: when non-null and *run == 0 the launch does nothing
+  const uint32_t* run;
 };

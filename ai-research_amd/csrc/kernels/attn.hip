@@ -648,6 +648,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
 template <int DPL, int T>
 __device__ __forceinline__ void attn_decode_k(const AttnArgs& a) {
   __shared__ DecodeSmem sm;
+  if (a.run != nullptr && *a.run == 0u) return;  // a gated-off layer
   if (a.flags != nullptr && (*a.flags & 2u) != 0u)
     attn_decode<DPL, T, true>(a, sm);
   else
@@ -931,6 +932,7 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs 
 // the block-wide max.  The four waves' sums combine in wave order through LDS.
 #define MERGE_U 8
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) {
+  if (a.run != nullptr && *a.run == 0u) return;  // a gated-off layer
   __shared__ float c[MAX_SPLIT];
   __shared__ float red[ATT_WAVES];
   __shared__ float4 acc[ATT_WAVES][MAX_D / 4];

@@ -753,6 +753,7 @@ template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
                                             uint32_t K) {
   extern __shared__ float lds[];
+  if (xp.run != nullptr && *xp.run == 0u) return;  // a gated-off layer
   const uint32_t nb = K >> 5, ng = nb >> 2;
   float* xs = lds;
   float* bsum = lds + ng * GROUP_STRIDE;

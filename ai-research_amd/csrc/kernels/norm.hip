@@ -109,3 +109,73 @@ extern "C" __global__ __launch_bounds__(256) void gh_argmax_k(const float* __res
     partial[2 * blockIdx.x + 1] = bi;
   }
 }
+
+// Layer gate of the decode graph with quiescence on (shaders/
+// quiescence_gate.wgsl:16-62 with the layer input it gates,
+// src/gpu/model_dispatch.zig:45-101).  One workgroup.
+//  1. The layer's input x: with prev_mode 1 (the previous layer ran) or 2
+//     with *prev_run set, the previous layer's post-FFN add,
+//       x = (xmid + RMSNorm(m) * wpost) * s      (m as given without wpost),
+//     written to A; otherwise (no previous layer, or it was gated off) x is
+//     A as it stands.
+//  2. With gate set: mean((x - xprev)^2) over H, xprev <- x, and *run_out =
+//     (mean >= thr || thr <= 0).  Without gate only step 1 runs (the
+//     residual for the LM head after the last layer).
+// H <= 4096 * 4 (four float4 per thread).
+#define QG_U 4
+extern "C" __global__ __launch_bounds__(NORM_NT) void gh_qgate_k(
+    const float* xmid, const float* m, const float* __restrict__ wpost, float s,
+    uint32_t prev_mode, const uint32_t* prev_run, float* A, float* xprev, float thr,
+    uint32_t* run_out, uint32_t H, float eps, uint32_t gate) {
+  __shared__ float red[NORM_NT / 64];
+  const uint32_t n4 = H >> 2;
+  const bool add = prev_mode == 1u || (prev_mode == 2u && *prev_run != 0u);
+  float4 xv[QG_U];
+  if (add) {
+    float4 mv[QG_U];
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < QG_U; u++) {
+      const uint32_t i = u * NORM_NT + threadIdx.x;
+      const uint32_t ic = i < n4 ? i : n4 - 1;
+      xv[u] = reinterpret_cast<const float4*>(xmid)[ic];
+      mv[u] = reinterpret_cast<const float4*>(m)[ic];
+      if (i < n4) ss += mv[u].x * mv[u].x + mv[u].y * mv[u].y + mv[u].z * mv[u].z + mv[u].w * mv[u].w;
+    }
+    const float c = wpost ? 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps) : 1.0f;
+#pragma unroll
+    for (int u = 0; u < QG_U; u++) {
+      const uint32_t i = u * NORM_NT + threadIdx.x;
+      if (i < n4) {
+        float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (wpost) w = reinterpret_cast<const float4*>(wpost)[i];
+        const float4 r = wpost ? make_float4(mv[u].x * c * w.x, mv[u].y * c * w.y,
+                                             mv[u].z * c * w.z, mv[u].w * c * w.w)
+                               : mv[u];
+        xv[u] = make_float4((xv[u].x + r.x) * s, (xv[u].y + r.y) * s, (xv[u].z + r.z) * s,
+                            (xv[u].w + r.w) * s);
+        reinterpret_cast<float4*>(A)[i] = xv[u];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < QG_U; u++) {
+      const uint32_t i = u * NORM_NT + threadIdx.x;
+      xv[u] = reinterpret_cast<const float4*>(A)[i < n4 ? i : n4 - 1];
+    }
+  }
+  if (!gate) return;
+  float d = 0.f;
+#pragma unroll
+  for (int u = 0; u < QG_U; u++) {
+    const uint32_t i = u * NORM_NT + threadIdx.x;
+    if (i < n4) {
+      const float4 p = reinterpret_cast<const float4*>(xprev)[i];
+      const float a = xv[u].x - p.x, b = xv[u].y - p.y, e = xv[u].z - p.z, f = xv[u].w - p.w;
+      d += a * a + b * b + e * e + f * f;
+      reinterpret_cast<float4*>(xprev)[i] = xv[u];
+    }
+  }
+  const float ms = block_sum(d, red) / (float)H;
+  if (threadIdx.x == 0) *run_out = (ms >= thr || thr <= 0.0f) ? 1u : 0u;
+}

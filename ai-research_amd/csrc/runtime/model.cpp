@@ -84,6 +84,10 @@ struct gh_model {
   // GH_EAGER_DECODE=1 (read at init): each token launches its kernels
   // directly instead of replaying the recorded graph (for kernel tracing).
   bool eager = false;
+  // layer gating (quiescence): layers >= num_layers / 3 are gated when on
+  bool q_on = false;
+  float q_thr = 0.f;
+  size_t xprev = 0, gate_flags = 0;  // [L][hidden] f32 previous layer inputs, [L] u32 ran flags
   // batched prefill buffers (gh_model_prefill), sized for pf_cap tokens
   uint32_t pf_cap = 0, pf_stride = 0;
   uint8_t* pf_arena = nullptr;
@@ -109,6 +113,7 @@ struct gh_model {
 
 namespace {
 gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride);
+gh_status reset_gates(gh_model* m);
 gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits);
 }  // namespace
 
@@ -202,6 +207,8 @@ gh_status plan(gh_model* m) {
   m->ring_clock = take((size_t)c.max_slots * 4);
   m->ring_flag = take((size_t)c.max_slots * 4);
   m->rope_tab = take(2 * 2 * 256 * 4);
+  m->xprev = take((size_t)c.num_hidden_layers * H * 4);
+  m->gate_flags = take((size_t)c.num_hidden_layers * 4);
   for (auto& L : m->layers) {
     m->rope_rot[L.full ? 1 : 0] = L.rot;
     m->rope_theta[L.full ? 1 : 0] = L.theta;
@@ -297,7 +304,7 @@ gh_status copy_words(gh_model* m, void* dst, const void* src, uint64_t n) {
 // Records one forward pass (all layers; with the LM head when logits).  The
 // graph holds kernels only: the caller copies the io region in before the
 // replay and the token out after it.
-gh_status record_forward(gh_model* m, bool logits) {
+gh_status record_forward(gh_model* m, bool logits, float thr) {
   gh_context* ctx = m->ctx;
   const gh_model_config& c = m->cfg;
   const uint32_t H = c.hidden_size, I = c.intermediate_size;
@@ -318,13 +325,58 @@ gh_status record_forward(gh_model* m, bool logits) {
   if (m->trace_on && (st = copy_words(m, m->trace, m->at<float>(m->x0), H)) != GH_OK) return st;
 
   size_t xcur = m->x0, xoth = m->x1;
+  // Gated layers (quiescence on, layers >= L / 3; src/gpu/model_dispatch.zig:
+  // 45-101): their input lives in buffer A and their mid-layer residual in B.
+  // gh_qgate_k before each such layer finishes the previous layer's post-FFN
+  // add into A (when that layer ran), gates, and sets the layer's run flag;
+  // every kernel of the layer then returns at once when the flag is 0.
+  const uint32_t dense_limit = m->q_on ? c.num_hidden_layers / 3 : c.num_hidden_layers;
+  const uint32_t* flags = m->at<uint32_t>(m->gate_flags);
+  size_t bufA = 0, bufB = 0;
   for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& L = m->layers[l];
+    const bool gated = l >= dense_limit;
+    const uint32_t* run = gated ? flags + l : nullptr;
+    if (gated) {
+      uint32_t prev_mode;
+      const Layer* P = l > 0 ? &m->layers[l - 1] : nullptr;
+      if (l == dense_limit) {  // the first gated layer
+        if (l == 0) {
+          bufA = m->x0;
+          bufB = m->x1;
+          prev_mode = 0;  // the embedding, as it stands
+        } else {
+          bufB = xcur;  // the previous (ungated) layer's mid-layer residual
+          bufA = xoth;
+          prev_mode = 1;
+        }
+      } else {
+        prev_mode = 2;
+      }
+      float* xmid = m->at<float>(bufB);
+      float* mo = m->at<float>(m->m_out);
+      const float* wpost = P && P->post_ffn != kNone ? m->at<float>(P->post_ffn) : nullptr;
+      float sc = P ? P->scalar : 1.0f;
+      const uint32_t* prun = l > 0 ? flags + l - 1 : nullptr;
+      float* A = m->at<float>(bufA);
+      float* xp = m->at<float>(m->xprev) + (size_t)l * H;
+      uint32_t* ro = const_cast<uint32_t*>(flags) + l;
+      uint32_t Hh = H, one = 1;
+      float eps = c.rms_norm_eps, th = thr;
+      void* args[] = {&xmid, &mo, const_cast<float**>(&wpost), &sc, &prev_mode,
+                      const_cast<uint32_t**>(&prun), &A, &xp, &th, &ro, &Hh, &eps, &one};
+      if ((st = ctx->launch("gh_qgate_k", dim3(1), dim3(1024), 0, args)) != GH_OK) return st;
+      if (m->trace_on && (st = copy_words(m, m->trace + (size_t)l * H, A, H)) != GH_OK) return st;
+    }
     // 1. [q|k|v] = W_qkv . norm(x)  (layer 0: RMSNorm; later: post-FFN add + norm)
     XPro p{};
     p.eps = c.rms_norm_eps;
     p.w = m->at<float>(L.input_norm);
-    if (l == 0) {
+    p.run = run;
+    if (gated) {
+      p.x = m->at<float>(bufA);
+      p.mode = 1;
+    } else if (l == 0) {
       p.x = m->at<float>(xcur);
       p.mode = 1;
     } else {
@@ -339,7 +391,7 @@ gh_status record_forward(gh_model* m, bool logits) {
     }
     Q4Args qa{m->at<uint8_t>(L.qkv), m->at<float>(m->qkv_out)};
     if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H)) != GH_OK) return st;
-    if (m->trace_on && l > 0 &&
+    if (m->trace_on && l > 0 && !gated &&
         (st = copy_words(m, m->trace + (size_t)l * H, m->at<float>(xcur), H)) != GH_OK)
       return st;
     // 2. q/k norm + RoPE + cache write + split-K attention
@@ -369,31 +421,64 @@ gh_status record_forward(gh_model* m, bool logits) {
     a.theta = L.theta;
     a.eps = c.rms_norm_eps;
     a.scale = 1.0f;  // inv_sqrt_dim = 1.0 (src/model/forward.zig:80)
+    a.run = run;
     if ((st = gh::launch_attention(ctx, A)) != GH_OK) return st;
     // 3. o = W_o . attn
     Q4Args oa{m->at<uint8_t>(L.o), m->at<float>(m->o_out)};
-    if ((st = gh::launch_stream(ctx, gemv, &oa, pro_plain(m->at<float>(m->attn_out)), H,
-                                L.q_dim)) != GH_OK)
-      return st;
+    XPro op = pro_plain(m->at<float>(m->attn_out));
+    op.run = run;
+    if ((st = gh::launch_stream(ctx, gemv, &oa, op, H, L.q_dim)) != GH_OK) return st;
     // 4. x += post_attn_norm(o); act = geglu(W_gate, W_up . pre_ffn_norm(x))
     XPro g{};
-    g.x = m->at<float>(xcur);
+    g.x = m->at<float>(gated ? bufA : xcur);
     g.r = m->at<float>(m->o_out);
     g.wr = L.post_attn == kNone ? nullptr : m->at<float>(L.post_attn);
     g.w = m->at<float>(L.pre_ffn);
-    g.xout = m->at<float>(xoth);
+    g.xout = m->at<float>(gated ? bufB : xoth);
     g.s = 1.0f;
     g.eps = c.rms_norm_eps;
     g.mode = 2;
-    std::swap(xcur, xoth);
+    g.run = run;
+    if (!gated) std::swap(xcur, xoth);
     GateUpArgs ga{m->at<uint8_t>(L.gate), m->at<uint8_t>(L.up), m->at<float>(m->act)};
     if ((st = gh::launch_stream(ctx, gateup, &ga, g, I, H)) != GH_OK) return st;
     // 5. m = W_down . act
     Q4Args da{m->at<uint8_t>(L.down), m->at<float>(m->m_out)};
-    if ((st = gh::launch_stream(ctx, gemv, &da, pro_plain(m->at<float>(m->act)), H, I)) != GH_OK)
-      return st;
+    XPro dp = pro_plain(m->at<float>(m->act));
+    dp.run = run;
+    if ((st = gh::launch_stream(ctx, gemv, &da, dp, H, I)) != GH_OK) return st;
   }
-  if (logits) {
+  if (logits && dense_limit < c.num_hidden_layers) {
+    // gated tail: the last layer's post-FFN add (when it ran) into A, then
+    // token = argmax(head . final_norm(A))
+    const Layer& P = m->layers.back();
+    float* xmid = m->at<float>(bufB);
+    float* mo = m->at<float>(m->m_out);
+    const float* wpost = P.post_ffn != kNone ? m->at<float>(P.post_ffn) : nullptr;
+    float sc = P.scalar;
+    uint32_t prev_mode = 2, Hh = H, zero = 0;
+    const uint32_t* prun = flags + c.num_hidden_layers - 1;
+    float* Ab = m->at<float>(bufA);
+    float* xp = m->at<float>(m->xprev);
+    uint32_t* ro = m->at<uint32_t>(m->gate_flags);
+    float eps = c.rms_norm_eps, th = 0.f;
+    void* args[] = {&xmid, &mo, const_cast<float**>(&wpost), &sc, &prev_mode,
+                    const_cast<uint32_t**>(&prun), &Ab, &xp, &th, &ro, &Hh, &eps, &zero};
+    if ((st = ctx->launch("gh_qgate_k", dim3(1), dim3(1024), 0, args)) != GH_OK) return st;
+    XPro p{};
+    p.x = Ab;
+    p.w = m->at<float>(m->final_norm);
+    p.eps = c.rms_norm_eps;
+    p.mode = 1;
+    m->hidden_decode = bufA;
+    ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
+    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
+        GH_OK)
+      return st;
+    if (m->trace_on &&
+        (st = copy_words(m, m->trace + (size_t)c.num_hidden_layers * H, Ab, H)) != GH_OK)
+      return st;
+  } else if (logits) {
     // x = (x + post_ffn_norm(m)) * layer_scalar; token = argmax(head . final_norm(x))
     const Layer& P = m->layers.back();
     XPro p{};
@@ -422,7 +507,7 @@ gh_status record_graphs(gh_model* m) {
   for (int pass = 0; pass < 2; pass++) {
     gh_status st = gh_graph_begin(m->ctx);
     if (st != GH_OK) return st;
-    gh_status rs = record_forward(m, pass == 0);
+    gh_status rs = record_forward(m, pass == 0, pass == 0 ? m->q_thr : 0.0f);
     void* g = nullptr;
     st = gh_graph_end(m->ctx, &g);
     if (rs != GH_OK) {
@@ -438,7 +523,8 @@ gh_status record_graphs(gh_model* m) {
 gh_status finish_init(gh_model* m, gh_model** out) {
   const char* eager = getenv("GH_EAGER_DECODE");
   m->eager = eager && eager[0] == '1';
-  gh_status st = record_graphs(m);
+  gh_status st = reset_gates(m);
+  if (st == GH_OK) st = record_graphs(m);
   if (st != GH_OK) {
     delete m;
     return st;
@@ -450,6 +536,17 @@ gh_status finish_init(gh_model* m, gh_model** out) {
   }
   *out = m;
   return GH_OK;
+}
+
+// Gate state: every layer's ran flag 1, every previous layer input 0 (the
+// reference's freshly created x_prev buffers).
+gh_status reset_gates(gh_model* m) {
+  const gh_model_config& c = m->cfg;
+  gh_status st = gh_buffer_fill_u32(m->ctx, m->arena + m->gate_flags, 1u, c.num_hidden_layers);
+  if (st == GH_OK)
+    st = gh_buffer_fill_u32(m->ctx, m->arena + m->xprev, 0u,
+                            (size_t)c.num_hidden_layers * c.hidden_size);
+  return st;
 }
 
 // Sends the host mirror's layer-0 ring state to the device arrays the ring
@@ -477,7 +574,7 @@ gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_t
   hipStream_t s = m->ctx->stream;
   hipError_t e = hipMemcpyAsync(m->arena + m->io, m->h_io, bytes, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "forward: input copy");
-  gh_status st = m->eager ? record_forward(m, want_logits)
+  gh_status st = m->eager ? record_forward(m, want_logits, want_logits ? m->q_thr : 0.0f)
                           : gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
   if (st != GH_OK) return st;
   if (want_logits) {
@@ -502,8 +599,6 @@ gh_status gh_model_init(gh_context* ctx, const gh_model_config* cfg,
   if (!ctx || !cfg || !layers || !embed_tokens || !out)
     return fail(GH_ERR_INVALID, "gh_model_init: null argument");
   *out = nullptr;
-  if (quiescence_thresh != 0.0f)
-    return fail(GH_ERR_UNSUPPORTED, "gh_model_init: quiescence gating is not part of this backend");
   gh_status st = validate(ctx, *cfg, mode);
   if (st != GH_OK) return st;
   gh_model* m = new gh_model();
@@ -585,6 +680,10 @@ gh_status gh_model_init(gh_context* ctx, const gh_model_config* cfg,
     delete m;
     return st;
   }
+  // GpuModelContext.init records the decode graph with the threshold
+  // (src/gpu/model_gpu.zig:182); 0 records it ungated
+  m->q_on = quiescence_thresh != 0.0f;
+  m->q_thr = quiescence_thresh;
   return finish_init(m, out);
 }
 
@@ -799,6 +898,15 @@ gh_status gh_model_ring_prefill(gh_model* m, const float* x, uint32_t T, uint64_
   gh_ring_destroy(m->ring);
   m->ring = r;
   return ring_upload(m);
+}
+
+gh_status gh_model_set_quiescence(gh_model* m, float threshold) {
+  if (!m) return fail(GH_ERR_INVALID, "gh_model_set_quiescence: null model");
+  m->q_on = threshold != 0.0f;
+  m->q_thr = threshold;
+  gh_status st = reset_gates(m);
+  if (st != GH_OK) return st;
+  return rerecord(m);
 }
 
 gh_status gh_model_set_trace(gh_model* m, int enable) {
@@ -1062,6 +1170,13 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
                           m->at<float>(L.input_norm), P.scalar, 2, m_nz);
     }
     if (st != GH_OK) return st;
+    // with gating on, the per-token prefill graph runs every gate at
+    // threshold 0 (model_gpu.zig:183): each gated layer ends holding the last
+    // token's input as its previous input, and every layer has run
+    if (m->q_on && l >= c.num_hidden_layers / 3 &&
+        (st = copy_words(m, m->at<float>(m->xprev) + (size_t)l * H, m->pf_x + (size_t)(T - 1) * H,
+                         H)) != GH_OK)
+      return st;
     // 2. [q|k|v] rows of every token
     const uint16_t* xh = reinterpret_cast<const uint16_t*>(m->pf_xn);
     if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.qkv), nullptr, xh,
@@ -1145,6 +1260,10 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
                                       last ? nullptr : &m_nz)) != GH_OK)
       return st;
   }
+  if (m->q_on) {  // every layer ran
+    gh_status fs = gh_buffer_fill_u32(ctx, m->arena + m->gate_flags, 1u, c.num_hidden_layers);
+    if (fs != GH_OK) return fs;
+  }
   if (want_logits) {
     // last token: x = (x + post_ffn_norm(m)) * layer_scalar; argmax(head . final_norm(x))
     const Layer& P = m->layers.back();
@@ -1189,6 +1308,10 @@ std::pair<uint8_t*, size_t> tensor_ref(const gh_model* m, int layer, gh_tensor t
       return {m->arena + m->ring_clock, (size_t)c.max_slots * 4};
     case GH_T_RING_FLAGS:
       return {m->arena + m->ring_flag, (size_t)c.max_slots * 4};
+    case GH_T_GATE_FLAGS:
+      return {m->arena + m->gate_flags, (size_t)c.num_hidden_layers * 4};
+    case GH_T_GATE_PREV:
+      return {m->arena + m->xprev, (size_t)c.num_hidden_layers * H * 4};
     default:
       break;
   }

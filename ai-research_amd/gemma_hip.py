@@ -127,6 +127,7 @@ _SIGS.update({
     "gh_model_ring_clear_recall": (_i, [_vp]),
     "gh_model_write_recall_kv": (_i, [_vp, _u32, _u32, _vp, _vp, _u64]),
     "gh_model_set_trace": (_i, [_vp, _i]),
+    "gh_model_set_quiescence": (_i, [_vp, _f32]),
     "gh_model_tensor_bytes": (_sz, [_vp, _i, _i]),
     "gh_model_read_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
     "gh_model_write_tensor": (_i, [_vp, _i, _i, _vp, _sz]),
@@ -137,6 +138,7 @@ _SIGS.update({
  T_PRE_FFN_NORM, T_POST_FFN_NORM, T_K_CACHE, T_V_CACHE) = range(13)
 T_LM_HEAD, T_FINAL_NORM, T_EMBED, T_LOGITS, T_HIDDEN = 20, 21, 22, 23, 24
 T_STEP, T_ACTIVE, T_RING_CLOCKS, T_RING_FLAGS, T_TRACE = 25, 26, 27, 28, 29
+T_GATE_FLAGS, T_GATE_PREV = 30, 31
 
 _lib = None
 
@@ -547,6 +549,9 @@ class Model:
         v = np.ascontiguousarray(v, np.float32)
         _check(lib().gh_model_write_recall_kv(self.h, layer, rank, _ptr(k), _ptr(v), clock),
                "gh_model_write_recall_kv")
+
+    def set_quiescence(self, threshold):
+        _check(lib().gh_model_set_quiescence(self.h, threshold), "gh_model_set_quiescence")
 
     def set_trace(self, enable):
         _check(lib().gh_model_set_trace(self.h, int(enable)), "gh_model_set_trace")

@@ -317,8 +317,9 @@ typedef struct gh_layer_weights {
  * quantizeMatrix's bytes (Q4_0 or Q8_0 per mode; the tied LM head is always
  * Q8_0, model_gpu.zig:160-161), widens norms to f32, allocates the K/V ring
  * caches and records the decode and prefill graphs.  embed_tokens is
- * [vocab][hidden] bf16.  quiescence_thresh must be 0 (layer gating is not
- * part of this backend). */
+ * [vocab][hidden] bf16.  quiescence_thresh != 0 records the decode graph
+ * with layer gating, as gh_model_set_quiescence describes; 0 records it
+ * ungated (the reference's default). */
 gh_status gh_model_init(gh_context *ctx, const gh_model_config *cfg,
                         const gh_layer_weights *layers, const uint16_t *embed_tokens,
                         const uint16_t *final_norm, gh_quant_mode mode,
@@ -400,6 +401,19 @@ gh_status gh_model_ring_clear_recall(gh_model *m);
 gh_status gh_model_write_recall_kv(gh_model *m, uint32_t layer, uint32_t rank, const float *k,
                                    const float *v, uint64_t clock);
 
+/* Layer gating ("quiescence", the threshold GpuModelContext.init takes,
+ * src/gpu/model_gpu.zig:75,182; src/gpu/model_dispatch.zig:45-101,
+ * shaders/quiescence_gate.wgsl:16-62).  With threshold != 0 every layer l >=
+ * num_layers / 3 of the decode graph first compares its input residual x
+ * with the input it saw on the previous call, mean((x - x_prev)^2) over
+ * hidden, stores x as x_prev, and runs only when that mean is >= threshold
+ * (or threshold <= 0); a gated-off layer is skipped whole -- x passes
+ * through, and its K/V row of this token is not written.  The prefill graph
+ * (want_logits 0) and gh_model_prefill run every layer but record x_prev as
+ * the reference's prefill graph does (gates at threshold 0).  threshold 0
+ * turns gating off.  Resets every x_prev to 0 and records the graphs again. */
+gh_status gh_model_set_quiescence(gh_model *m, float threshold);
+
 /* Per-layer residual trace (no reference counterpart; for checking): when
  * enabled, every forward call also copies the residual stream at each
  * layer's input into row l of a [num_layers + 1][hidden] buffer, and with
@@ -432,7 +446,9 @@ typedef enum gh_tensor {
   GH_T_ACTIVE = 26,    /* u32 [max_slots]: the last step's active list (S entries) */
   GH_T_RING_CLOCKS = 27, /* u32 [max_slots]: device ring clock per slot */
   GH_T_RING_FLAGS = 28,  /* u32 [max_slots]: device ring active flag per slot */
-  GH_T_TRACE = 29      /* f32 [hidden]: trace row `layer` (0 .. num_layers) */
+  GH_T_TRACE = 29,     /* f32 [hidden]: trace row `layer` (0 .. num_layers) */
+  GH_T_GATE_FLAGS = 30, /* u32 [num_layers]: 1 where the last step ran the layer */
+  GH_T_GATE_PREV = 31  /* f32 [num_layers][hidden]: each gated layer's previous input */
 } gh_tensor;
 /* Byte size of a tensor (0 when it does not exist). */
 size_t gh_model_tensor_bytes(const gh_model *m, int layer, gh_tensor t);

@@ -514,57 +514,154 @@ static void gum_rows(void *p, size_t r0, size_t r1) {
  *   [m = RMSNorm(m, post_ffn)]; x = (x + m) * layer_scalar
  * tail: logits = Q8 head . RMSNorm(x, final_norm); token = argmax (raw logits).
  * x is updated in place; returns the greedy token when want_logits. */
-uint32_t orc_forward_token(const orc_model *m, float *x, uint64_t clock,
-                           size_t slot_idx, const uint32_t *active, size_t n_active,
-                           int want_logits, float *logits, int nt) {
-  size_t H = m->hidden, I = m->intermediate, nq = m->num_q_heads;
-  size_t maxq = 0, maxkv = 0;
+typedef struct {
+  float *normed, *q, *k, *v, *attn, *o, *act;
+} orc_scratch;
+
+static int scratch_init(const orc_model *m, orc_scratch *s) {
+  size_t H = m->hidden, I = m->intermediate, nq = m->num_q_heads, maxq = 0, maxkv = 0;
   for (size_t l = 0; l < m->num_layers; l++) {
     const orc_layer *L = &m->layers[l];
     if (nq * L->head_dim > maxq) maxq = nq * L->head_dim;
     if (L->num_kv_heads * L->head_dim > maxkv) maxkv = L->num_kv_heads * L->head_dim;
   }
-  float *normed = (float *)malloc(H * sizeof(float));
-  float *q = (float *)malloc(maxq * sizeof(float));
-  float *k = (float *)malloc(maxkv * sizeof(float));
-  float *v = (float *)malloc(maxkv * sizeof(float));
-  float *attn = (float *)malloc(maxq * sizeof(float));
-  float *o = (float *)malloc(H * sizeof(float));
-  float *act = (float *)malloc(I * sizeof(float));
+  if (!maxq) maxq = 1;
+  if (!maxkv) maxkv = 1;
+  s->normed = (float *)malloc(H * sizeof(float));
+  s->q = (float *)malloc(maxq * sizeof(float));
+  s->k = (float *)malloc(maxkv * sizeof(float));
+  s->v = (float *)malloc(maxkv * sizeof(float));
+  s->attn = (float *)malloc(maxq * sizeof(float));
+  s->o = (float *)malloc(H * sizeof(float));
+  s->act = (float *)malloc(I * sizeof(float));
+  return s->normed && s->q && s->k && s->v && s->attn && s->o && s->act;
+}
+
+static void scratch_free(orc_scratch *s) {
+  free(s->normed); free(s->q); free(s->k); free(s->v); free(s->attn); free(s->o); free(s->act);
+}
+
+/* One layer (the op order above), x updated in place. */
+static void forward_layer(const orc_model *m, const orc_layer *L, orc_scratch *s, float *x,
+                          uint64_t clock, size_t slot_idx, const uint32_t *active,
+                          size_t n_active, int nt) {
+  size_t H = m->hidden, I = m->intermediate, nq = m->num_q_heads;
   int q8 = m->layer_mode == ORC_QUANT_Q8;
   size_t wpr_h = orc_quantized_row_words(H, q8 ? ORC_QUANT_Q8 : ORC_QUANT_Q4);
+  size_t hd = L->head_dim, qd = nq * hd, kvd = L->num_kv_heads * hd;
+  float theta = L->full_attention ? m->rope_theta_full : m->rope_theta;
+  orc_rmsnorm(s->normed, x, L->input_norm, H, m->eps);
+  layer_gemv(m, L->wq, s->normed, s->q, qd, H, nt);
+  layer_gemv(m, L->wk, s->normed, s->k, kvd, H, nt);
+  if (!L->k_eq_v) layer_gemv(m, L->wv, s->normed, s->v, kvd, H, nt);
+  orc_qkv_norm_rope(s->q, s->k, s->v, L->q_norm, L->k_norm, nq, L->num_kv_heads, hd,
+                    L->rotary_dim, L->k_eq_v, theta, m->eps, clock);
+  memcpy(L->k_cache + slot_idx * kvd, s->k, kvd * sizeof(float));
+  memcpy(L->v_cache + slot_idx * kvd, s->v, kvd * sizeof(float));
+  orc_attention(s->q, L->k_cache, L->v_cache, kvd, active, n_active, nq, L->num_kv_heads, hd,
+                s->attn);
+  layer_gemv(m, L->wo, s->attn, s->o, H, qd, nt);
+  if (L->post_attn_norm) orc_rmsnorm(s->o, s->o, L->post_attn_norm, H, m->eps);
+  for (size_t i = 0; i < H; i++) x[i] = (x[i] + s->o[i]) * 1.0f;
+  orc_rmsnorm(s->normed, x, L->pre_ffn_norm, H, m->eps);
+  gum_ctx gc = {s->act, s->normed, L->wg, L->wu, H, wpr_h, q8};
+  par_rows(I, nt, gum_rows, &gc);
+  layer_gemv(m, L->wd, s->act, s->o, H, I, nt);
+  if (L->post_ffn_norm) orc_rmsnorm(s->o, s->o, L->post_ffn_norm, H, m->eps);
+  for (size_t i = 0; i < H; i++) x[i] = (x[i] + s->o[i]) * L->layer_scalar;
+}
 
-  for (size_t l = 0; l < m->num_layers; l++) {
-    const orc_layer *L = &m->layers[l];
-    size_t hd = L->head_dim, qd = nq * hd, kvd = L->num_kv_heads * hd;
-    float theta = L->full_attention ? m->rope_theta_full : m->rope_theta;
-    orc_rmsnorm(normed, x, L->input_norm, H, m->eps);
-    layer_gemv(m, L->wq, normed, q, qd, H, nt);
-    layer_gemv(m, L->wk, normed, k, kvd, H, nt);
-    if (!L->k_eq_v) layer_gemv(m, L->wv, normed, v, kvd, H, nt);
-    orc_qkv_norm_rope(q, k, v, L->q_norm, L->k_norm, nq, L->num_kv_heads, hd,
-                      L->rotary_dim, L->k_eq_v, theta, m->eps, clock);
-    memcpy(L->k_cache + slot_idx * kvd, k, kvd * sizeof(float));
-    memcpy(L->v_cache + slot_idx * kvd, v, kvd * sizeof(float));
-    orc_attention(q, L->k_cache, L->v_cache, kvd, active, n_active, nq,
-                  L->num_kv_heads, hd, attn);
-    layer_gemv(m, L->wo, attn, o, H, qd, nt);
-    if (L->post_attn_norm) orc_rmsnorm(o, o, L->post_attn_norm, H, m->eps);
-    for (size_t i = 0; i < H; i++) x[i] = (x[i] + o[i]) * 1.0f;
-    orc_rmsnorm(normed, x, L->pre_ffn_norm, H, m->eps);
-    gum_ctx gc = {act, normed, L->wg, L->wu, H, wpr_h, q8};
-    par_rows(I, nt, gum_rows, &gc);
-    layer_gemv(m, L->wd, act, o, H, I, nt);
-    if (L->post_ffn_norm) orc_rmsnorm(o, o, L->post_ffn_norm, H, m->eps);
-    for (size_t i = 0; i < H; i++) x[i] = (x[i] + o[i]) * L->layer_scalar;
-  }
+static uint32_t forward_tail(const orc_model *m, orc_scratch *s, const float *x, float *logits,
+                             int nt) {
+  orc_rmsnorm(s->normed, x, m->final_norm, m->hidden, m->eps);
+  orc_gemv_q8(m->lm_head_q8, s->normed, logits, m->vocab, m->hidden, nt);
+  return orc_argmax(logits, m->vocab);
+}
 
+uint32_t orc_forward_token(const orc_model *m, float *x, uint64_t clock,
+                           size_t slot_idx, const uint32_t *active, size_t n_active,
+                           int want_logits, float *logits, int nt) {
+  orc_scratch s;
   uint32_t tok = 0;
-  if (want_logits) {
-    orc_rmsnorm(normed, x, m->final_norm, H, m->eps);
-    orc_gemv_q8(m->lm_head_q8, normed, logits, m->vocab, H, nt);
-    tok = orc_argmax(logits, m->vocab);
+  if (scratch_init(m, &s)) {
+    for (size_t l = 0; l < m->num_layers; l++)
+      forward_layer(m, &m->layers[l], &s, x, clock, slot_idx, active, n_active, nt);
+    if (want_logits) tok = forward_tail(m, &s, x, logits, nt);
   }
-  free(normed); free(q); free(k); free(v); free(attn); free(o); free(act);
+  scratch_free(&s);
   return tok;
+}
+
+/* quiescence_gate.wgsl:16-62: the mean over H of (x - x_prev)^2, summed the
+ * way the shader sums it (32 lanes, lane k over elements k, k + 32, ...; then
+ * s[l] += s[l + 16], s[l + 8], s[l + 4], s[l + 2] and s[0] + s[1]), and
+ * x_prev <- x. */
+float orc_gate_mean_sq(const float *x, float *x_prev, size_t H) {
+  float s[32];
+  for (size_t lane = 0; lane < 32; lane++) {
+    float acc = 0.0f;
+    for (size_t i = lane; i < H; i += 32) {
+      float d = x[i] - x_prev[i];
+      acc = acc + d * d;
+    }
+    s[lane] = acc;
+  }
+  for (size_t i = 0; i < H; i++) x_prev[i] = x[i];
+  for (size_t w = 16; w >= 2; w /= 2)
+    for (size_t l = 0; l < w; l++) s[l] = s[l] + s[l + w];
+  return (s[0] + s[1]) / (float)H;
+}
+
+/* The GPU graph with layer gating (src/gpu/model_dispatch.zig:45-101,
+ * 103-129): layers l < L/3 always run; a layer l >= L/3 first runs the gate
+ * (orc_gate_mean_sq against x_prev[l], which it then overwrites) and runs
+ * only when the mean square is >= thresh or thresh <= 0.  A gated-off layer
+ * is skipped whole: no K/V write, x unchanged.  run[l] gets 1 or 0. */
+uint32_t orc_forward_token_gated(const orc_model *m, float *x, uint64_t clock, size_t slot_idx,
+                                 const uint32_t *active, size_t n_active, int want_logits,
+                                 float *logits, int nt, float *x_prev, float thresh,
+                                 uint32_t *run) {
+  orc_scratch s;
+  uint32_t tok = 0;
+  size_t dense_limit = m->num_layers / 3;
+  if (scratch_init(m, &s)) {
+    for (size_t l = 0; l < m->num_layers; l++) {
+      int go = 1;
+      if (l >= dense_limit) {
+        float ms = orc_gate_mean_sq(x, x_prev + l * m->hidden, m->hidden);
+        go = (ms >= thresh) || (thresh <= 0.0f);
+      }
+      if (run) run[l] = (uint32_t)go;
+      if (go) forward_layer(m, &m->layers[l], &s, x, clock, slot_idx, active, n_active, nt);
+    }
+    if (want_logits) tok = forward_tail(m, &s, x, logits, nt);
+  }
+  scratch_free(&s);
+  return tok;
+}
+
+/* QuiescenceTracker.shouldExecute (src/quiescence.zig:29-55), the CPU
+ * path's layer gating: lower layers (l < split_ratio * L) and clocks on the
+ * forced cadence always run; otherwise a layer runs unless the relative
+ * velocity sqrt(sum (x - prev)^2 / sum x^2) (0 when sum x^2 <= 1e-12) is
+ * below the threshold. */
+int orc_qtracker_should_execute(orc_qtracker *t, size_t layer, uint64_t clock, const float *x,
+                                const float *prev_x, size_t n) {
+  if (!t->enabled) return 1;
+  size_t split = (size_t)((float)t->num_layers * t->split_ratio);
+  if (layer < split) return 1;
+  if (clock % t->forced_cadence == 0) return 1;
+  t->total_evals++;
+  float dsum = 0.0f, nsum = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    float d = x[i] - prev_x[i];
+    dsum += d * d;
+    nsum += x[i] * x[i];
+  }
+  float vel = nsum > 1e-12f ? sqrtf(dsum / nsum) : 0.0f;
+  if (vel < t->threshold) {
+    t->skipped_evals++;
+    return 0;
+  }
+  return 1;
 }

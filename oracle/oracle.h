@@ -9,7 +9,7 @@
  * and cites the file:line it follows.  The reference itself is Zig and cannot
  * be built here (no zig toolchain), so there is no oracle/_ref build; the
  * restatement is pinned instead by known answers, invariants and an
- * independent numpy restatement (tests/test_oracle_*.py).
+ * independent numpy restatement (tests/test_oracle.py, tests/numpy_ref.py).
  *
  * Parity status per function (what pins it):
  *   orc_bf16_*                 pinned: tensor.zig:30-41 KAT + RNE tie cases
@@ -26,8 +26,18 @@
  *   orc_ring_*                 pinned: ring_buffer.zig:149-187 KATs + wraparound
  *   orc_attention              pinned: equal scores -> mean(V), S=1 -> V,
  *                              dominant score -> that V, fp64 brute force
- *   orc_forward_token          pinned by composition of the above plus an
- *                              fp64 numpy restatement of the layer op order
+ *   orc_forward_token          pinned: an independent fp64 numpy forward
+ *                              (tests/numpy_ref.forward64) within 1e-5, with
+ *                              planted mistakes in it shown to miss by >1e-3
+ *   orc_embed                  pinned: bit-exact vs a numpy restatement
+ *   orc_gate_up_geglu_q4 /     pinned: fp64 brute force; gate/up swap caught
+ *   orc_gated_mlp_q4
+ *   orc_gate_mean_sq           pinned: fp64 closed form; x_prev update
+ *   orc_forward_token_gated    pinned: with every gate open it equals
+ *                              orc_forward_token; gated-off layers are the
+ *                              identity and write no K/V (checked against
+ *                              orc_forward_token on the remaining layers)
+ *   orc_qtracker_*             pinned: src/quiescence.zig:63-77 KAT
  */
 #ifndef ORACLE_H
 #define ORACLE_H
@@ -131,6 +141,24 @@ void orc_embed(const uint16_t *embed_bf16, uint32_t token, size_t hidden, float 
 uint32_t orc_forward_token(const orc_model *m, float *x, uint64_t clock,
                            size_t slot_idx, const uint32_t *active, size_t n_active,
                            int want_logits, float *logits, int nthreads);
+
+/* ---- layer gating ------------------------------------------------------- */
+/* quiescence_gate.wgsl: mean (x - x_prev)^2 in the shader's order; x_prev <- x */
+float orc_gate_mean_sq(const float *x, float *x_prev, size_t H);
+/* model_dispatch.zig:45-101: layers >= L/3 gated against x_prev [L][H] */
+uint32_t orc_forward_token_gated(const orc_model *m, float *x, uint64_t clock,
+                                 size_t slot_idx, const uint32_t *active, size_t n_active,
+                                 int want_logits, float *logits, int nthreads,
+                                 float *x_prev, float thresh, uint32_t *run);
+/* QuiescenceTracker (src/quiescence.zig:3-61), the CPU path's gating */
+typedef struct orc_qtracker {
+  int enabled;
+  float split_ratio, threshold;
+  size_t forced_cadence, num_layers;
+  uint64_t total_evals, skipped_evals;
+} orc_qtracker;
+int orc_qtracker_should_execute(orc_qtracker *t, size_t layer, uint64_t clock, const float *x,
+                                const float *prev_x, size_t n);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,13 @@ def lib():
         L.orc_forward_token.restype = C.c_uint32
         L.orc_forward_token.argtypes = [C.c_void_p, _f32p, C.c_uint64, _sz, _u32p, _sz,
                                         C.c_int, _f32p, C.c_int]
+        L.orc_gate_mean_sq.restype = C.c_float
+        L.orc_gate_mean_sq.argtypes = [_f32p, _f32p, _sz]
+        L.orc_forward_token_gated.restype = C.c_uint32
+        L.orc_forward_token_gated.argtypes = [C.c_void_p, _f32p, C.c_uint64, _sz, _u32p, _sz,
+                                              C.c_int, _f32p, C.c_int, _f32p, C.c_float, _u32p]
+        L.orc_qtracker_should_execute.restype = C.c_int
+        L.orc_qtracker_should_execute.argtypes = [C.c_void_p, _sz, C.c_uint64, _f32p, _f32p, _sz]
         _lib = L
     return _lib
 
@@ -240,6 +247,42 @@ def embed(embed_bf16, token, hidden):
     return x
 
 
+# ---- layer gating ------------------------------------------------------------
+def gate_mean_sq(x, x_prev):
+    """quiescence_gate.wgsl's mean (x - x_prev)^2; x_prev (float32) <- x in place."""
+    x = _c(x, np.float32)
+    assert x_prev.dtype == np.float32 and x_prev.flags.c_contiguous
+    return lib().orc_gate_mean_sq(_p(x, C.c_float), _p(x_prev, C.c_float), x.size)
+
+
+class _QTracker(C.Structure):
+    _fields_ = [("enabled", C.c_int), ("split_ratio", C.c_float), ("threshold", C.c_float),
+                ("forced_cadence", _sz), ("num_layers", _sz), ("total_evals", C.c_uint64),
+                ("skipped_evals", C.c_uint64)]
+
+
+class QTracker:
+    """QuiescenceTracker (src/quiescence.zig:3-61), defaults of QuiescenceConfig."""
+
+    def __init__(self, num_layers, enabled=True, split_ratio=0.5, threshold=0.02,
+                 forced_cadence=4):
+        self._t = _QTracker(int(enabled), split_ratio, threshold, forced_cadence, num_layers, 0, 0)
+
+    def should_execute(self, layer, clock, x, prev_x):
+        x = _c(x, np.float32)
+        p = _c(prev_x, np.float32)
+        return bool(lib().orc_qtracker_should_execute(C.byref(self._t), layer, clock,
+                                                      _p(x, C.c_float), _p(p, C.c_float), x.size))
+
+    @property
+    def total_evals(self):
+        return self._t.total_evals
+
+    @property
+    def skipped_evals(self):
+        return self._t.skipped_evals
+
+
 # ---- ring buffer (src/ring_buffer.zig), a thin Python mirror over C -------
 class _Ring(C.Structure):
     _fields_ = [("num_layers", _sz), ("max_kv_dim", _sz), ("num_anchors", _sz),
@@ -384,3 +427,19 @@ class Model:
                                       _p(act, C.c_uint32), act.size, int(want_logits),
                                       _p(logits, C.c_float), nthreads)
         return int(tok), x, (logits if want_logits else None)
+
+    def forward_gated(self, x, clock, slot_idx, active, x_prev, thresh, want_logits=True,
+                      nthreads=1):
+        """The gated GPU graph (model_dispatch.zig:45-101); x_prev [L][H]
+        float32 is updated in place.  Returns (token, x_out, logits, run)."""
+        x = np.array(x, np.float32, copy=True)
+        act = _c(active, np.uint32)
+        assert x_prev.dtype == np.float32 and x_prev.flags.c_contiguous
+        logits = np.empty(self.vocab if want_logits else 1, np.float32)
+        run = np.zeros(self._m.num_layers, np.uint32)
+        tok = lib().orc_forward_token_gated(C.byref(self._m), _p(x, C.c_float), clock, slot_idx,
+                                            _p(act, C.c_uint32), act.size, int(want_logits),
+                                            _p(logits, C.c_float), nthreads,
+                                            _p(x_prev, C.c_float), thresh,
+                                            _p(run, C.c_uint32))
+        return int(tok), x, (logits if want_logits else None), run

@@ -403,3 +403,78 @@ def test_forward_restatement_catches_planted_mistakes(mistake):
     _, _, logits = om.forward(x, 7, 7, active, True, 1)
     _, _, blog = nr.forward64(bad, x, 7, 7, active, head, fnorm, nq, mistake=mistake)
     assert np.max(np.abs(logits - blog)) / np.max(np.abs(blog)) > 1e-3
+
+
+# ------------------------------------------------------------- layer gating ----
+def test_gate_mean_sq_closed_form_and_update():
+    rng = np.random.default_rng(31)
+    H = 3840
+    x = rng.standard_normal(H).astype(np.float32)
+    prev = rng.standard_normal(H).astype(np.float32)
+    want = np.mean((x.astype(np.float64) - prev) ** 2)
+    p = prev.copy()
+    got = orc.gate_mean_sq(x, p)
+    assert abs(got - want) < 1e-5 * want
+    assert np.array_equal(p, x)  # X_prev <- X_curr (quiescence_gate.wgsl:28)
+    assert orc.gate_mean_sq(x, p) == 0.0  # the same input again: no motion
+
+
+def test_qtracker_reference_kat():
+    # src/quiescence.zig:63-77
+    t = orc.QTracker(10, split_ratio=0.5, threshold=0.5)
+    x = np.ones(2, np.float32)
+    for layer in range(5):  # lower layers always execute
+        assert t.should_execute(layer, 1, x, x)
+    assert not t.should_execute(5, 1, x, x)  # zero delta, off cadence: skip
+    assert t.should_execute(5, 4, x, x)  # forced cadence
+    assert t.total_evals == 1 and t.skipped_evals == 1
+    # relative velocity sqrt(sum d^2 / sum x^2) against the threshold
+    t2 = orc.QTracker(4, split_ratio=0.5, threshold=0.1)
+    x = np.array([1.0, 0.0], np.float32)
+    assert t2.should_execute(3, 1, x, np.array([0.85, 0.0], np.float32))      # 0.15
+    assert not t2.should_execute(3, 1, x, np.array([0.95, 0.0], np.float32))  # 0.05
+    assert t2.should_execute(0, 1, x, x)  # 0 < split 2
+    assert not orc.QTracker(4, threshold=0.1).should_execute(3, 1, np.zeros(2, np.float32),
+                                                             np.zeros(2, np.float32))  # velocity 0
+
+
+def test_forward_gated_matches_ungated_and_skips_whole_layers():
+    H, I, V, nq, layers, head, fnorm, rng = _tiny_forward_model("q4")
+    L = len(layers)  # 3 layers: layer 0 always runs (3 // 3 = 1), layers 1, 2 gated
+    active = np.array([0, 2, 5, 7, 9, 11], np.uint32)
+    x = rng.standard_normal(H).astype(np.float32) * 3
+    # every gate open (thresh <= 0): the ungated forward, bit for bit
+    a, b = _copy_layers(layers), _copy_layers(layers)
+    om_a = orc.Model(H, I, V, nq, a, head, fnorm)
+    om_b = orc.Model(H, I, V, nq, b, head, fnorm)
+    xp = np.zeros((L, H), np.float32)
+    ta, xa, la, run = om_a.forward_gated(x, 7, 7, active, xp, 0.0)
+    tb, xb, lb = om_b.forward(x, 7, 7, active)
+    assert list(run) == [1, 1, 1] and ta == tb
+    assert np.array_equal(la, lb) and np.array_equal(xa, xb)
+    # x_prev of a gated layer holds that layer's input: layer 1's is layer 0's output
+    _, x1, _ = orc.Model(H, I, V, nq, _copy_layers(layers)[:1], head, fnorm).forward(
+        x, 7, 7, active, False)
+    assert np.array_equal(xp[1], x1) and not np.any(xp[0])
+    # the same input again with a threshold: layer 1 sees zero motion and is
+    # skipped whole (its cache keeps the slot's old row); that changes layer
+    # 2's input, whose gate then opens -- the result is layers 0 and 2 alone
+    c = _copy_layers(layers)
+    om_c = orc.Model(H, I, V, nq, c, head, fnorm)
+    xp2 = xp.copy()
+    k_before = [d["k_cache"][7].copy() for d in c]
+    tc, xc, lc, run = om_c.forward_gated(x, 7, 7, active, xp2, 1e-3)
+    assert list(run) == [1, 0, 1]
+    d02 = [d for i, d in enumerate(_copy_layers(layers)) if i != 1]
+    td, xd, ld = orc.Model(H, I, V, nq, d02, head, fnorm).forward(x, 7, 7, active)
+    assert np.array_equal(lc, ld) and np.array_equal(xc, xd) and tc == td
+    assert np.array_equal(c[1]["k_cache"][7], k_before[1])
+    assert not np.array_equal(c[0]["k_cache"][7], k_before[0])
+    assert not np.array_equal(c[2]["k_cache"][7], k_before[2])
+    assert np.array_equal(xp2[1], xp[1])  # a skipped layer still records its input
+    # a threshold above every motion skips all gated layers
+    e = _copy_layers(layers)
+    xp3 = xp.copy()
+    xp3[1:] += 1.0
+    _, _, _, run = orc.Model(H, I, V, nq, e, head, fnorm).forward_gated(x, 7, 7, active, xp3, 1e9)
+    assert list(run) == [1, 0, 0]

@@ -11,9 +11,6 @@ struct XPro {
   float* xout;
   float s, eps;
   uint32_t mode;
-  // layer gating: when non-null and *run == 0 the launch does nothing (the
-  // layer is skipped); null in ungated graphs
-  const uint32_t* run;
 };
 
 struct Q4Args {  // Q4Fmt::Args / Q8Fmt::Args

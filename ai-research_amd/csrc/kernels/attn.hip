@@ -648,7 +648,6 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
 template <int DPL, int T>
 __device__ __forceinline__ void attn_decode_k(const AttnArgs& a) {
   __shared__ DecodeSmem sm;
-  if (a.run != nullptr && *a.run == 0u) return;  // a gated-off layer
   if (a.flags != nullptr && (*a.flags & 2u) != 0u)
     attn_decode<DPL, T, true>(a, sm);
   else
@@ -659,6 +658,13 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { 
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d2_k(AttnArgs a) { attn_decode_k<2, 8>(a); }
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d4_k(AttnArgs a) { attn_decode_k<4, 8>(a); }
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { attn_decode_k<8, 4>(a); }
+// gated layers (quiescence on): nothing when the layer's run flag is 0
+#define GH_ATTN_GATED(DPL, T)                                                                   \
+  extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d##DPL##_q_k(AttnArgs a) {       \
+    if (*a.run == 0u) return;                                                                   \
+    attn_decode_k<DPL, T>(a);                                                                   \
+  }
+GH_ATTN_GATED(1, 8) GH_ATTN_GATED(2, 8) GH_ATTN_GATED(4, 8) GH_ATTN_GATED(8, 4)
 
 // Batched prefill: grid (kv heads, tokens); each workgroup runs token
 // blockIdx.y's whole active list (q already normalised and roped by
@@ -931,8 +937,7 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs 
 // indices, so the kernel costs one L2 round trip; only the weights wait for
 // the block-wide max.  The four waves' sums combine in wave order through LDS.
 #define MERGE_U 8
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) {
-  if (a.run != nullptr && *a.run == 0u) return;  // a gated-off layer
+__device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   __shared__ float c[MAX_SPLIT];
   __shared__ float red[ATT_WAVES];
   __shared__ float4 acc[ATT_WAVES][MAX_D / 4];
@@ -999,6 +1004,12 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a)
     r.w = ((a0.w + a1.w) + (a2.w + a3.w)) * inv;
     *reinterpret_cast<float4*>(a.out + (size_t)h * D + col * 4) = r;
   }
+}
+
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) { attn_merge(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_q_k(AttnArgs a) {
+  if (*a.run == 0u) return;  // a gated-off layer
+  attn_merge(a);
 }
 
 // ---------------------------------------------------------------------------

@@ -753,7 +753,6 @@ template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
                                             uint32_t K) {
   extern __shared__ float lds[];
-  if (xp.run != nullptr && *xp.run == 0u) return;  // a gated-off layer
   const uint32_t nb = K >> 5, ng = nb >> 2;
   float* xs = lds;
   float* bsum = lds + ng * GROUP_STRIDE;
@@ -892,13 +891,26 @@ __device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro
 // pointers are separate kernel parameters: loaded out of a by-value struct
 // parameter they lose the kernel-argument address-space and alignment facts,
 // and the stream then needs ~100 more VGPRs (220 vs 126 for the Q4 d3 form).
-#define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)      \
-  extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX(   \
-      GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                             \
-    stream_rows<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);        \
+// Gated forms (suffix _q): the decode graph's gated layers (quiescence on)
+// launch these; they take the layer's run flag and do nothing when it is 0.
+// The ungated kernels carry no gating code at all: even a null-pointer test
+// at entry measured +0.3 us per launch.
+#define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)        \
+  extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX(     \
+      GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                               \
+    stream_rows<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);          \
+  }
+#define GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)      \
+  GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)              \
+  extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX##_q( \
+      GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K, const uint32_t* run) {          \
+    if (*run == 0u) return;                                                               \
+    stream_rows<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);          \
   }
 #define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED) \
   GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, 256, )
+#define GH_STREAM_KERNEL_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED) \
+  GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, 256, )
 #define GH_UNPAREN(...) __VA_ARGS__
 
 #define GH_P_W (const uint8_t* W, float* Y)
@@ -908,19 +920,23 @@ __device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro
 #define GH_P_AM (const uint8_t* W, float* Y, uint32_t* partial)
 #define GH_A_AM (W, Y, partial)
 
-#define GH_PLAIN(T, G, D)                                                        \
-  GH_STREAM_KERNEL(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false)            \
-  GH_STREAM_KERNEL(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false)            \
-  GH_STREAM_KERNEL(gh_gateup_q4, GateUpFmt, GH_P_GU, GH_A_GU, T, G, D, false)    \
-  GH_STREAM_KERNEL(gh_gateup_q8, GateUpQ8Fmt, GH_P_GU, GH_A_GU, T, G, D, false)  \
+// Depth 1 (the default) has gated forms too; depth 2 is for tuning only.
+#define GH_PLAIN_K(T, G, D, K)                                                   \
+  K(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false)                           \
+  K(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false)                           \
+  K(gh_gateup_q4, GateUpFmt, GH_P_GU, GH_A_GU, T, G, D, false)                   \
+  K(gh_gateup_q8, GateUpQ8Fmt, GH_P_GU, GH_A_GU, T, G, D, false)                 \
   GH_STREAM_KERNEL(gh_argmax_q8, Q8ArgmaxFmt, GH_P_AM, GH_A_AM, T, G, D, false)
-
-#define GH_NORMED(T, G, D)                                                       \
-  GH_STREAM_KERNEL(gh_gemv_q4n, Q4Fmt, GH_P_W, GH_A_W, T, G, D, true)            \
-  GH_STREAM_KERNEL(gh_gemv_q8n, Q8Fmt, GH_P_W, GH_A_W, T, G, D, true)            \
-  GH_STREAM_KERNEL(gh_gateup_q4n, GateUpFmt, GH_P_GU, GH_A_GU, T, G, D, true)    \
-  GH_STREAM_KERNEL(gh_gateup_q8n, GateUpQ8Fmt, GH_P_GU, GH_A_GU, T, G, D, true)  \
+#define GH_NORMED_K(T, G, D, K)                                                  \
+  K(gh_gemv_q4n, Q4Fmt, GH_P_W, GH_A_W, T, G, D, true)                           \
+  K(gh_gemv_q8n, Q8Fmt, GH_P_W, GH_A_W, T, G, D, true)                           \
+  K(gh_gateup_q4n, GateUpFmt, GH_P_GU, GH_A_GU, T, G, D, true)                   \
+  K(gh_gateup_q8n, GateUpQ8Fmt, GH_P_GU, GH_A_GU, T, G, D, true)                 \
   GH_STREAM_KERNEL(gh_argmax_q8n, Q8ArgmaxFmt, GH_P_AM, GH_A_AM, T, G, D, true)
+#define GH_PLAIN(T, G, D) GH_PLAIN_K(T, G, D, GH_STREAM_KERNEL)
+#define GH_PLAIN_Q(T, G, D) GH_PLAIN_K(T, G, D, GH_STREAM_KERNEL_Q)
+#define GH_NORMED(T, G, D) GH_NORMED_K(T, G, D, GH_STREAM_KERNEL)
+#define GH_NORMED_Q(T, G, D) GH_NORMED_K(T, G, D, GH_STREAM_KERNEL_Q)
 
 #define GH_SHAPES(X, D) X(16, 1, D) X(32, 1, D) X(64, 1, D) X(32, 2, D) X(64, 2, D) X(32, 4, D) X(64, 4, D)
 
@@ -928,15 +944,15 @@ __device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro
 // of LDS for K = 15360) serves 16 wavefronts instead of 4.  (At K ~ 4096
 // they measured slower than 256-thread workgroups, so only these exist.)
 #define GH_WIDE(T, G, D)                                                                   \
-  GH_STREAM_KERNEL_NT(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)         \
-  GH_STREAM_KERNEL_NT(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)
+  GH_STREAM_KERNEL_NT_Q(gh_gemv_q4, Q4Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)       \
+  GH_STREAM_KERNEL_NT_Q(gh_gemv_q8, Q8Fmt, GH_P_W, GH_A_W, T, G, D, false, 1024, _w)
 
 // Depth 1 is the default everywhere; depth 2 stays for tuning (GH_GEMV_CFG).
 #if defined(GH_GEMV_NORMED)
-GH_SHAPES(GH_NORMED, 1)
+GH_SHAPES(GH_NORMED_Q, 1)
 GH_SHAPES(GH_NORMED, 2)
 #else
-GH_SHAPES(GH_PLAIN, 1)
+GH_SHAPES(GH_PLAIN_Q, 1)
 GH_SHAPES(GH_PLAIN, 2)
 GH_WIDE(32, 4, 1) GH_WIDE(64, 2, 1) GH_WIDE(64, 4, 1)  // depth 2 at 1024 threads spills
 

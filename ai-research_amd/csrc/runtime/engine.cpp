@@ -118,7 +118,7 @@ gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_
 }
 
 gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> fmt_params,
-                        const XPro& xp, uint32_t M, uint32_t K) {
+                        const XPro& xp, uint32_t M, uint32_t K, const uint32_t* run) {
   if (xp.mode != 0 && K > 4u * 4u * 256u)  // PRO_U float4 per thread of 256
     return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": normed prologue needs K <= 4096");
   StreamShape sh;
@@ -127,6 +127,10 @@ gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> 
   XPro xpc = xp;
   std::vector<void*> args = std::move(fmt_params);
   args.insert(args.end(), {&xpc, &M, &K});
+  if (run) {  // the gated form takes the run flag as its last parameter
+    args.push_back(&run);
+    sh.name += "_q";
+  }
   return ctx->launch(sh.name, dim3(sh.grid), dim3(sh.nt), sh.lds, args.data());
 }
 
@@ -305,12 +309,13 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
   if (D > 512 || D % 4 != 0 || D % dpl != 0)
     return fail(GH_ERR_UNSUPPORTED, "attention: head_dim must be a multiple of 4 up to 512");
   void* args[] = {const_cast<AttnArgs*>(&L.args)};
-  const char* name = dpl == 1 ? "gh_attn_d1_k"
-                     : dpl == 2 ? "gh_attn_d2_k"
-                     : dpl == 4 ? "gh_attn_d4_k" : "gh_attn_d8_k";
+  // a.run non-null: the gated forms (nothing when the layer's flag is 0)
+  const bool gated = L.args.run != nullptr;
+  const std::string name = std::string("gh_attn_d") + std::to_string(dpl) + (gated ? "_q_k" : "_k");
   gh_status st = ctx->launch(name, dim3(L.args.nkv * L.args.nsplit), dim3(256), 0, args);
   if (st != GH_OK) return st;
-  return ctx->launch("gh_attn_merge_k", dim3(L.args.nq), dim3(256), 0, args);
+  return ctx->launch(gated ? "gh_attn_merge_q_k" : "gh_attn_merge_k", dim3(L.args.nq), dim3(256),
+                     0, args);
 }
 
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,

@@ -372,7 +372,6 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     XPro p{};
     p.eps = c.rms_norm_eps;
     p.w = m->at<float>(L.input_norm);
-    p.run = run;
     if (gated) {
       p.x = m->at<float>(bufA);
       p.mode = 1;
@@ -390,7 +389,7 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
       std::swap(xcur, xoth);
     }
     Q4Args qa{m->at<uint8_t>(L.qkv), m->at<float>(m->qkv_out)};
-    if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H)) != GH_OK) return st;
+    if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H, run)) != GH_OK) return st;
     if (m->trace_on && l > 0 && !gated &&
         (st = copy_words(m, m->trace + (size_t)l * H, m->at<float>(xcur), H)) != GH_OK)
       return st;
@@ -425,9 +424,9 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     if ((st = gh::launch_attention(ctx, A)) != GH_OK) return st;
     // 3. o = W_o . attn
     Q4Args oa{m->at<uint8_t>(L.o), m->at<float>(m->o_out)};
-    XPro op = pro_plain(m->at<float>(m->attn_out));
-    op.run = run;
-    if ((st = gh::launch_stream(ctx, gemv, &oa, op, H, L.q_dim)) != GH_OK) return st;
+    if ((st = gh::launch_stream(ctx, gemv, &oa, pro_plain(m->at<float>(m->attn_out)), H,
+                                L.q_dim, run)) != GH_OK)
+      return st;
     // 4. x += post_attn_norm(o); act = geglu(W_gate, W_up . pre_ffn_norm(x))
     XPro g{};
     g.x = m->at<float>(gated ? bufA : xcur);
@@ -438,15 +437,14 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     g.s = 1.0f;
     g.eps = c.rms_norm_eps;
     g.mode = 2;
-    g.run = run;
     if (!gated) std::swap(xcur, xoth);
     GateUpArgs ga{m->at<uint8_t>(L.gate), m->at<uint8_t>(L.up), m->at<float>(m->act)};
-    if ((st = gh::launch_stream(ctx, gateup, &ga, g, I, H)) != GH_OK) return st;
+    if ((st = gh::launch_stream(ctx, gateup, &ga, g, I, H, run)) != GH_OK) return st;
     // 5. m = W_down . act
     Q4Args da{m->at<uint8_t>(L.down), m->at<float>(m->m_out)};
-    XPro dp = pro_plain(m->at<float>(m->act));
-    dp.run = run;
-    if ((st = gh::launch_stream(ctx, gemv, &da, dp, H, I)) != GH_OK) return st;
+    if ((st = gh::launch_stream(ctx, gemv, &da, pro_plain(m->at<float>(m->act)), H, I, run)) !=
+        GH_OK)
+      return st;
   }
   if (logits && dense_limit < c.num_hidden_layers) {
     // gated tail: the last layer's post-FFN add (when it ran) into A, then

@@ -54,15 +54,18 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L);
 // Row-stream GEMV launch (gemv.hip); family = gh_gemv_q4, gh_gemv_q8,
 // gh_gateup_q4, gh_gateup_q8 or gh_argmax_q8.  The kernels take the
 // argument block's members as separate parameters, in member order.
+// run non-null: the gated form (a layer of the gated decode graph), which
+// does nothing when *run == 0.
 gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> fmt_params,
-                        const XPro& xp, uint32_t M, uint32_t K);
+                        const XPro& xp, uint32_t M, uint32_t K, const uint32_t* run = nullptr);
 inline gh_status launch_stream(gh_context* ctx, const char* family, Q4Args* a, const XPro& xp,
-                               uint32_t M, uint32_t K) {
-  return launch_stream(ctx, family, {&a->W, &a->Y}, xp, M, K);
+                               uint32_t M, uint32_t K, const uint32_t* run = nullptr) {
+  return launch_stream(ctx, family, {&a->W, &a->Y}, xp, M, K, run);
 }
 inline gh_status launch_stream(gh_context* ctx, const char* family, GateUpArgs* a,
-                               const XPro& xp, uint32_t M, uint32_t K) {
-  return launch_stream(ctx, family, {&a->Wg, &a->Wu, &a->Y}, xp, M, K);
+                               const XPro& xp, uint32_t M, uint32_t K,
+                               const uint32_t* run = nullptr) {
+  return launch_stream(ctx, family, {&a->Wg, &a->Wu, &a->Y}, xp, M, K, run);
 }
 // The fused Q8 LM-head stream (family gh_argmax_q8) followed by the
 // reduction of its block partials to the token.

@@ -363,6 +363,26 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
         slot = ring.activate_slot(0, c)
         tok = m.forward(emb(tok), c, slot, ring.active_slots(0, c), True)
     host_s = time.perf_counter() - t0
+    # layer gating at the reference CLI's default threshold (--quiescence:
+    # 0.001, src/main.zig:56): 32 more steps timed, then 8 whose run flags
+    # are read back for the skip fraction
+    m.set_quiescence(0.001)
+    n_q = 32
+    c0 = n_prompt + n_decode + n_host
+    t0 = time.perf_counter()
+    for i in range(n_q):
+        tok = m.forward_clock(emb(tok), c0 + i, True)
+    q_s = time.perf_counter() - t0
+    gated, skipped = 0, 0
+    for i in range(8):
+        tok = m.forward_clock(emb(tok), c0 + n_q + i, True)
+        flags = m.read(-1, gh.T_GATE_FLAGS, np.uint32)[48 // 3:]
+        gated += flags.size
+        skipped += int((flags == 0).sum())
+    m.set_quiescence(0.0)
+    for i in range(n_q + 8):
+        ring.activate_slot(0, c0 + i)
+    n_host += n_q + 8
     cpu_dec = None
     if cpu:
         cpu_dec = cpu_decode_baseline(m, cfg, n_prompt + n_decode + n_host,
@@ -380,7 +400,9 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
             "decode_roofline_frac": round(ideal_s / decode_s, 4),
             "decode_path": "device ring (gh_model_forward_clock): x and the clock go up, the "
                            "token comes back, one host round trip per token",
-            "decode_tok_s_host_lists": round(n_host / host_s, 2),
+            "decode_tok_s_host_lists": round(32 / host_s, 2),
+            "decode_tok_s_quiescence_0.001": round(n_q / q_s, 2),
+            "quiescence_skip_fraction": round(skipped / max(1, gated), 4),
             "prefill_tok_s": round(n_prompt / prefill_s, 1),
             "prefill_ms": round(prefill_s * 1e3, 2),
             "prefill_path": "batched (MFMA Q4 dequant GEMM), one call; median of 3 after 2 warm-up calls",

@@ -735,6 +735,158 @@ struct Q8ArgmaxFmt {
 };
 
 // ------------------------------------------------------------------------
+// bf16 weights (the reference's --gpu mode, mode none: src/gpu/kernels.zig:36
+// selects shaders/gemv_bf16.wgsl).  Rows are the plain row-major bf16 of the
+// checkpoint, K / 8 chunks of 16 bytes.  The stream is interleaved: item j of
+// lane l of a row team holds chunks (8 j + k) TPR + l, k = 0..7, so each of
+// the 8 loads of a wavefront reads TPR consecutive chunks (whole cache lines;
+// 256 contiguous bytes per lane instead measured 8.1 vs 5.4 us for 19.7 MB).
+// A chunk's 8 weights widen exactly to fp32 (low half first) and meet x in
+// fp32, as the shader's bf16_to_f32(p & 0xFFFF) * X[2i] + ... does.
+// ------------------------------------------------------------------------
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// x of chunk c (8 floats) in the group-padded LDS staging
+__device__ __forceinline__ const float* x_of_chunk(const float* xs, uint32_t c) {
+  return xs + (c >> 4) * GROUP_STRIDE + ((c & 15u) << 3);
+}
+
+__device__ __forceinline__ float bf16_chunk_dot(const u32x4& w, const float* xc) {
+  const float4 xa = *reinterpret_cast<const float4*>(xc);
+  const float4 xb = *reinterpret_cast<const float4*>(xc + 4);
+  float s = bf_lo(w.x) * xa.x + bf_hi(w.x) * xa.y;
+  s += bf_lo(w.y) * xa.z + bf_hi(w.y) * xa.w;
+  s += bf_lo(w.z) * xb.x + bf_hi(w.z) * xb.y;
+  s += bf_lo(w.w) * xb.z + bf_hi(w.w) * xb.w;
+  return s;
+}
+
+constexpr uint32_t kBfChunks = 8;  // 16-byte chunks per lane per item (64 weights)
+
+template <int TPR>
+__device__ __forceinline__ void load_bf_item(u32x4 (&w)[kBfChunks], const uint8_t* row,
+                                             uint32_t c0, uint32_t nch) {
+#pragma unroll
+  for (uint32_t k = 0; k < kBfChunks; k++) {
+    uint32_t c = c0 + k * TPR;
+    c = c < nch ? c : nch - 1;  // past the row: an in-range duplicate, weighted 0
+    w[k] = ldw(row + (size_t)c * 16);
+  }
+}
+
+// Sum of an item's chunk dots into acc (chunks past the row add 0).
+template <int TPR>
+__device__ __forceinline__ void bf_item_dot(float& acc, const u32x4 (&w)[kBfChunks],
+                                            const float* xs, uint32_t c0, uint32_t nch) {
+#pragma unroll
+  for (uint32_t k = 0; k < kBfChunks; k++) {
+    const uint32_t ch = c0 + k * TPR;
+    const float d = bf16_chunk_dot(w[k], x_of_chunk(xs, ch < nch ? ch : nch - 1));
+    acc += ch < nch ? d : 0.0f;
+  }
+}
+
+struct Bf16Fmt {  // shaders/gemv_bf16.wgsl
+  static constexpr uint32_t kChunks = kBfChunks, kBlockBytes = 64;  // 32 weights = 64 B
+  struct Item {
+    u32x4 w[kBfChunks];
+  };
+  using Acc = Q4Fmt::Acc;
+  using Args = Q4Fmt::Args;
+  template <int TPR>
+  __device__ static void load(Item& it, const Args& a, size_t row_off, uint32_t c0, uint32_t nch) {
+    load_bf_item<TPR>(it.w, a.W + row_off, c0, nch);
+  }
+  __device__ static void init(Acc& c) { c.s = 0.f; }
+  __device__ static void zero(Acc& c) { c.s = 0.f; }
+  template <int TPR>
+  __device__ static void fma(Acc& c, const Item& it, const float* xs, uint32_t c0, uint32_t nch) {
+    bf_item_dot<TPR>(c.s, it.w, xs, c0, nch);
+  }
+  template <int TPR>
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
+    Q4Fmt::finish<TPR>(c, a, row, writer);
+  }
+  template <int NT>
+  __device__ static void block_end(const Acc&, const Args&, float*) {}
+};
+
+// bf16 gate and up rows of the same (row, item) travel together, so every x
+// value read from LDS feeds both.  (In the reference's mode none the fused
+// MLP pipeline is the Q4 shader, src/gpu/kernels.zig:41, which reads bf16
+// rows as Q4 blocks; this computes what the CPU path computes,
+// src/kernels.zig:100-129: act = gelu_tanh(Wg x) * (Wu x).)
+struct GateUpBf16Fmt {
+  static constexpr uint32_t kChunks = kBfChunks, kBlockBytes = 64;
+  struct Item {
+    u32x4 g[kBfChunks], u[kBfChunks];
+  };
+  using Acc = GateUpFmt::Acc;
+  using Args = GateUpFmt::Args;
+  template <int TPR>
+  __device__ static void load(Item& it, const Args& a, size_t row_off, uint32_t c0, uint32_t nch) {
+    load_bf_item<TPR>(it.g, a.Wg + row_off, c0, nch);
+    load_bf_item<TPR>(it.u, a.Wu + row_off, c0, nch);
+  }
+  __device__ static void init(Acc& c) { c.g = c.u = 0.f; }
+  __device__ static void zero(Acc& c) { c.g = c.u = 0.f; }
+  template <int TPR>
+  __device__ static void fma(Acc& c, const Item& it, const float* xs, uint32_t c0, uint32_t nch) {
+#pragma unroll
+    for (uint32_t k = 0; k < kBfChunks; k++) {
+      const uint32_t ch = c0 + k * TPR;
+      const float* xc = x_of_chunk(xs, ch < nch ? ch : nch - 1);
+      const float dg = bf16_chunk_dot(it.g[k], xc);
+      const float du = bf16_chunk_dot(it.u[k], xc);
+      c.g += ch < nch ? dg : 0.0f;
+      c.u += ch < nch ? du : 0.0f;
+    }
+  }
+  template <int TPR>
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
+    GateUpFmt::finish<TPR>(c, a, row, writer);
+  }
+  template <int NT>
+  __device__ static void block_end(const Acc&, const Args&, float*) {}
+};
+
+// bf16 vocab projection with the argmax fused in: the head of mode none is
+// the bf16 embedding itself (src/gpu/model_gpu.zig:160-161; the logits
+// pipeline is the bf16 GEMV, src/gpu/kernels.zig:38).
+struct Bf16ArgmaxFmt {
+  static constexpr uint32_t kChunks = kBfChunks, kBlockBytes = 64;
+  using Item = Bf16Fmt::Item;
+  using Acc = Q8ArgmaxFmt::Acc;
+  using Args = Q8ArgmaxFmt::Args;
+  template <int TPR>
+  __device__ static void load(Item& it, const Args& a, size_t row_off, uint32_t c0, uint32_t nch) {
+    load_bf_item<TPR>(it.w, a.W + row_off, c0, nch);
+  }
+  __device__ static void init(Acc& c) { Q8ArgmaxFmt::init(c); }
+  __device__ static void zero(Acc& c) { c.s = 0.f; }
+  template <int TPR>
+  __device__ static void fma(Acc& c, const Item& it, const float* xs, uint32_t c0, uint32_t nch) {
+    bf_item_dot<TPR>(c.s, it.w, xs, c0, nch);
+  }
+  template <int TPR>
+  __device__ static void finish(Acc& c, const Args& a, uint32_t row, bool writer) {
+    Q8ArgmaxFmt::finish<TPR>(c, a, row, writer);
+  }
+  template <int NT>
+  __device__ static void block_end(const Acc& c, const Args& a, float* red) {
+    Q8ArgmaxFmt::block_end<NT>(c, a, red);
+  }
+};
+
+// Formats with kChunks stream interleaved (stream_rows_il), the others by
+// 4-block groups (stream_rows).
+template <class F>
+constexpr auto interleaved(int) -> decltype(F::kChunks, bool()) { return true; }
+template <class F>
+constexpr bool interleaved(long) { return false; }
+
+// ------------------------------------------------------------------------
 // Persistent row-team streaming.  Team t (TPR lanes) owns rows t, t + T,
 // t + 2T, ... (T = teams in the grid); lane l of a team owns groups
 // l, l + TPR, ..., l + (GPL-1) TPR of each of its rows.  A lane walks its
@@ -749,6 +901,42 @@ struct Q8ArgmaxFmt {
 // item.  Teams with no rows skip the stream but still take part in the
 // block-wide prologue and epilogue.
 // ------------------------------------------------------------------------
+// The prologue of a stream and its first weight loads (issue()).
+template <int NT, bool NORMED, class Issue>
+__device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* xs, float* bsum,
+                                             float* ext, Issue issue) {
+  // A wave's loads complete in order, so x loads issued behind its own
+  // weight loads would wait for them (barriers do not wait for outstanding
+  // loads).  Every thread therefore issues its prologue loads (x, and for
+  // the normed streams r and the norm weights) first, then its weight loads,
+  // then runs the prologue (whose reductions need every thread).
+  if constexpr (NORMED) {
+    ProIn pin;
+    pro_load<NT>(xp, K, pin);
+    issue();
+    pro_finish<NT>(xp, K, pin, xs, bsum, ext);
+  } else if (K <= PRO_U * 4 * NT) {
+    // x first: every thread issues its slices of x, then its first weight
+    // loads, then stages x (the x loads return first; measured 14.8 vs
+    // 15.2 us against splitting the workgroup into stagers and streamers)
+    ProIn pin;
+    XPro x_only = xp;
+    x_only.mode = 0;
+    pro_load<NT>(x_only, K, pin);
+    issue();
+    pro_finish<NT>(x_only, K, pin, xs, bsum, ext);
+  } else {
+    // longer x than the registers hold: the first NS threads stage x while
+    // the others' first weight loads are in flight, then issue their own
+    constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
+    const bool late = threadIdx.x < NS;
+    if (!late) issue();
+    if (late) stage_x<NS>(xp.x, K, xs, bsum);
+    __syncthreads();
+    if (late) issue();
+  }
+}
+
 template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
                                             uint32_t K) {
@@ -776,49 +964,12 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
     return (size_t)row * row_bytes + (size_t)g * F::kGroupBytes;
   };
 
-  // A wave's loads complete in order, so x loads issued behind its own
-  // weight loads would wait for them (barriers do not wait for outstanding
-  // loads).  Every thread therefore issues its prologue loads (x, and for
-  // the normed streams r and the norm weights) first, then its weight loads,
-  // then runs the prologue (whose reductions need every thread).
   typename F::Item buf[D];
-  if constexpr (NORMED) {
-    ProIn pin;
-    pro_load<NT>(xp, K, pin);
+  stream_start<NT, NORMED>(xp, K, xs, bsum, ext, [&]() {
 #pragma unroll
     for (int d = 0; d < D; d++)
       if (d < n_items) F::load(buf[d], a, offset_of(d));
-    pro_finish<NT>(xp, K, pin, xs, bsum, ext);
-  } else if (K <= PRO_U * 4 * NT) {
-    // x first: every thread issues its slices of x, then its first weight
-    // loads, then stages x (the x loads return first; measured 14.8 vs
-    // 15.2 us against splitting the workgroup into stagers and streamers)
-    ProIn pin;
-    XPro x_only = xp;
-    x_only.mode = 0;
-    pro_load<NT>(x_only, K, pin);
-#pragma unroll
-    for (int d = 0; d < D; d++)
-      if (d < n_items) F::load(buf[d], a, offset_of(d));
-    pro_finish<NT>(x_only, K, pin, xs, bsum, ext);
-  } else {
-    // longer x than the registers hold: the first NS threads stage x while
-    // the others' first weight loads are in flight, then issue their own
-    constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
-    const bool late = threadIdx.x < NS;
-    if (!late) {
-#pragma unroll
-      for (int d = 0; d < D; d++)
-        if (d < n_items) F::load(buf[d], a, offset_of(d));
-    }
-    if (late) stage_x<NS>(xp.x, K, xs, bsum);
-    __syncthreads();
-    if (late) {
-#pragma unroll
-      for (int d = 0; d < D; d++)
-        if (d < n_items) F::load(buf[d], a, offset_of(d));
-    }
-  }
+  });
   typename F::Acc acc;
   F::init(acc);
 #pragma unroll 1
@@ -839,6 +990,64 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
     }
   }
   F::template block_end<NT>(acc, a, ext);
+}
+
+// ------------------------------------------------------------------------
+// Interleaved row-team streaming (bf16 rows): as stream_rows, but item j of
+// lane l covers the row's 16-byte chunks (kChunks j + k) TPR + l, so the
+// team reads whole cache lines per load instruction.  GPL items per row per
+// lane, TPR GPL kChunks >= K / 8.
+// ------------------------------------------------------------------------
+template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
+__device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const XPro& xp,
+                                               uint32_t M, uint32_t K) {
+  extern __shared__ float lds[];
+  const uint32_t nb = K >> 5, ng = nb >> 2, nch = K >> 3;
+  float* xs = lds;
+  float* bsum = lds + ng * GROUP_STRIDE;
+  float* ext = bsum + nb;
+  constexpr uint32_t TEAMS = NT / TPR, C = F::kChunks;
+  const uint32_t lr = threadIdx.x % TPR;
+  const uint32_t team = blockIdx.x * TEAMS + threadIdx.x / TPR;
+  const uint32_t nteams = gridDim.x * TEAMS;
+  const uint32_t n_items = team < M ? ((M - 1 - team) / nteams + 1) * GPL : 0;
+  const size_t row_bytes = (size_t)K * 2;
+  auto row_of = [&](uint32_t i) -> uint32_t { return team + (i / GPL) * nteams; };
+  auto c0_of = [&](uint32_t i) -> uint32_t { return (i % GPL) * C * TPR + lr; };
+  typename F::Item buf[D];
+  stream_start<NT, NORMED>(xp, K, xs, bsum, ext, [&]() {
+#pragma unroll
+    for (int d = 0; d < D; d++)
+      if (d < n_items) F::template load<TPR>(buf[d], a, row_of(d) * row_bytes, c0_of(d), nch);
+  });
+  typename F::Acc acc;
+  F::init(acc);
+#pragma unroll 1
+  for (uint32_t base = 0; base < n_items; base += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      const uint32_t i = base + d;
+      if (i < n_items) {  // uniform within a team
+        F::template fma<TPR>(acc, buf[d], xs, c0_of(i), nch);
+        if (i % GPL == GPL - 1) {
+          F::template finish<TPR>(acc, a, row_of(i), lr == 0);
+          F::zero(acc);
+        }
+      }
+      if (i + D < n_items)
+        F::template load<TPR>(buf[d], a, row_of(i + D) * row_bytes, c0_of(i + D), nch);
+    }
+  }
+  F::template block_end<NT>(acc, a, ext);
+}
+
+template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
+__device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp, uint32_t M,
+                                       uint32_t K) {
+  if constexpr (interleaved<F>(0))
+    stream_rows_il<F, TPR, GPL, D, NT, NORMED>(a, xp, M, K);
+  else
+    stream_rows<F, TPR, GPL, D, NT, NORMED>(a, xp, M, K);
 }
 
 // ------------------------------------------------------------------------
@@ -898,14 +1107,14 @@ __device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro
 #define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)        \
   extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX(     \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                               \
-    stream_rows<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);          \
+    stream<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
   }
 #define GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)      \
   GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)              \
   extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX##_q( \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K, const uint32_t* run) {          \
     if (*run == 0u) return;                                                               \
-    stream_rows<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);          \
+    stream<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
   }
 #define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED) \
   GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, 256, )
@@ -940,6 +1149,16 @@ __device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro
 
 #define GH_SHAPES(X, D) X(16, 1, D) X(32, 1, D) X(64, 1, D) X(32, 2, D) X(64, 2, D) X(32, 4, D) X(64, 4, D)
 
+// bf16 rows (64 weights per lane item): the shapes the default pick can
+// choose (one item per lane per row first, ties to the wider team).
+#define GH_BF16_K(T, G, D, NORMED, SFX)                                                     \
+  GH_STREAM_KERNEL_Q(gh_gemv_bf16##SFX, Bf16Fmt, GH_P_W, GH_A_W, T, G, D, NORMED)           \
+  GH_STREAM_KERNEL_Q(gh_gateup_bf16##SFX, GateUpBf16Fmt, GH_P_GU, GH_A_GU, T, G, D, NORMED) \
+  GH_STREAM_KERNEL(gh_argmax_bf16##SFX, Bf16ArgmaxFmt, GH_P_AM, GH_A_AM, T, G, D, NORMED)
+#define GH_BF16_PLAIN(T, G, D) GH_BF16_K(T, G, D, false, )
+#define GH_BF16_NORMED(T, G, D) GH_BF16_K(T, G, D, true, n)
+#define GH_BF16_SHAPES(X) X(16, 1, 1) X(32, 1, 1) X(64, 1, 1) X(64, 2, 1) X(64, 4, 1)
+
 // Wide workgroups (1024 threads) for long rows: one x staging (up to 64 KB
 // of LDS for K = 15360) serves 16 wavefronts instead of 4.  (At K ~ 4096
 // they measured slower than 256-thread workgroups, so only these exist.)
@@ -951,9 +1170,11 @@ __device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro
 #if defined(GH_GEMV_NORMED)
 GH_SHAPES(GH_NORMED_Q, 1)
 GH_SHAPES(GH_NORMED, 2)
+GH_BF16_SHAPES(GH_BF16_NORMED)
 #else
 GH_SHAPES(GH_PLAIN_Q, 1)
 GH_SHAPES(GH_PLAIN, 2)
+GH_BF16_SHAPES(GH_BF16_PLAIN)
 GH_WIDE(32, 4, 1) GH_WIDE(64, 2, 1) GH_WIDE(64, 4, 1)  // depth 2 at 1024 threads spills
 
 // The token from the n block partials of a fused argmax stream: the largest

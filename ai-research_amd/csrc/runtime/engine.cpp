@@ -25,8 +25,9 @@ unsigned x_lds_bytes(uint32_t K);
 // Lanes per row team (TPR) and 4-block groups per lane per row (GPL) with
 // TPR * GPL >= the row's group count and the least idle lanes; then a
 // persistent grid of wgs_per_cu workgroups per CU (bounded by LDS).
-GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool wide_ok) {
-  const uint32_t ng = K / 128;
+GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool wide_ok,
+                  bool bf16) {
+  const uint32_t ng = K / (bf16 ? 64 : 128);  // lane items per row: 64 bf16 or 128 quantized
   static const int kT[] = {16, 32, 64};
   int best_t = 64, best_g = 4;
   uint32_t best_waste = ~0u;
@@ -49,6 +50,7 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool w
   // Long rows (the down projection, K = 15360): 1024-thread workgroups, so
   // one LDS staging of x serves 16 wavefronts; measured 11.6 vs 13.6 us.
   if (wide_ok && K >= 8192 && best_t * best_g >= 128) c = {best_t, best_g, 2, 1, 1024};
+  if (bf16) c.depth = 1;  // the bf16 streams exist at depth 1 only
   // tuning "tpr,gpl,wgs_per_cu,depth[,nt]": GH_GEMV_CFG_<M>x<K> for one shape,
   // else GH_GEMV_CFG for every shape it fits
   const std::string shape_key = "GH_GEMV_CFG_" + std::to_string(M) + "x" + std::to_string(K);
@@ -56,7 +58,8 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool w
   if (const char* env = shape_env ? shape_env : getenv("GH_GEMV_CFG")) {
     int t = 0, g = 0, w = 0, d = 0, n = 256;
     const int got = sscanf(env, "%d,%d,%d,%d,%d", &t, &g, &w, &d, &n);
-    if (got >= 4 && (t == 16 || t == 32 || t == 64) && (g == 1 || g == 2 || g == 4) &&
+    const bool built = !bf16 || ((t == 64 || g == 1) && d == 1 && n == 256);
+    if (got >= 4 && built && (t == 16 || t == 32 || t == 64) && (g == 1 || g == 2 || g == 4) &&
         !(t == 16 && g > 1) && w >= 1 && w <= 32 && (uint32_t)(t * g) >= ng && d >= 1 &&
         d <= 2 && (n == 256 || (n == 1024 && wide_ok && t * g >= 128 && d == 1))) {
       c = {t, g, w, d, n};
@@ -92,7 +95,12 @@ gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_
                        StreamShape* out) {
   // 1024-thread variants exist for the plain GEMVs (long rows)
   const bool wide_ok = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0);
-  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, wide_ok);
+  const bool bf16 = strstr(family, "bf16") != nullptr;
+  GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, wide_ok, bf16);
+  // a row team covers at most 64 lanes x 4 items (of 128 quantized or 64 bf16 weights)
+  if ((uint64_t)c.tpr * c.gpl * (bf16 ? 64u : 128u) < K)
+    return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": rows longer than " +
+                                        std::to_string(bf16 ? 16384 : 32768) + " weights");
   out->lds = x_lds_bytes(K) + 256;  // + the prologue/epilogue scratch (64 floats)
   if (out->lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
   out->name = std::string(family) + (normed ? "n" : "") + "_t" + std::to_string(c.tpr) + "_g" +
@@ -134,13 +142,21 @@ gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> 
   return ctx->launch(sh.name, dim3(sh.grid), dim3(sh.nt), sh.lds, args.data());
 }
 
+const char* gemv_family(gh_quant_mode mode) {
+  return mode == GH_QUANT_Q4 ? "gh_gemv_q4" : mode == GH_QUANT_Q8 ? "gh_gemv_q8" : "gh_gemv_bf16";
+}
+const char* gateup_family(gh_quant_mode mode) {
+  return mode == GH_QUANT_Q4 ? "gh_gateup_q4" : mode == GH_QUANT_Q8 ? "gh_gateup_q8" : "gh_gateup_bf16";
+}
+
 gh_status launch_argmax_stream(gh_context* ctx, ArgmaxArgs* a, const XPro& xp, uint32_t M,
-                               uint32_t K, uint32_t* token) {
+                               uint32_t K, uint32_t* token, bool bf16) {
+  const char* family = bf16 ? "gh_argmax_bf16" : "gh_argmax_q8";
   StreamShape sh;
-  gh_status st = stream_shape(ctx, "gh_argmax_q8", xp.mode != 0, M, K, &sh);
+  gh_status st = stream_shape(ctx, family, xp.mode != 0, M, K, &sh);
   if (st != GH_OK) return st;
   if (sh.grid > kArgmaxMaxBlocks) return fail(GH_ERR_UNSUPPORTED, "argmax stream: grid too large");
-  if ((st = launch_stream(ctx, "gh_argmax_q8", {&a->W, &a->Y, &a->partial}, xp, M, K)) != GH_OK)
+  if ((st = launch_stream(ctx, family, {&a->W, &a->Y, &a->partial}, xp, M, K)) != GH_OK)
     return st;
   uint32_t n = sh.grid;
   void* args[] = {&a->partial, &n, &token};
@@ -205,6 +221,14 @@ gh_status gh_gemv_q8(gh_context* ctx, const void* W, const float* X, float* Y, u
   return launch_stream(ctx, "gh_gemv_q8", &a, plain_x(X), M, K);
 }
 
+gh_status gh_gemv_bf16(gh_context* ctx, const void* W, const float* X, float* Y, uint32_t M,
+                       uint32_t K) {
+  gh_status st = check_gemv(ctx, W, X, Y, M, K, "gh_gemv_bf16");
+  if (st != GH_OK) return st;
+  Q4Args a{static_cast<const uint8_t*>(W), Y};
+  return launch_stream(ctx, "gh_gemv_bf16", &a, plain_x(X), M, K);
+}
+
 gh_status gh_gate_up_geglu_q4(gh_context* ctx, const void* Wg, const void* Wu, const float* X,
                               float* Y, uint32_t M, uint32_t K) {
   gh_status st = check_gemv(ctx, Wg, X, Y, M, K, "gh_gate_up_geglu_q4");
@@ -218,22 +242,22 @@ gh_status gh_gate_up_geglu_q4(gh_context* ctx, const void* Wg, const void* Wu, c
 gh_status gh_norm_gemv(gh_context* ctx, gh_quant_mode mode, const void* W, float* Y, uint32_t M,
                        uint32_t K, const gh_xprologue* pro) {
   if (!pro) return fail(GH_ERR_INVALID, "gh_norm_gemv: prologue is null");
-  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
-    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gemv: mode must be Q4 or Q8");
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8 && mode != GH_QUANT_NONE)
+    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gemv: mode must be Q4, Q8 or NONE (bf16)");
   gh_status st = check_gemv(ctx, W, pro->x, Y, M, K, "gh_norm_gemv");
   if (st != GH_OK) return st;
   XPro p = from_abi(pro);
   if ((st = gh::check_pro(ctx, p, K, "gh_norm_gemv")) != GH_OK) return st;
   Q4Args a{static_cast<const uint8_t*>(W), Y};
-  return launch_stream(ctx, mode == GH_QUANT_Q4 ? "gh_gemv_q4" : "gh_gemv_q8", &a, p, M, K);
+  return launch_stream(ctx, gh::gemv_family(mode), &a, p, M, K);
 }
 
 gh_status gh_norm_gate_up_geglu(gh_context* ctx, gh_quant_mode mode, const void* Wg,
                                 const void* Wu, float* Y, uint32_t M, uint32_t K,
                                 const gh_xprologue* pro) {
   if (!pro) return fail(GH_ERR_INVALID, "gh_norm_gate_up_geglu: prologue is null");
-  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
-    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gate_up_geglu: mode must be Q4 or Q8");
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8 && mode != GH_QUANT_NONE)
+    return fail(GH_ERR_UNSUPPORTED, "gh_norm_gate_up_geglu: mode must be Q4, Q8 or NONE (bf16)");
   gh_status st = check_gemv(ctx, Wg, pro->x, Y, M, K, "gh_norm_gate_up_geglu");
   if (st != GH_OK) return st;
   if (!Wu || (reinterpret_cast<uintptr_t>(Wu) & 15))
@@ -241,22 +265,36 @@ gh_status gh_norm_gate_up_geglu(gh_context* ctx, gh_quant_mode mode, const void*
   XPro p = from_abi(pro);
   if ((st = gh::check_pro(ctx, p, K, "gh_norm_gate_up_geglu")) != GH_OK) return st;
   GateUpArgs a{static_cast<const uint8_t*>(Wg), static_cast<const uint8_t*>(Wu), Y};
-  return launch_stream(ctx, mode == GH_QUANT_Q4 ? "gh_gateup_q4" : "gh_gateup_q8", &a, p, M, K);
+  return launch_stream(ctx, gh::gateup_family(mode), &a, p, M, K);
 }
 
-gh_status gh_norm_gemv_argmax_q8(gh_context* ctx, const void* W, float* logits,
-                                 uint32_t* token, uint32_t M, uint32_t K,
-                                 const gh_xprologue* pro) {
-  if (!pro || !token) return fail(GH_ERR_INVALID, "gh_norm_gemv_argmax_q8: null argument");
-  gh_status st = check_gemv(ctx, W, pro->x, token, M, K, "gh_norm_gemv_argmax_q8");
+namespace {
+gh_status norm_gemv_argmax(gh_context* ctx, const void* W, float* logits, uint32_t* token,
+                           uint32_t M, uint32_t K, const gh_xprologue* pro, bool bf16,
+                           const char* who) {
+  if (!pro || !token) return fail(GH_ERR_INVALID, std::string(who) + ": null argument");
+  gh_status st = check_gemv(ctx, W, pro->x, token, M, K, who);
   if (st != GH_OK) return st;
   XPro p = from_abi(pro);
-  if ((st = gh::check_pro(ctx, p, K, "gh_norm_gemv_argmax_q8")) != GH_OK) return st;
+  if ((st = gh::check_pro(ctx, p, K, who)) != GH_OK) return st;
   st = ctx->ensure_zeroed(&ctx->argmax_scratch, &ctx->argmax_scratch_bytes, kArgmaxScratchBytes);
   if (st != GH_OK) return st;
   uint32_t* base = static_cast<uint32_t*>(ctx->argmax_scratch);
   ArgmaxArgs a{static_cast<const uint8_t*>(W), logits, base + 64};
-  return gh::launch_argmax_stream(ctx, &a, p, M, K, token);
+  return gh::launch_argmax_stream(ctx, &a, p, M, K, token, bf16);
+}
+}  // namespace
+
+gh_status gh_norm_gemv_argmax_q8(gh_context* ctx, const void* W, float* logits,
+                                 uint32_t* token, uint32_t M, uint32_t K,
+                                 const gh_xprologue* pro) {
+  return norm_gemv_argmax(ctx, W, logits, token, M, K, pro, false, "gh_norm_gemv_argmax_q8");
+}
+
+gh_status gh_norm_gemv_argmax_bf16(gh_context* ctx, const void* W, float* logits,
+                                   uint32_t* token, uint32_t M, uint32_t K,
+                                   const gh_xprologue* pro) {
+  return norm_gemv_argmax(ctx, W, logits, token, M, K, pro, true, "gh_norm_gemv_argmax_bf16");
 }
 
 gh_status gh_rmsnorm(gh_context* ctx, const float* X, const float* W, float* Y, uint32_t dim,

@@ -106,7 +106,11 @@ struct gh_model {
     return reinterpret_cast<T*>(arena + off);
   }
   size_t row_bytes(uint32_t cols) const {
-    return (size_t)(cols / 32) * (mode == GH_QUANT_Q8 ? 36 : 20);
+    return (size_t)(cols / 32) * (mode == GH_QUANT_Q8 ? 36 : mode == GH_QUANT_Q4 ? 20 : 64);
+  }
+  // the tied head: bf16 rows in mode none, else Q8_0 (src/gpu/model_gpu.zig:160-161)
+  size_t head_bytes() const {
+    return (size_t)cfg.vocab_size * (cfg.hidden_size / 32) * (mode == GH_QUANT_NONE ? 64 : 36);
   }
   ~gh_model();
 };
@@ -133,8 +137,8 @@ gh_model::~gh_model() {
 namespace {
 
 gh_status validate(const gh_context* ctx, const gh_model_config& c, gh_quant_mode mode) {
-  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
-    return fail(GH_ERR_UNSUPPORTED, "model: mode must be Q4 or Q8 (the bf16 path is not built)");
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8 && mode != GH_QUANT_NONE)
+    return fail(GH_ERR_UNSUPPORTED, "model: mode must be Q4, Q8 or NONE (bf16)");
   if (c.num_hidden_layers == 0 || c.num_hidden_layers > 64)
     return fail(GH_ERR_INVALID, "model: num_hidden_layers must be 1..64");
   if (c.hidden_size == 0 || c.hidden_size % 128 || c.intermediate_size == 0 ||
@@ -196,7 +200,7 @@ gh_status plan(gh_model* m) {
     m->max_kv = std::max(m->max_kv, L.kv_dim);
     m->layers.push_back(L);
   }
-  m->lm_head = take((size_t)V * (H / 32) * 36);
+  m->lm_head = take(m->head_bytes());
   m->final_norm = take(H * 4);
   m->io_bytes = align_up((size_t)H * 4, 256) + 64 + (size_t)c.max_slots * 4;
   m->io = take(m->io_bytes);
@@ -262,9 +266,11 @@ gh_status alloc_all(gh_model* m) {
 
 // Quantize [rows][cols] bf16 into dst, with the bf16 rows provided chunk by
 // chunk by fill(staging, row0, nrows) (an upload or the device generator).
+// Mode none keeps the bf16 rows: fill writes them in place.
 template <typename Fill>
 gh_status quantize_rows(gh_model* m, uint8_t* dst, uint32_t rows, uint32_t cols, gh_quant_mode q,
                         uint16_t* staging, size_t staging_elems, Fill fill) {
+  if (q == GH_QUANT_NONE) return fill(reinterpret_cast<uint16_t*>(dst), 0, rows);
   const uint32_t chunk = (uint32_t)std::max<size_t>(1, staging_elems / cols);
   const size_t rb = (size_t)(cols / 32) * (q == GH_QUANT_Q8 ? 36 : 20);
   for (uint32_t r0 = 0; r0 < rows; r0 += chunk) {
@@ -308,8 +314,9 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
   gh_context* ctx = m->ctx;
   const gh_model_config& c = m->cfg;
   const uint32_t H = c.hidden_size, I = c.intermediate_size;
-  const char* gemv = m->mode == GH_QUANT_Q8 ? "gh_gemv_q8" : "gh_gemv_q4";
-  const char* gateup = m->mode == GH_QUANT_Q8 ? "gh_gateup_q8" : "gh_gateup_q4";
+  const char* gemv = gh::gemv_family(m->mode);
+  const char* gateup = gh::gateup_family(m->mode);
+  const bool head_bf16 = m->mode == GH_QUANT_NONE;
   gh_status st;
   {  // device ring: slot_idx, S and the active list from the clock (step mode 1)
     uint32_t* rc = m->at<uint32_t>(m->ring_clock);
@@ -470,8 +477,8 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     p.mode = 1;
     m->hidden_decode = bufA;
     ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
-    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
-        GH_OK)
+    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token),
+                                       head_bf16)) != GH_OK)
       return st;
     if (m->trace_on &&
         (st = copy_words(m, m->trace + (size_t)c.num_hidden_layers * H, Ab, H)) != GH_OK)
@@ -490,8 +497,8 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     p.mode = 2;
     m->hidden_decode = xoth;
     ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
-    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
-        GH_OK)
+    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token),
+                                       head_bf16)) != GH_OK)
       return st;
     if (m->trace_on &&
         (st = copy_words(m, m->trace + (size_t)c.num_hidden_layers * H, m->at<float>(xoth), H)) !=
@@ -567,13 +574,18 @@ gh_status rerecord(gh_model* m) {
 }
 
 // One token: the first `bytes` of the io region go up, the graph replays, and
-// with logits the token comes back.
-gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_token) {
+// with logits the token comes back.  open_gates: a prompt token with logits
+// while gating is on runs with every gate open (threshold 0), as the batched
+// prefill does; no graph holds that combination, so its kernels launch
+// directly.
+gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_token,
+                    bool open_gates = false) {
   hipStream_t s = m->ctx->stream;
   hipError_t e = hipMemcpyAsync(m->arena + m->io, m->h_io, bytes, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "forward: input copy");
-  gh_status st = m->eager ? record_forward(m, want_logits, want_logits ? m->q_thr : 0.0f)
-                          : gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
+  const bool direct = m->eager || (open_gates && want_logits && m->q_on);
+  gh_status st = direct ? record_forward(m, want_logits, want_logits && !open_gates ? m->q_thr : 0.0f)
+                        : gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
   if (st != GH_OK) return st;
   if (want_logits) {
     e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost, s);
@@ -669,8 +681,9 @@ gh_status gh_model_init(gh_context* ctx, const gh_model_config* cfg,
     }
   }
   if (st == GH_OK)
-    st = quantize_rows(m, m->at<uint8_t>(m->lm_head), cfg->vocab_size, H, GH_QUANT_Q8, staging,
-                       staging_elems, upload_from(embed_tokens, H));
+    st = quantize_rows(m, m->at<uint8_t>(m->lm_head), cfg->vocab_size, H,
+                       mode == GH_QUANT_NONE ? GH_QUANT_NONE : GH_QUANT_Q8, staging, staging_elems,
+                       upload_from(embed_tokens, H));
   if (st == GH_OK) st = upload_norm(m, m->final_norm, final_norm, H);
   hipStreamSynchronize(ctx->stream);
   hipFree(staging);
@@ -754,7 +767,11 @@ gh_status gh_model_init_synthetic(gh_context* ctx, const gh_model_config* cfg, g
   // tied embedding / LM head: stream 999
   if (st == GH_OK) st = gh_synth_normal_bf16_dev(ctx, m->embed_dev, (size_t)V * H, seed, 999, 0.0,
                                                   0.02, 0);
-  if (st == GH_OK) {
+  if (st == GH_OK && mode == GH_QUANT_NONE) {  // the bf16 head is the embedding itself
+    hipError_t e = hipMemcpyAsync(m->at<uint8_t>(m->lm_head), m->embed_dev, (size_t)V * H * 2,
+                                  hipMemcpyDeviceToDevice, ctx->stream);
+    if (e != hipSuccess) st = fail(GH_ERR_HIP, std::string("LM head copy: ") + hipGetErrorString(e));
+  } else if (st == GH_OK) {
     const uint32_t chunk = (uint32_t)std::max<size_t>(1, staging_elems / H);
     for (uint32_t r0 = 0; r0 < V && st == GH_OK; r0 += chunk) {
       const uint32_t n = std::min(chunk, V - r0);
@@ -774,9 +791,25 @@ gh_status gh_model_init_synthetic(gh_context* ctx, const gh_model_config* cfg, g
 
 void gh_model_deinit(gh_model* m) { delete m; }
 
+namespace {
+gh_status forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
+                        uint32_t slot_idx, const uint32_t* active_slots, uint32_t n_active,
+                        uint32_t* out_token, bool open_gates);
+}  // namespace
+
 gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
                                     uint32_t slot_idx, const uint32_t* active_slots,
                                     uint32_t n_active, uint32_t* out_token) {
+  return forward_token(m, x, want_logits, clock, slot_idx, active_slots, n_active, out_token,
+                       false);
+}
+
+}  // extern "C"
+
+namespace {
+gh_status forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
+                        uint32_t slot_idx, const uint32_t* active_slots, uint32_t n_active,
+                        uint32_t* out_token, bool open_gates) {
   if (!m || !x || !active_slots || !out_token)
     return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: null argument");
   *out_token = 0;
@@ -802,8 +835,12 @@ gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits
                                   "for this clock");
     gh_ring_activate_slot(m->ring, 0, clock);
   }
-  return run_token(m, want_logits != 0, (m->active - m->io) + (size_t)n_active * 4, out_token);
+  return run_token(m, want_logits != 0, (m->active - m->io) + (size_t)n_active * 4, out_token,
+                   open_gates);
 }
+}  // namespace
+
+extern "C" {
 
 gh_status gh_model_ring_init(gh_model* m, uint32_t num_anchors, uint32_t window_size,
                              uint32_t num_recall) {
@@ -958,6 +995,20 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     for (uint32_t t = 0; t < T; t++)
       if (slot_idx[t] != gh_ring_slot_index(m->ring, clocks[t]))
         return fail(GH_ERR_INVALID, "gh_model_prefill: a slot is not the ring's slot for its clock");
+  if (m->mode == GH_QUANT_NONE) {
+    // bf16 layers prefill token by token through the decode graphs, as the
+    // reference prefills every mode (src/interactive.zig:33-37); the batched
+    // matrix-core prefill takes Q4_0 / Q8_0 rows
+    uint32_t tok = 0;
+    for (uint32_t t = 0; t < T; t++) {
+      gh_status ts = forward_token(m, x + (size_t)t * c.hidden_size, want_logits && t + 1 == T,
+                                   clocks[t], slot_idx[t], active + (size_t)t * active_stride,
+                                   n_active[t], &tok, true);
+      if (ts != GH_OK) return ts;
+    }
+    if (want_logits) *out_token = tok;
+    return GH_OK;
+  }
   gh_status st = ensure_prefill(m, T, active_stride);
   if (st != GH_OK) return st;
   hipStream_t s = m->ctx->stream;
@@ -1288,7 +1339,7 @@ std::pair<uint8_t*, size_t> tensor_ref(const gh_model* m, int layer, gh_tensor t
   const uint32_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
   switch (t) {
     case GH_T_LM_HEAD:
-      return {m->arena + m->lm_head, (size_t)V * (H / 32) * 36};
+      return {m->arena + m->lm_head, m->head_bytes()};
     case GH_T_FINAL_NORM:
       return {m->arena + m->final_norm, (size_t)H * 4};
     case GH_T_EMBED:

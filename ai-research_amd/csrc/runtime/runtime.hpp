@@ -67,10 +67,13 @@ inline gh_status launch_stream(gh_context* ctx, const char* family, GateUpArgs* 
                                const uint32_t* run = nullptr) {
   return launch_stream(ctx, family, {&a->Wg, &a->Wu, &a->Y}, xp, M, K, run);
 }
-// The fused Q8 LM-head stream (family gh_argmax_q8) followed by the
-// reduction of its block partials to the token.
+// The fused LM-head stream (family gh_argmax_q8, or gh_argmax_bf16 for the
+// bf16 head) followed by the reduction of its block partials to the token.
 gh_status launch_argmax_stream(gh_context* ctx, ArgmaxArgs* a, const XPro& xp, uint32_t M,
-                               uint32_t K, uint32_t* token);
+                               uint32_t K, uint32_t* token, bool bf16 = false);
+// Stream family names of a weight mode (Q4_0, Q8_0 or bf16 rows).
+const char* gemv_family(gh_quant_mode mode);
+const char* gateup_family(gh_quant_mode mode);
 // Kernel name and persistent grid of one row-stream launch.
 struct StreamShape {
   std::string name;

@@ -60,6 +60,7 @@ _SIGS = {
     "gh_synth_uniform_u32": (_i, [_vp, _sz, _u64, _u64, _u32]),
     "gh_gemv_q4": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
     "gh_gemv_q8": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
+    "gh_gemv_bf16": (_i, [_vp, _vp, _vp, _vp, _u32, _u32]),
     "gh_gate_up_geglu_q4": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32]),
     "gh_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _u32, _f32]),
     "gh_add_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _f32, _f32]),
@@ -84,6 +85,7 @@ _SIGS.update({
     "gh_norm_gemv": (_i, [_vp, _i, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
     "gh_norm_gate_up_geglu": (_i, [_vp, _i, _vp, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
     "gh_norm_gemv_argmax_q8": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
+    "gh_norm_gemv_argmax_bf16": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, C.POINTER(XPrologue)]),
 })
 
 class ModelConfig(C.Structure):
@@ -328,6 +330,9 @@ class Context:
     def gemv_q8(self, W, X, Y, M, K):
         _check(lib().gh_gemv_q8(self.h, _addr(W), _addr(X), _addr(Y), M, K), "gh_gemv_q8")
 
+    def gemv_bf16(self, W, X, Y, M, K):
+        _check(lib().gh_gemv_bf16(self.h, _addr(W), _addr(X), _addr(Y), M, K), "gh_gemv_bf16")
+
     def gate_up_geglu_q4(self, Wg, Wu, X, Y, M, K):
         _check(lib().gh_gate_up_geglu_q4(self.h, _addr(Wg), _addr(Wu), _addr(X), _addr(Y), M, K),
                "gh_gate_up_geglu_q4")
@@ -349,6 +354,11 @@ class Context:
         _check(lib().gh_norm_gemv_argmax_q8(self.h, _addr(W), _addr(logits) if logits else None,
                                             _addr(token), M, K, C.byref(pro)),
                "gh_norm_gemv_argmax_q8")
+
+    def norm_gemv_argmax_bf16(self, W, logits, token, M, K, pro):
+        _check(lib().gh_norm_gemv_argmax_bf16(self.h, _addr(W), _addr(logits) if logits else None,
+                                              _addr(token), M, K, C.byref(pro)),
+               "gh_norm_gemv_argmax_bf16")
 
     def rmsnorm(self, X, W, Y, dim, eps=1e-6):
         _check(lib().gh_rmsnorm(self.h, _addr(X), _addr(W), _addr(Y), dim, eps), "gh_rmsnorm")

@@ -125,6 +125,11 @@ gh_status gh_gemv_q4(gh_context *ctx, const void *W, const float *X, float *Y,
 /* recordGemvLogits / Q8 pipeline (kernels.zig:88-91), shaders/gemv_q8.wgsl. */
 gh_status gh_gemv_q8(gh_context *ctx, const void *W, const float *X, float *Y,
                      uint32_t M, uint32_t K);
+/* recordGemv in mode none (the --gpu flag; kernels.zig:36 selects
+ * shaders/gemv_bf16.wgsl:1-63): Y[M] = W[M x K] . X[K] with W row-major bf16
+ * widened exactly to f32.  K % 128 == 0, W 16-byte aligned. */
+gh_status gh_gemv_bf16(gh_context *ctx, const void *W, const float *X, float *Y,
+                       uint32_t M, uint32_t K);
 /* recordGateUpSwiGlu (kernels.zig:92-95), shaders/fused_mlp_q4.wgsl:
  * Y[r] = gelu_tanh(Wg[r] . X) * (Wu[r] . X) for r < M. */
 gh_status gh_gate_up_geglu_q4(gh_context *ctx, const void *Wg, const void *Wu,
@@ -146,11 +151,14 @@ typedef struct gh_xprologue {
   float scalar, eps;
   uint32_t mode;
 } gh_xprologue;
-/* Y = W . prologue(x) with Q4_0 or Q8_0 rows (recordRmsNorm + recordGemv). */
+/* Y = W . prologue(x) with Q4_0, Q8_0 or (GH_QUANT_NONE) bf16 rows
+ * (recordRmsNorm + recordGemv). */
 gh_status gh_norm_gemv(gh_context *ctx, gh_quant_mode mode, const void *W, float *Y, uint32_t M,
                        uint32_t K, const gh_xprologue *pro);
 /* Y = gelu_tanh(Wg . x) * (Wu . x), x = prologue (recordAddRmsNorm +
- * recordGateUpSwiGlu). */
+ * recordGateUpSwiGlu); Q4_0, Q8_0 or bf16 rows.  (For mode none the
+ * reference binds the Q4 shader to bf16 rows, kernels.zig:41; the bf16 form
+ * computes the CPU path's gatedMlp, src/kernels.zig:100-129.) */
 gh_status gh_norm_gate_up_geglu(gh_context *ctx, gh_quant_mode mode, const void *Wg,
                                 const void *Wu, float *Y, uint32_t M, uint32_t K,
                                 const gh_xprologue *pro);
@@ -160,6 +168,11 @@ gh_status gh_norm_gate_up_geglu(gh_context *ctx, gh_quant_mode mode, const void 
  * (device, M floats) are written when non-null. */
 gh_status gh_norm_gemv_argmax_q8(gh_context *ctx, const void *W, float *logits, uint32_t *token,
                                  uint32_t M, uint32_t K, const gh_xprologue *pro);
+/* The same with the bf16 head of mode none (the embedding itself,
+ * model_gpu.zig:160-161; gemv_logits = the bf16 GEMV, kernels.zig:38). */
+gh_status gh_norm_gemv_argmax_bf16(gh_context *ctx, const void *W, float *logits,
+                                   uint32_t *token, uint32_t M, uint32_t K,
+                                   const gh_xprologue *pro);
 
 /* recordRmsNorm (kernels.zig:108-111), shaders/rmsnorm.wgsl:
  * Y = X * (mean(X^2) + eps)^-1/2 * W.  Y may alias X. */
@@ -314,9 +327,11 @@ typedef struct gh_layer_weights {
 } gh_layer_weights;
 
 /* GpuModelContext.init (model_gpu.zig:75): quantizes every layer matrix with
- * quantizeMatrix's bytes (Q4_0 or Q8_0 per mode; the tied LM head is always
- * Q8_0, model_gpu.zig:160-161), widens norms to f32, allocates the K/V ring
- * caches and records the decode and prefill graphs.  embed_tokens is
+ * quantizeMatrix's bytes (Q4_0 or Q8_0 per mode), or keeps the bf16 rows in
+ * mode GH_QUANT_NONE (createWeightBuffer, model_gpu.zig:51-57); the tied LM
+ * head is Q8_0 in the quantized modes and bf16 in mode none (model_gpu.zig:
+ * 160-161).  Widens norms to f32, allocates the K/V ring caches and records
+ * the decode and prefill graphs.  embed_tokens is
  * [vocab][hidden] bf16.  quiescence_thresh != 0 records the decode graph
  * with layer gating, as gh_model_set_quiescence describes; 0 records it
  * ungated (the reference's default). */

@@ -241,6 +241,18 @@ void orc_gemv_bf16(const uint16_t *w, const float *x, float *y, size_t rows, siz
   for (size_t r = 0; r < rows; r++) y[r] = dot_bf16(w + r * cols, x, cols);
 }
 
+/* gemvParallel (kernels.zig:76-92): the same rows split over threads. */
+typedef struct { const uint16_t *w; const float *x; float *y; size_t cols; } gvb_ctx;
+static void gvb_rows(void *p, size_t r0, size_t r1) {
+  gvb_ctx *c = (gvb_ctx *)p;
+  for (size_t r = r0; r < r1; r++) c->y[r] = dot_bf16(c->w + r * c->cols, c->x, c->cols);
+}
+static void gemv_bf16_par(const uint16_t *w, const float *x, float *y, size_t rows, size_t cols,
+                          int nthreads) {
+  gvb_ctx c = {w, x, y, cols};
+  par_rows(rows, nthreads, gvb_rows, &c);
+}
+
 /* ------------------------------------------------------------------------ */
 /* kernels.zig                                                              */
 /* ------------------------------------------------------------------------ */
@@ -488,18 +500,31 @@ void orc_embed(const uint16_t *embed_bf16, uint32_t token, size_t hidden, float 
   for (size_t i = 0; i < hidden; i++) x[i] = orc_bf16_to_f32(row[i]) * scale;
 }
 
+/* Mode none (the reference's --gpu bf16 mode, src/gpu/model_gpu.zig:51-57)
+ * keeps the checkpoint's bf16 rows: the layer pointers then address bf16
+ * elements, two per word.  The CPU forward uses the same bf16 rows
+ * (src/model/forward.zig:112-124). */
 static void layer_gemv(const orc_model *m, const uint32_t *w, const float *x,
                        float *y, size_t rows, size_t cols, int nt) {
   if (m->layer_mode == ORC_QUANT_Q8) orc_gemv_q8(w, x, y, rows, cols, nt);
-  else orc_gemv_q4(w, x, y, rows, cols, nt);
+  else if (m->layer_mode == ORC_QUANT_Q4) orc_gemv_q4(w, x, y, rows, cols, nt);
+  else gemv_bf16_par((const uint16_t *)w, x, y, rows, cols, nt);
 }
 
-typedef struct { float *act; const float *x; const uint32_t *wg, *wu; size_t h, wpr; int q8; } gum_ctx;
+/* one row of gate or up in the layer mode */
+static float mode_row_dot(int mode, const uint32_t *w, size_t r, size_t wpr, const float *x,
+                          size_t h) {
+  if (mode == ORC_QUANT_Q8) return q8_row_dot(w + r * wpr, x, h);
+  if (mode == ORC_QUANT_Q4) return q4_row_dot(w + r * wpr, x, h);
+  return dot_bf16((const uint16_t *)w + r * h, x, h);
+}
+
+typedef struct { float *act; const float *x; const uint32_t *wg, *wu; size_t h, wpr; int mode; } gum_ctx;
 static void gum_rows(void *p, size_t r0, size_t r1) {
   gum_ctx *c = (gum_ctx *)p;
   for (size_t r = r0; r < r1; r++) {
-    float g = c->q8 ? q8_row_dot(c->wg + r * c->wpr, c->x, c->h) : q4_row_dot(c->wg + r * c->wpr, c->x, c->h);
-    float u = c->q8 ? q8_row_dot(c->wu + r * c->wpr, c->x, c->h) : q4_row_dot(c->wu + r * c->wpr, c->x, c->h);
+    float g = mode_row_dot(c->mode, c->wg, r, c->wpr, c->x, c->h);
+    float u = mode_row_dot(c->mode, c->wu, r, c->wpr, c->x, c->h);
     c->act[r] = orc_gelu_tanh(g) * u;
   }
 }
@@ -546,8 +571,7 @@ static void forward_layer(const orc_model *m, const orc_layer *L, orc_scratch *s
                           uint64_t clock, size_t slot_idx, const uint32_t *active,
                           size_t n_active, int nt) {
   size_t H = m->hidden, I = m->intermediate, nq = m->num_q_heads;
-  int q8 = m->layer_mode == ORC_QUANT_Q8;
-  size_t wpr_h = orc_quantized_row_words(H, q8 ? ORC_QUANT_Q8 : ORC_QUANT_Q4);
+  size_t wpr_h = orc_quantized_row_words(H, m->layer_mode);
   size_t hd = L->head_dim, qd = nq * hd, kvd = L->num_kv_heads * hd;
   float theta = L->full_attention ? m->rope_theta_full : m->rope_theta;
   orc_rmsnorm(s->normed, x, L->input_norm, H, m->eps);
@@ -564,7 +588,7 @@ static void forward_layer(const orc_model *m, const orc_layer *L, orc_scratch *s
   if (L->post_attn_norm) orc_rmsnorm(s->o, s->o, L->post_attn_norm, H, m->eps);
   for (size_t i = 0; i < H; i++) x[i] = (x[i] + s->o[i]) * 1.0f;
   orc_rmsnorm(s->normed, x, L->pre_ffn_norm, H, m->eps);
-  gum_ctx gc = {s->act, s->normed, L->wg, L->wu, H, wpr_h, q8};
+  gum_ctx gc = {s->act, s->normed, L->wg, L->wu, H, wpr_h, m->layer_mode};
   par_rows(I, nt, gum_rows, &gc);
   layer_gemv(m, L->wd, s->act, s->o, H, I, nt);
   if (L->post_ffn_norm) orc_rmsnorm(s->o, s->o, L->post_ffn_norm, H, m->eps);
@@ -574,7 +598,10 @@ static void forward_layer(const orc_model *m, const orc_layer *L, orc_scratch *s
 static uint32_t forward_tail(const orc_model *m, orc_scratch *s, const float *x, float *logits,
                              int nt) {
   orc_rmsnorm(s->normed, x, m->final_norm, m->hidden, m->eps);
-  orc_gemv_q8(m->lm_head_q8, s->normed, logits, m->vocab, m->hidden, nt);
+  if (m->layer_mode == ORC_QUANT_NONE)  /* the bf16 embedding (model_gpu.zig:160-161) */
+    gemv_bf16_par((const uint16_t *)m->lm_head, s->normed, logits, m->vocab, m->hidden, nt);
+  else
+    orc_gemv_q8(m->lm_head, s->normed, logits, m->vocab, m->hidden, nt);
   return orc_argmax(logits, m->vocab);
 }
 

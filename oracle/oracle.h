@@ -124,15 +124,16 @@ typedef struct orc_layer {
   const float *input_norm, *q_norm, *k_norm, *post_attn_norm, *pre_ffn_norm,
       *post_ffn_norm; /* post_* may be NULL */
   float layer_scalar;
-  const uint32_t *wq, *wk, *wv, *wo, *wg, *wu, *wd; /* Q4_0 (or Q8_0) rows */
+  /* Q4_0 or Q8_0 rows; in mode none the bf16 rows (uint16 pairs per word) */
+  const uint32_t *wq, *wk, *wv, *wo, *wg, *wu, *wd;
   float *k_cache, *v_cache; /* [total_slots][num_kv_heads*head_dim] */
 } orc_layer;
 
 typedef struct orc_model {
   size_t hidden, intermediate, vocab, num_q_heads, num_layers;
-  int layer_mode; /* ORC_QUANT_Q4 or ORC_QUANT_Q8 */
+  int layer_mode; /* ORC_QUANT_Q4, ORC_QUANT_Q8 or ORC_QUANT_NONE (bf16) */
   float eps, rope_theta, rope_theta_full;
-  const uint32_t *lm_head_q8;
+  const uint32_t *lm_head; /* Q8_0 rows; bf16 rows in mode none */
   const float *final_norm;
   const orc_layer *layers;
 } orc_model;

@@ -366,11 +366,14 @@ class _Model(C.Structure):
     _fields_ = [("hidden", _sz), ("intermediate", _sz), ("vocab", _sz),
                 ("num_q_heads", _sz), ("num_layers", _sz), ("layer_mode", C.c_int),
                 ("eps", C.c_float), ("rope_theta", C.c_float), ("rope_theta_full", C.c_float),
-                ("lm_head_q8", _u32p), ("final_norm", _f32p), ("layers", C.POINTER(_Layer))]
+                ("lm_head", _u32p), ("final_norm", _f32p), ("layers", C.POINTER(_Layer))]
 
 
 class Model:
     """Quantized weights + per-layer K/V caches for orc_forward_token.
+
+    Matrices and the head are uint32 word arrays: Q4_0 / Q8_0 rows, or in
+    layer_mode QUANT_NONE the bf16 rows (two per word) with a bf16 head.
 
     layers: list of dicts with keys full, head_dim, rotary_dim, num_kv_heads,
     k_eq_v, input_norm, q_norm, k_norm, post_attn_norm, pre_ffn_norm,
@@ -379,7 +382,7 @@ class Model:
     updated in place by forward().
     """
 
-    def __init__(self, hidden, intermediate, vocab, num_q_heads, layers, lm_head_q8,
+    def __init__(self, hidden, intermediate, vocab, num_q_heads, layers, lm_head,
                  final_norm, eps=1e-6, rope_theta=10000.0, rope_theta_full=1e6,
                  layer_mode=QUANT_Q4):
         self._keep = []
@@ -409,7 +412,7 @@ class Model:
                 self._keep.append(a)
                 setattr(L, name, _p(a, C.c_float))
         self._layers = arr
-        head = _c(lm_head_q8, np.uint32)
+        head = _c(lm_head, np.uint32)
         fn = _c(final_norm, np.float32)
         self._keep += [head, fn]
         self._m = _Model(hidden, intermediate, vocab, num_q_heads, len(layers), layer_mode,

@@ -1,5 +1,6 @@
 """Builds the oracle's model (oracle.Model) from a GPU model's own tensors, so
-the CPU restatement and the device run the same quantized bytes."""
+the CPU restatement and the device run the same quantized bytes (or, in
+mode none, the same bf16 rows)."""
 import numpy as np
 
 import gemma_hip as gh
@@ -15,9 +16,14 @@ def layer_dims(cfg, l):
                 k_eq_v=full and bool(cfg.attention_k_eq_v))
 
 
+# uint32 words per 32 weights of a row, and the oracle's mode, per weight mode
+WORDS = {gh.QUANT_Q4: 5, gh.QUANT_Q8: 9, gh.QUANT_NONE: 16}
+ORC_MODE = {gh.QUANT_Q4: orc.QUANT_Q4, gh.QUANT_Q8: orc.QUANT_Q8, gh.QUANT_NONE: orc.QUANT_NONE}
+
+
 def oracle_model(m, cfg, mode=gh.QUANT_Q4):
     H, I, V, nq = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_attention_heads
-    words = 9 if mode == gh.QUANT_Q8 else 5
+    words = WORDS[mode]
     layers = []
     for l in range(cfg.num_hidden_layers):
         d = layer_dims(cfg, l)
@@ -43,4 +49,4 @@ def oracle_model(m, cfg, mode=gh.QUANT_Q4):
     head = m.read(-1, gh.T_LM_HEAD, np.uint32).reshape(V, -1)
     fn = m.read(-1, gh.T_FINAL_NORM, np.float32)
     return orc.Model(H, I, V, nq, layers, head, fn, cfg.rms_norm_eps, cfg.rope_theta,
-                     cfg.rope_theta_full, orc.QUANT_Q8 if mode == gh.QUANT_Q8 else orc.QUANT_Q4), layers
+                     cfg.rope_theta_full, ORC_MODE[mode]), layers

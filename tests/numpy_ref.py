@@ -145,6 +145,8 @@ def attention64(q, k_cache, v_cache, active, nq, nkv, hd):
 #   "scalar_before_ffn" layer_scalar applied before the FFN add
 # ---------------------------------------------------------------------------
 def _deq(w, cols, mode):
+    if mode == "bf16":  # mode none: the bf16 rows themselves, two per uint32 word
+        return bf16_to_f32(np.ascontiguousarray(w).view(np.uint16)).astype(np.float64).reshape(-1, cols)
     return dequant_q8(w, cols) if mode == "q8" else dequant_q4(w, cols)
 
 
@@ -232,6 +234,8 @@ def forward64(layers, x, clock, slot, active, head_q8, final_norm, nq, eps=1e-6,
             x = x * s_l  # forward.zig:61-63
     if not want_logits:
         return 0, x, None
-    # forward.zig:62-70 with the GPU's Q8_0 head (model_dispatch.zig:121-127)
-    logits = dequant_q8(head_q8, H) @ _rms64(x, final_norm, eps)
+    # forward.zig:62-70 with the GPU's Q8_0 head (model_dispatch.zig:121-127),
+    # or the bf16 embedding in mode none (model_gpu.zig:160-161)
+    head = _deq(head_q8, H, "bf16") if mode == "bf16" else dequant_q8(head_q8, H)
+    logits = head @ _rms64(x, final_norm, eps)
     return int(np.argmax(logits)), x, logits

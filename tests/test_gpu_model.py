@@ -9,7 +9,7 @@ import pytest
 import gemma_hip as gh
 import numpy_ref as nr
 import oracle as orc
-from model_ref import layer_dims, oracle_model
+from model_ref import WORDS, layer_dims, oracle_model
 from tol import assert_close
 
 pytestmark = pytest.mark.gpu
@@ -42,7 +42,7 @@ def check_token(m, ref_logits, tok, rtok, what):
 
 
 @pytest.mark.parametrize("k_eq_v", [False, True])
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 def test_tiny_model_decode_sequence(gpu, mode, k_eq_v):
     # k_eq_v: attention_k_eq_v = 1, so the full-attention layer (layer 2) has
     # no v rows and its values are the raw keys (src/model/loader.zig:36-42,
@@ -52,7 +52,7 @@ def test_tiny_model_decode_sequence(gpu, mode, k_eq_v):
     try:
         om, layers = oracle_model(m, cfg, mode)
         assert layers[2]["k_eq_v"] == k_eq_v and not layers[0]["k_eq_v"]
-        qkv_rows = m.read(2, gh.T_QKV, np.uint32).size // ((cfg.hidden_size // 32) * (9 if mode == gh.QUANT_Q8 else 5))
+        qkv_rows = m.read(2, gh.T_QKV, np.uint32).size // ((cfg.hidden_size // 32) * WORDS[mode])
         assert qkv_rows == 4 * 128 + 2 * 128 * (1 if k_eq_v else 2)
         embed = m.read(-1, gh.T_EMBED, np.uint16).reshape(cfg.vocab_size, cfg.hidden_size)
         ring = gh.Ring(cfg.num_hidden_layers, 4, 16, 4)
@@ -81,8 +81,11 @@ def test_tiny_model_decode_sequence(gpu, mode, k_eq_v):
         m.close()
 
 
-def test_model_init_from_host_bf16(gpu):
-    # gh_model_init quantizes borrowed host bf16 tensors with quantizeMatrix's bytes
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_NONE])
+def test_model_init_from_host_bf16(gpu, mode):
+    # gh_model_init quantizes borrowed host bf16 tensors with quantizeMatrix's
+    # bytes, or in mode none (--gpu) keeps the bf16 rows and a bf16 head
+    # (src/gpu/model_gpu.zig:51-57,160-161)
     cfg = tiny_cfg(layers=2, full_layers=())
     H, I, V, nq = 256, 512, 1024, 4
     rng = np.random.default_rng(3)
@@ -102,17 +105,20 @@ def test_model_init_from_host_bf16(gpu):
         layers.append(w)  # layer 1 has no v_proj: the key projection serves as value
     embed = bf(V, H)
     fnorm = bf(H, mean=1, std=0.1)
-    m = gh.Model(gpu, cfg, layers=layers, embed=embed, final_norm=fnorm)
+    m = gh.Model(gpu, cfg, mode=mode, layers=layers, embed=embed, final_norm=fnorm)
+    bf = mode == gh.QUANT_NONE
+    rows = (lambda w: np.ascontiguousarray(w).view(np.uint32)) if bf else orc.quantize_q4  # noqa: E731
     try:
         w0 = layers[0]
-        qkv = m.read(0, gh.T_QKV, np.uint32).reshape(-1, (H // 32) * 5)
-        assert np.array_equal(qkv, orc.quantize_q4(np.concatenate([w0["q_proj"], w0["k_proj"], w0["v_proj"]])))
-        assert np.array_equal(m.read(1, gh.T_QKV, np.uint32).reshape(-1, (H // 32) * 5),
-                              orc.quantize_q4(np.concatenate([layers[1]["q_proj"], layers[1]["k_proj"]])))
-        assert np.array_equal(m.read(0, gh.T_DOWN, np.uint32).reshape(H, -1), orc.quantize_q4(w0["down_proj"]))
-        assert np.array_equal(m.read(-1, gh.T_LM_HEAD, np.uint32).reshape(V, -1), orc.quantize_q8(embed))
+        qkv = m.read(0, gh.T_QKV, np.uint32).reshape(-1, (H // 32) * WORDS[mode])
+        assert np.array_equal(qkv, rows(np.concatenate([w0["q_proj"], w0["k_proj"], w0["v_proj"]])))
+        assert np.array_equal(m.read(1, gh.T_QKV, np.uint32).reshape(-1, (H // 32) * WORDS[mode]),
+                              rows(np.concatenate([layers[1]["q_proj"], layers[1]["k_proj"]])))
+        assert np.array_equal(m.read(0, gh.T_DOWN, np.uint32).reshape(H, -1), rows(w0["down_proj"]))
+        assert np.array_equal(m.read(-1, gh.T_LM_HEAD, np.uint32).reshape(V, -1),
+                              rows(embed) if bf else orc.quantize_q8(embed))
         assert np.array_equal(m.read(0, gh.T_Q_NORM, np.float32), nr.bf16_to_f32(w0["q_norm"]))
-        om, _ = oracle_model(m, cfg)
+        om, _ = oracle_model(m, cfg, mode)
         for l in range(2):
             om._layers[l].layer_scalar = 0.5
         ring = gh.Ring(2, 4, 16, 4)
@@ -133,11 +139,11 @@ def _12b(layers, full_layers):
                            full_layers=full_layers)
 
 
-def _populated_step(gpu, cfg):
+def _populated_step(gpu, cfg, mode=gh.QUANT_Q4):
     """A model with every ring cache filled (K ~ N(0,1), V unit-RMS rows) and
     the clock at 600 (S = 544 active slots); returns what both sides need."""
     nl = cfg.num_hidden_layers
-    m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=1)
+    m = gh.Model(gpu, cfg, mode=mode, seed=1)
     ring = gh.Ring(nl, 32, 512, 96)
     for c in range(600):
         ring.activate_slot(0, c)
@@ -152,14 +158,16 @@ def _populated_step(gpu, cfg):
         v /= np.sqrt(np.mean(v * v, axis=2, keepdims=True) + 1e-6)
         m.write(l, gh.T_K_CACHE, k)
         m.write(l, gh.T_V_CACHE, v)
-    om, layers = oracle_model(m, cfg)
+    om, layers = oracle_model(m, cfg, mode)
     return m, om, layers, clock, slot, active
 
 
-def test_12b_width_two_layers_strict(gpu):
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_NONE])
+def test_12b_width_two_layers_strict(gpu, mode):
     # 12B widths, one sliding and one full-attention layer, 544 active slots:
     # logits within the 2e-3 bar elementwise and the greedy token bit-exact.
-    m, om, layers, clock, slot, active = _populated_step(gpu, _12b(2, [1]))
+    # Mode none: bf16 layers and the bf16 262144 x 3840 head.
+    m, om, layers, clock, slot, active = _populated_step(gpu, _12b(2, [1]), mode)
     try:
         x = m.embed(4242)
         tok = m.forward(x, clock, slot, active)

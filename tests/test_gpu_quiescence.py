@@ -30,11 +30,11 @@ def _cfg():
                            global_head_dim=128, full_layers=(5,))
 
 
-def _oracle_run(m, cfg, embed, thr, record=None):
+def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4):
     """The reference sequence on the oracle: the prompt through the prefill
     graph (gates at threshold 0), then the decode steps gated at thr.
     Returns per step (token, logits, run, motions, caches) when record."""
-    om, layers = oracle_model(m, cfg)
+    om, layers = oracle_model(m, cfg, mode)
     ring = gh.Ring(1, 4, 24, 4)
     L, H = cfg.num_hidden_layers, cfg.hidden_size
     xp = np.zeros((L, H), np.float32)
@@ -52,22 +52,25 @@ def _oracle_run(m, cfg, embed, thr, record=None):
     return out, layers
 
 
-def test_quiescence_gating_matches_oracle(gpu):
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_NONE])
+def test_quiescence_gating_matches_oracle(gpu, mode):
+    # mode none: bf16 layers, the gated bf16 streams, and a prompt that goes
+    # token by token (its last token with every gate open)
     cfg = _cfg()
-    m = gh.Model(gpu, cfg, seed=21)
+    m = gh.Model(gpu, cfg, mode=mode, seed=21)
     try:
         embed = m.read(-1, gh.T_EMBED, np.uint16).reshape(cfg.vocab_size, cfg.hidden_size)
         dl = cfg.num_hidden_layers // 3
         thr = None
         for cand in (0.1, 0.07, 0.15, 0.2, 0.05, 0.3):
-            ref, _ = _oracle_run(m, cfg, embed, cand)
+            ref, _ = _oracle_run(m, cfg, embed, cand, mode=mode)
             motions = np.concatenate([r[3][dl:] for r in ref if r[4]])
             runs = np.concatenate([r[2][dl:] for r in ref if r[4]])
             if np.all(np.abs(motions - cand) > 0.05 * cand) and 0 < runs.sum() < runs.size:
                 thr = cand
                 break
         assert thr is not None, "no threshold with a 5% margin"
-        ref, layers = _oracle_run(m, cfg, embed, thr)
+        ref, layers = _oracle_run(m, cfg, embed, thr, mode=mode)
         m.set_quiescence(thr)
         ring = gh.Ring(1, 4, 24, 4)
         xs = np.stack([orc.embed(embed, t, cfg.hidden_size) for t in TOKENS])

@@ -326,7 +326,8 @@ def _tiny_forward_model(mode):
     layer_scalar 0.5."""
     rng = np.random.default_rng(99)
     H, I, V, nq, slots = 256, 512, 512, 4, 24
-    quant = nr.quantize_q8 if mode == "q8" else nr.quantize_q4
+    quant = {"q8": nr.quantize_q8, "q4": nr.quantize_q4,
+             "bf16": lambda w: np.ascontiguousarray(w).view(np.uint32)}[mode]
     mat = lambda r, c: quant(nr.bf16_rne(rng.standard_normal((r, c)).astype(np.float32) * 0.05))  # noqa: E731
     vec = lambda n: nr.bf16_to_f32(nr.bf16_rne((1 + 0.1 * rng.standard_normal(n)).astype(np.float32)))  # noqa: E731
     specs = [dict(full=False, head_dim=64, num_kv_heads=2, k_eq_v=False, scalar=1.0, post_attn=True),
@@ -348,24 +349,27 @@ def _tiny_forward_model(mode):
         v /= np.sqrt(np.mean(v.reshape(slots, nkv, hd) ** 2, axis=2, keepdims=True) + 1e-6).repeat(hd, 2).reshape(slots, kvd)
         d["k_cache"], d["v_cache"] = k, v
         layers.append(d)
-    head = nr.quantize_q8(nr.bf16_rne(rng.standard_normal((V, H)).astype(np.float32) * 0.05))
+    head = nr.bf16_rne(rng.standard_normal((V, H)).astype(np.float32) * 0.05)
+    head = quant(head) if mode == "bf16" else nr.quantize_q8(head)
     fnorm = vec(H)
     return H, I, V, nq, layers, head, fnorm, rng
+
+
+_ORC_MODE = {"q4": orc.QUANT_Q4, "q8": orc.QUANT_Q8, "bf16": orc.QUANT_NONE}
 
 
 def _copy_layers(layers):
     return [dict(d, k_cache=d["k_cache"].copy(), v_cache=d["v_cache"].copy()) for d in layers]
 
 
-@pytest.mark.parametrize("mode", ["q4", "q8"])
+@pytest.mark.parametrize("mode", ["q4", "q8", "bf16"])
 def test_forward_token_matches_fp64_restatement(mode):
     # orc_forward_token against tests/numpy_ref.forward64, written separately
     # from forward.zig / model_dispatch.zig: layer order, norm placement, the
     # layer scalar, gate/up roles, k_eq_v / missing v_proj, partial RoPE per
     # layer type, the cache write before attention and the Q8 head.
     H, I, V, nq, layers, head, fnorm, rng = _tiny_forward_model(mode)
-    om = orc.Model(H, I, V, nq, layers, head, fnorm,
-                   layer_mode=orc.QUANT_Q8 if mode == "q8" else orc.QUANT_Q4)
+    om = orc.Model(H, I, V, nq, layers, head, fnorm, layer_mode=_ORC_MODE[mode])
     ref_layers = _copy_layers(layers)
     for clock in (3, 4, 9, 17):
         slot = clock % 24

@@ -168,6 +168,26 @@ def bench_gemv(ctx, reps=256):
     return nbytes / (ms * 1e-3) / 1e9, ms * 1e3
 
 
+def bench_gemv_bf16(ctx, reps=96):
+    """The bf16 GEMV of mode none (shaders/gemv_bf16.wgsl), 8192 x 2048 bf16
+    rows, rotated over 24 weight copies (805 MB)."""
+    M, K, ncopy = 8192, 2048, 24
+    ws = []
+    for c in range(ncopy):
+        w = ctx.alloc(M * K * 2)
+        ctx.synth_normal_dev(w, M * K, 0, 600 + c, 0.0, 0.02, bf16=True)
+        ws.append(w)
+    X = ctx.upload(gh.synth_normal(K, 0, 3, 0.0, 1.0))
+    Y = ctx.alloc(M * 4)
+    ms = timed_graph(ctx, lambda i: ctx.gemv_bf16(ws[i % ncopy], X, Y, M, K), reps)
+    for w in ws:
+        w.free()
+    nbytes = M * K * 2 + K * 4 + M * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"us": round(ms * 1e3, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def timed_graph(ctx, launch, reps):
     """Average ms of one launch: `reps` launches recorded once as a graph,
     replayed once untimed, then timed with HIP events on the context stream.
@@ -306,6 +326,45 @@ def cpu_decode_baseline(m, cfg, clock, nt, steps=2):
             "host_cpus": os.cpu_count(), "kind": "port",
             "sample": "%d full 12B decode steps (48 layers + Q8 head, S = %d) after one untimed, "
                       "%.2f s each" % (steps, len(act), dt)}
+
+
+def bench_decode_bf16(ctx, n_prompt=512, n_decode=32):
+    """The 12B shape in mode none (the reference's --gpu): bf16 layers and the
+    bf16 262144 x 3840 head (24.2 GB of weights per token).  The prompt goes
+    token by token (the reference's prefill), then n_decode greedy steps on
+    the device ring."""
+    cfg = gh.model_config(vocab=262144, hidden=H, intermediate=I, layers=48, heads=16,
+                          kv_heads=8, head_dim=256, max_slots=640,
+                          full_layers=[l for l in range(48) if (l + 1) % 6 == 0])
+    m = gh.Model(ctx, cfg, mode=gh.QUANT_NONE, seed=0)
+    embed = m.read(-1, gh.T_EMBED, np.uint16).reshape(cfg.vocab_size, H)
+    scale = np.sqrt(np.float32(H))
+
+    def emb(t):
+        return (embed[t].astype(np.uint32) << 16).view(np.float32) * scale
+
+    m.ring_init(32, 512, 96)
+    prompt = gh.synth_uniform_u32(n_prompt, 1, 0, cfg.vocab_size)
+    xs = np.stack([emb(int(t)) for t in prompt])
+    t0 = time.perf_counter()
+    tok = m.ring_prefill(xs, 0, True)
+    prefill_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for i in range(n_decode):
+        tok = m.forward_clock(emb(tok), n_prompt + i, True)
+    decode_s = time.perf_counter() - t0
+    m.close()
+    layers = 48 * (8192 * H + H * 4096 + 2 * I * H + H * I) * 2
+    head = 262144 * H * 2
+    norms = 48 * (4 * H + 2 * 256) * 4 + H * 4
+    ideal_s = sum(layers + head + norms + 262144 * 4 + min(c + 1, 544) * 8 * 256 * 4 * 2 * 48
+                  for c in range(n_prompt, n_prompt + n_decode)) / (HBM_PEAK_GBS * 1e9)
+    return {"decode_tok_s": round(n_decode / decode_s, 2),
+            "decode_ms_per_token": round(decode_s / n_decode * 1e3, 3),
+            "weight_bytes_per_token": layers + head,
+            "decode_weight_gbs": round((layers + head) * n_decode / decode_s / 1e9, 1),
+            "decode_roofline_frac": round(ideal_s / decode_s, 4),
+            "prefill_token_by_token_ms": round(prefill_s * 1e3, 1)}
 
 
 def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
@@ -463,7 +522,9 @@ def main():
     gemv_gbs, gemv_us = bench_gemv(ctx)
     attn = bench_attention(ctx)
     head = bench_lm_head(ctx)
+    gemv_bf16 = bench_gemv_bf16(ctx)
     dec = bench_decode(ctx, args.prompt, args.decode, cpu=not args.no_cpu) if not args.no_decode else None
+    dec_bf16 = bench_decode_bf16(ctx, args.prompt) if not args.no_decode else None
     if dec:
         log("decode %.1f tok/s (%.3f ms/token), prefill %.1f tok/s"
             % (dec["decode_tok_s"], dec["decode_ms_per_token"], dec["prefill_tok_s"]))
@@ -521,6 +582,8 @@ def main():
                                                  "bytes": 10526720},
                   "attention_640_slots": attn,
                   "lm_head_q8_argmax": head,
+                  "gemv_bf16_8192x2048": gemv_bf16,
+                  "decode_12b_bf16": dec_bf16,
                   "cpu_baseline_1thread": cpu1,
                   "decode_12b": dec},
     }

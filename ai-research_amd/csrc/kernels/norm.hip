@@ -129,39 +129,37 @@ extern "C" __global__ __launch_bounds__(NORM_NT) void gh_qgate_k(
     uint32_t* run_out, uint32_t H, float eps, uint32_t gate) {
   __shared__ float red[NORM_NT / 64];
   const uint32_t n4 = H >> 2;
-  const bool add = prev_mode == 1u || (prev_mode == 2u && *prev_run != 0u);
-  float4 xv[QG_U];
+  // every input is loaded up front (one memory round trip; all pointers but
+  // wpost are valid in every mode), then the mode picks what it uses
+  const uint32_t prun = prev_mode == 2u ? *prev_run : 1u;
+  float4 xv[QG_U], mv[QG_U], wv[QG_U], pv[QG_U], av[QG_U];
+#pragma unroll
+  for (int u = 0; u < QG_U; u++) {
+    const uint32_t i = u * NORM_NT + threadIdx.x;
+    const uint32_t ic = i < n4 ? i : n4 - 1;
+    xv[u] = reinterpret_cast<const float4*>(xmid)[ic];
+    mv[u] = reinterpret_cast<const float4*>(m)[ic];
+    wv[u] = wpost ? reinterpret_cast<const float4*>(wpost)[ic] : make_float4(1.f, 1.f, 1.f, 1.f);
+    pv[u] = reinterpret_cast<const float4*>(xprev)[ic];
+    av[u] = reinterpret_cast<const float4*>(A)[ic];
+  }
+  const bool add = prev_mode == 1u || (prev_mode == 2u && prun != 0u);
   if (add) {
-    float4 mv[QG_U];
     float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < QG_U; u++) {
-      const uint32_t i = u * NORM_NT + threadIdx.x;
-      const uint32_t ic = i < n4 ? i : n4 - 1;
-      xv[u] = reinterpret_cast<const float4*>(xmid)[ic];
-      mv[u] = reinterpret_cast<const float4*>(m)[ic];
-      if (i < n4) ss += mv[u].x * mv[u].x + mv[u].y * mv[u].y + mv[u].z * mv[u].z + mv[u].w * mv[u].w;
-    }
+    for (int u = 0; u < QG_U; u++)
+      if (u * NORM_NT + threadIdx.x < n4)
+        ss += mv[u].x * mv[u].x + mv[u].y * mv[u].y + mv[u].z * mv[u].z + mv[u].w * mv[u].w;
     const float c = wpost ? 1.0f / sqrtf(block_sum(ss, red) / (float)H + eps) : 1.0f;
 #pragma unroll
     for (int u = 0; u < QG_U; u++) {
       const uint32_t i = u * NORM_NT + threadIdx.x;
-      if (i < n4) {
-        float4 w = make_float4(1.f, 1.f, 1.f, 1.f);
-        if (wpost) w = reinterpret_cast<const float4*>(wpost)[i];
-        const float4 r = wpost ? make_float4(mv[u].x * c * w.x, mv[u].y * c * w.y,
-                                             mv[u].z * c * w.z, mv[u].w * c * w.w)
-                               : mv[u];
-        xv[u] = make_float4((xv[u].x + r.x) * s, (xv[u].y + r.y) * s, (xv[u].z + r.z) * s,
-                            (xv[u].w + r.w) * s);
-        reinterpret_cast<float4*>(A)[i] = xv[u];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < QG_U; u++) {
-      const uint32_t i = u * NORM_NT + threadIdx.x;
-      xv[u] = reinterpret_cast<const float4*>(A)[i < n4 ? i : n4 - 1];
+      const float4 r = wpost ? make_float4(mv[u].x * c * wv[u].x, mv[u].y * c * wv[u].y,
+                                           mv[u].z * c * wv[u].z, mv[u].w * c * wv[u].w)
+                             : mv[u];
+      av[u] = make_float4((xv[u].x + r.x) * s, (xv[u].y + r.y) * s, (xv[u].z + r.z) * s,
+                          (xv[u].w + r.w) * s);
+      if (i < n4) reinterpret_cast<float4*>(A)[i] = av[u];
     }
   }
   if (!gate) return;
@@ -170,10 +168,10 @@ extern "C" __global__ __launch_bounds__(NORM_NT) void gh_qgate_k(
   for (int u = 0; u < QG_U; u++) {
     const uint32_t i = u * NORM_NT + threadIdx.x;
     if (i < n4) {
-      const float4 p = reinterpret_cast<const float4*>(xprev)[i];
-      const float a = xv[u].x - p.x, b = xv[u].y - p.y, e = xv[u].z - p.z, f = xv[u].w - p.w;
+      const float a = av[u].x - pv[u].x, b = av[u].y - pv[u].y, e = av[u].z - pv[u].z,
+                  f = av[u].w - pv[u].w;
       d += a * a + b * b + e * e + f * f;
-      reinterpret_cast<float4*>(xprev)[i] = xv[u];
+      reinterpret_cast<float4*>(xprev)[i] = av[u];
     }
   }
   const float ms = block_sum(d, red) / (float)H;

@@ -118,6 +118,44 @@ extern "C" __global__ __launch_bounds__(256) void gh_copy_u32_k(uint32_t* dst, c
     dst[i] = src[i];
 }
 
+// HBM read-bandwidth probe: the buffer's n4 16-byte vectors are read once,
+// U loads in flight per lane, and each workgroup writes the sum of what it
+// read (so no load is dead).  CONTIG = 0: grid-stride over the whole buffer
+// (every round of the grid reads one contiguous span); CONTIG = 1: workgroup
+// b reads its own contiguous 1/grid share.  n4 is a multiple of 256 U * grid
+// (checked by the host), so no bounds test sits in the loop.
+template <int U, bool CONTIG>
+__device__ __forceinline__ void read_probe(const float4* __restrict__ src, uint64_t n4,
+                                           float* sums) {
+  __shared__ float red[4];
+  const uint64_t T = (uint64_t)gridDim.x * 256;
+  const uint64_t per_wg = n4 / gridDim.x;
+  const uint64_t start = CONTIG ? blockIdx.x * per_wg + threadIdx.x
+                                : (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  const uint64_t end = CONTIG ? (blockIdx.x + 1) * per_wg : n4;
+  const uint64_t step = CONTIG ? 256 : T;
+  float acc = 0.f;
+  for (uint64_t i = start; i < end; i += step * U) {
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = src[i + u * step];
+#pragma unroll
+    for (int u = 0; u < U; u++) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) sums[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+#define GH_READ_PROBE(U, C)                                                                \
+  extern "C" __global__ __launch_bounds__(256) void gh_read_probe_u##U##_c##C##_k(         \
+      const float4* __restrict__ src, uint64_t n4, float* sums) {                          \
+    read_probe<U, C>(src, n4, sums);                                                       \
+  }
+GH_READ_PROBE(1, 0) GH_READ_PROBE(2, 0) GH_READ_PROBE(4, 0) GH_READ_PROBE(8, 0)
+GH_READ_PROBE(1, 1) GH_READ_PROBE(2, 1) GH_READ_PROBE(4, 1) GH_READ_PROBE(8, 1)
+
 // The per-token step kernel at the head of every decode graph.
 //
 // RoPE tables: for each of the model's two layer types (rot_t, theta_t; rot 0

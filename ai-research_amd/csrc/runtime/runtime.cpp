@@ -276,6 +276,26 @@ gh_status gh_buffer_fill_u32(gh_context* ctx, void* dev, uint32_t value, size_t 
   return ctx->launch("gh_fill_u32_k", dim3(grid), dim3(256), 0, args);
 }
 
+gh_status gh_read_probe(gh_context* ctx, const void* dev, size_t bytes, uint32_t per_lane,
+                        uint32_t contiguous, uint32_t grid, float* sums) {
+  if (!ctx || !dev || !sums) return fail(GH_ERR_INVALID, "gh_read_probe: null pointer");
+  if (per_lane != 1 && per_lane != 2 && per_lane != 4 && per_lane != 8)
+    return fail(GH_ERR_INVALID, "gh_read_probe: per_lane must be 1, 2, 4 or 8");
+  if (contiguous > 1) return fail(GH_ERR_INVALID, "gh_read_probe: contiguous must be 0 or 1");
+  if (grid == 0) grid = 4u * (uint32_t)ctx->num_cus;
+  if (reinterpret_cast<uintptr_t>(dev) & 15)
+    return fail(GH_ERR_INVALID, "gh_read_probe: buffer not 16-byte aligned");
+  const uint64_t chunk = 16ull * 256 * per_lane * grid;  // bytes one round of the grid reads
+  if (bytes == 0 || bytes % chunk != 0)
+    return fail(GH_ERR_INVALID, "gh_read_probe: bytes must be a positive multiple of " +
+                                    std::to_string(chunk) + " (16 B x 256 x per_lane x grid)");
+  uint64_t n4 = bytes / 16;
+  void* args[] = {&dev, &n4, &sums};
+  const std::string name = "gh_read_probe_u" + std::to_string(per_lane) + "_c" +
+                           std::to_string(contiguous) + "_k";
+  return ctx->launch(name, dim3(grid), dim3(256), 0, args);
+}
+
 // ---- events ----------------------------------------------------------------
 gh_status gh_event_create(gh_context* ctx, void** ev) {
   if (!ctx || !ev) return fail(GH_ERR_INVALID, "gh_event_create");

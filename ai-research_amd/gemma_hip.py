@@ -41,6 +41,7 @@ _SIGS = {
     "gh_buffer_read": (_i, [_vp, _vp, _vp, _sz]),
     "gh_buffer_copy": (_i, [_vp, _vp, _vp, _sz]),
     "gh_buffer_fill_u32": (_i, [_vp, _vp, _u32, _sz]),
+    "gh_read_probe": (_i, [_vp, _vp, _sz, _u32, _u32, _u32, _vp]),
     "gh_event_create": (_i, [_vp, C.POINTER(_vp)]),
     "gh_event_record": (_i, [_vp, _vp]),
     "gh_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f32)]),
@@ -278,6 +279,11 @@ class Context:
 
     def fill_u32(self, buf, value, count):
         _check(lib().gh_buffer_fill_u32(self.h, _addr(buf), value, count), "gh_buffer_fill_u32")
+
+    def read_probe(self, buf, nbytes, per_lane, contiguous, grid, sums):
+        """HBM read-bandwidth probe: reads nbytes of buf once (gh_read_probe)."""
+        _check(lib().gh_read_probe(self.h, _addr(buf), nbytes, per_lane, contiguous, grid,
+                                   _addr(sums)), "gh_read_probe")
 
     # ---- events
     def event(self):

@@ -142,30 +142,35 @@ def bench_mlp(ctx, steps, warmup):
 
 
 def bench_gemv(ctx, reps=256):
-    """Single Q4_0 GEMV, 8192 x 2048, rotated over 64 weight copies (671 MB)."""
+    """Single Q4_0 GEMV, 8192 x 2048, rotated over 64 weight copies (671 MB).
+    The copies are consecutive in one arena, so the same bytes also serve as
+    256 matrices of 2048 rows and 16 of 32768: the three sizes give the
+    per-launch fixed cost and the marginal read rate of the stream (a line
+    t = a + bytes / b through the 2048- and 32768-row points)."""
     M, K, ncopy = 8192, 2048, 64
+    mat = M * Q4_ROW(K)
+    arena = ctx.alloc(ncopy * mat)
     staging = ctx.alloc(M * K * 2)
-    ws = [make_q4(ctx, M, K, 0, 500 + c, staging) for c in range(ncopy)]
+    for c in range(ncopy):
+        ctx.synth_normal_dev(staging, M * K, 0, 500 + c, 0.0, 0.02, bf16=True)
+        ctx.quantize_dev(arena.ptr + c * mat, staging, M, K, gh.QUANT_Q4)
     staging.free()
     X = ctx.upload(gh.synth_normal(K, 0, 3, 0.0, 1.0))
-    Y = ctx.alloc(M * 4)
-    for i in range(ncopy):
-        ctx.gemv_q4(ws[i], X, Y, M, K)
-    ctx.sync()
-    e0, e1 = ctx.event(), ctx.event()
-    ctx.graph_begin()
-    for i in range(reps):
-        ctx.gemv_q4(ws[i % ncopy], X, Y, M, K)
-    g = ctx.graph_end()
-    ctx.graph_launch(g)
-    ctx.sync()
-    ctx.record(e0)
-    ctx.graph_launch(g)
-    ctx.record(e1)
-    ms = ctx.elapsed_ms(e0, e1) / reps
-    ctx.graph_destroy(g)
-    nbytes = M * Q4_ROW(K) + K * 4 + M * 4
-    return nbytes / (ms * 1e-3) / 1e9, ms * 1e3
+    Y = ctx.alloc(32768 * 4)
+    sizes = {}
+    for rows in (8192, 2048, 32768):
+        nb = rows * Q4_ROW(K)
+        n = ncopy * mat // nb
+        ms = timed_graph(ctx, lambda i: ctx.gemv_q4(arena.ptr + (i % n) * nb, X, Y, rows, K), reps)
+        sizes[rows] = (ms * 1e3, rows * Q4_ROW(K) + K * 4 + rows * 4)
+    arena.free()
+    us, nbytes = sizes[M]
+    (t0, b0), (t1, b1) = sizes[2048], sizes[32768]
+    marginal = (b1 - b0) / ((t1 - t0) * 1e-6) / 1e9
+    fit = {"us_2048_rows": round(t0, 3), "us_8192_rows": round(us, 3), "us_32768_rows": round(t1, 3),
+           "marginal_gbs": round(marginal, 1),
+           "fixed_us": round(t0 - b0 / (marginal * 1e9) * 1e6, 3)}
+    return nbytes / (us * 1e-6) / 1e9, us, fit
 
 
 def bench_gemv_bf16(ctx, reps=96):
@@ -211,6 +216,44 @@ def timed_graph(ctx, launch, reps):
     ctx.destroy_event(e0)
     ctx.destroy_event(e1)
     return ms
+
+
+def bench_read_ceiling(ctx):
+    """Attainable HBM read rate (gh_read_probe, a plain 16-byte load stream):
+    1 GiB read once per launch (4x the Infinity Cache) over a sweep of loads
+    in flight per lane, grid sizes and access orders; then, with the best
+    shape, reads of 72 MiB and 36 MiB windows rotated over the same GiB -- the
+    MLP kernels' sizes, where the per-launch ramp shows."""
+    GiB = 1 << 30
+    buf = ctx.alloc(GiB)
+    ctx.fill_u32(buf, 0x3C000000, GiB // 4)  # 2^-7: sums stay finite
+    sums = ctx.alloc(4 * 4096)
+    ncu = 256
+    sweep = []
+    for grid_per_cu in (1, 2, 4, 8):
+        for u in (1, 2, 4, 8):
+            for contig in (0, 1):
+                g = ncu * grid_per_cu
+                ms = timed_graph(ctx, lambda i: ctx.read_probe(buf, GiB, u, contig, g, sums), 8)
+                sweep.append((GiB / (ms * 1e-3) / 1e9, g, u, contig))
+    sweep.sort(reverse=True)
+    best_gbs, g, u, contig = sweep[0]
+    windows = {}
+    chunk = 16 * 256 * u * g  # a launch reads a whole number of grid rounds
+    for mib in (72, 36):
+        nb = max(chunk, (mib << 20) // chunk * chunk)
+        nwin = GiB // nb
+        ms = timed_graph(ctx, lambda i: ctx.read_probe(buf.ptr + nb * (i % nwin), nb, u, contig, g, sums), 64)
+        windows["%dMiB" % mib] = {"bytes": nb, "us": round(ms * 1e3, 3),
+                                  "gbs": round(nb / (ms * 1e-3) / 1e9, 1)}
+    buf.free()
+    sums.free()
+    return {"gbs_1GiB": round(best_gbs, 1), "frac_of_8TBs": round(best_gbs / HBM_PEAK_GBS, 4),
+            "best_shape": {"grid": g, "loads_in_flight_per_lane": u, "contiguous": contig},
+            "windows": windows,
+            "sweep_top5": [{"gbs": round(s[0], 1), "grid": s[1], "u": s[2], "contiguous": s[3]}
+                           for s in sweep[:5]],
+            "sweep_worst": round(sweep[-1][0], 1)}
 
 
 def bench_attention(ctx, reps=96):
@@ -519,7 +562,8 @@ def main():
     step_bytes = gu_bytes + dn_bytes
     value = step_bytes * args.steps / wall / 1e9
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-    gemv_gbs, gemv_us = bench_gemv(ctx)
+    gemv_gbs, gemv_us, gemv_fit = bench_gemv(ctx)
+    ceiling = bench_read_ceiling(ctx)
     attn = bench_attention(ctx)
     head = bench_lm_head(ctx)
     gemv_bf16 = bench_gemv_bf16(ctx)
@@ -580,6 +624,8 @@ def main():
                                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                                  "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
                                                  "bytes": 10526720},
+                  "gemv_q4_k2048_size_fit": gemv_fit,
+                  "hbm_read_ceiling": ceiling,
                   "attention_640_slots": attn,
                   "lm_head_q8_argmax": head,
                   "gemv_bf16_8192x2048": gemv_bf16,

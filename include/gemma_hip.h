@@ -73,6 +73,16 @@ gh_status gh_buffer_read(gh_context *ctx, void *host_dst, const void *dev_src, s
 gh_status gh_buffer_copy(gh_context *ctx, void *dev_dst, const void *dev_src, size_t bytes);
 gh_status gh_buffer_fill_u32(gh_context *ctx, void *dev, uint32_t value, size_t count);
 
+/* HBM read-bandwidth probe (no reference counterpart; measurement only: the
+ * attainable read rate the GEMV streams are judged against).  Reads `bytes` of
+ * dev once with 16-byte loads, per_lane (1, 2, 4 or 8) loads in flight per
+ * lane, over `grid` workgroups of 256 threads (0: 4 per CU); contiguous = 0
+ * strides the grid over the whole buffer, 1 gives each workgroup its own
+ * contiguous share.  bytes must be a multiple of 16 * 256 * per_lane * grid.
+ * Writes one float per workgroup (the sum of what it read) to sums. */
+gh_status gh_read_probe(gh_context *ctx, const void *dev, size_t bytes, uint32_t per_lane,
+                        uint32_t contiguous, uint32_t grid, float *sums);
+
 /* ---- timing on the context stream (no reference counterpart: the reference
  * times with host clocks, src/model/bench.zig:14-21) ------------------------ */
 gh_status gh_event_create(gh_context *ctx, void **ev);

@@ -1050,50 +1050,6 @@ __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp
     stream_rows<F, TPR, GPL, D, NT, NORMED>(a, xp, M, K);
 }
 
-// ------------------------------------------------------------------------
-// Long rows split in two (plain x, single-sum formats Q4Fmt / Q8Fmt): virtual
-// row 2r + h is the h-th K half of row r (contiguous in memory), one team per
-// virtual row, one group per lane, so every lane holds exactly one item and
-// the whole matrix is in flight after one issue round.  The two half-sums of
-// a row (teams 2t and 2t + 1 of one workgroup) add in LDS at the end, first
-// half first.  Not persistent: the grid is ceil(2M / TEAMS) workgroups.
-// Requires (K / 128) even and K / 256 <= TPR.
-// ------------------------------------------------------------------------
-template <class F, int TPR, int NT>
-__device__ __forceinline__ void split_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
-                                           uint32_t K) {
-  extern __shared__ float lds[];
-  const uint32_t nb = K >> 5, ng = nb >> 2, ngh = ng >> 1;
-  float* xs = lds;
-  float* bsum = lds + ng * GROUP_STRIDE;
-  float* ext = bsum + nb;
-  constexpr uint32_t TEAMS = NT / TPR;
-  static_assert(TEAMS % 2 == 0 && TEAMS <= 64, "team pairs within the epilogue space");
-  const uint32_t lr = threadIdx.x % TPR, tw = threadIdx.x / TPR;
-  const uint32_t vrow = blockIdx.x * TEAMS + tw;
-  const uint32_t vr = vrow < 2 * M ? vrow : 2 * M - 1;  // tail teams load a duplicate
-  const uint32_t g = lr < ngh ? lr : ngh - 1;
-  const size_t off = (size_t)vr * (nb >> 1) * F::kBlockBytes + (size_t)g * F::kGroupBytes;
-  typename F::Item it;
-  constexpr uint32_t NS = NT >= 1024 ? 256 : NT / 2;
-  const bool late = threadIdx.x < NS;
-  if (!late) F::load(it, a, off);
-  if (late) stage_x<NS>(xp.x, K, xs, bsum);
-  __syncthreads();
-  if (late) F::load(it, a, off);
-  typename F::Acc acc;
-  F::init(acc);
-  const uint32_t gx = (vr & 1) * ngh + g;
-  F::fma(acc, it, xs + gx * GROUP_STRIDE, bsum + gx * 4, lr < ngh ? 1.0f : 0.0f);
-  const float v = team_sum<TPR>(acc.s);
-  if (lr == 0) ext[tw] = v;
-  __syncthreads();
-  if (threadIdx.x < TEAMS / 2) {
-    const uint32_t row = blockIdx.x * (TEAMS / 2) + threadIdx.x;
-    if (row < M) a.Y[row] = ext[2 * threadIdx.x] + ext[2 * threadIdx.x + 1];
-  }
-}
-
 // Kernel names: gh_<family>[n]_t<TPR>_g<GPL>_d<D>; the "n" variants carry the
 // normed x prologue (modes 1 and 2), the others stage x as given (mode 0)
 // and keep the prologue's registers out of the stream.  Weight and output

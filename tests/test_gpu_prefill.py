@@ -101,6 +101,32 @@ def test_prefill_gemm_row_range(gpu):
             assert_close(got[t], ref[t], what="prefill GEMM row %d" % t)
 
 
+def test_prefill_gemm_weight_scale_range(gpu):
+    # Q4 weights enter as two exact fp16 operands per block, (n - 8) times the
+    # 8-bit pieces of S d with S a power of two per weight row: rows whose
+    # blocks span 2^-24 .. 2^12 of each other, large and tiny rows, all-zero
+    # blocks and an all-zero row, against the fp64 product
+    T, N, K = 9, 64, 1024
+    rng = np.random.default_rng(5)
+    w = gh.synth_normal(N * K, 0, 350, 0.0, 0.02).reshape(N, K).astype(np.float64)
+    blocks = w.reshape(N, K // 32, 32)
+    blocks *= 2.0 ** rng.integers(-24, 13, size=(N, K // 32, 1))
+    blocks[1] *= 1e3
+    blocks[2] *= 1e-6
+    blocks[3, ::3] = 0.0
+    blocks[4] = 0.0
+    wq = nr.quantize_q4(nr.bf16_rne(w.astype(np.float32)))
+    deq = nr.dequant_q4(wq, K)
+    a = gh.synth_normal(T * K, 1, 351, 0.0, 1.0).reshape(T, K)
+    W, A, C = gpu.upload(wq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gemm(gh.QUANT_Q4, W, A, C, T, N, K)
+    got = C.read(np.float32, T * N).reshape(T, N)
+    ref = np.asarray(a, np.float64) @ deq.T
+    assert np.all(got[:, 4] == 0.0)
+    for n in (0, 1, 2, 3, 5, 63):  # each weight row against its own magnitude
+        assert_close(got[:, n], ref[:, n], what="prefill GEMM weight row %d" % n)
+
+
 @pytest.mark.parametrize("pair", [False, True])
 @pytest.mark.parametrize("split", ["1", "3", "200"])
 def test_prefill_split_k(gpu, monkeypatch, pair, split):

@@ -34,4 +34,11 @@ struct AttnArgs {
   const float* rope_tab;
   // layer gating: when non-null and *run == 0 the launch does nothing
   const uint32_t* run;
+  // batched prefill, gh_pf_qkv_rope4_k: the [q|k|v] rows as nplanes unsummed
+  // K-split planes of the QKV GEMM (plane p of token t at
+  // q_planes + p * plane_stride + t * q_stride), summed in plane order while
+  // loading; the roped q rows go to q.  nplanes 0: the rows are q itself.
+  const float* q_planes;
+  uint32_t nplanes;
+  uint64_t plane_stride;
 };

@@ -874,7 +874,9 @@ extern "C" __global__ __launch_bounds__(64) void gh_pf_qkv_rope_k(AttnArgs a,
 // Every job's row (4 floats per lane) loads before any is used, the RoPE
 // angles are computed once per wave rather than once per head, and each head
 // is normalised in registers, rotated through the wave's LDS row
-// (rope_lds), and stored: q in place, k and v into the caches at slots[t].
+// (rope_lds), and stored: q to a.q, k and v into the caches at slots[t].
+// With a.nplanes >= 1 the rows are the QKV GEMM's unsummed K-split planes,
+// added in plane order as they load (each plane's rows all in flight at once).
 #define PFR_JOBS 16  // jobs per wave: nq + 2 nkv <= 64
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs a,
                                                                       const uint32_t* clocks,
@@ -883,20 +885,33 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs 
   const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t clock = clocks[t], slot = slots[t];
   float* row = const_cast<float*>(a.q) + (size_t)t * a.q_stride;
+  const float* srow = a.nplanes ? a.q_planes + (size_t)t * a.q_stride : row;
   const uint32_t nq = a.nq, nkv = a.nkv, njobs = nq + 2 * nkv;
   const uint32_t per = (njobs + ATT_WAVES - 1) / ATT_WAVES;  // the same for every wave
   const size_t q_dim = (size_t)nq * 256, kv_dim = (size_t)nkv * 256;
-  auto src = [&](uint32_t j) -> const float* {
-    if (j < nq) return row + (size_t)j * 256;
-    if (j < nq + nkv) return row + q_dim + (size_t)(j - nq) * 256;
-    return (a.k_eq_v ? row + q_dim : row + q_dim + kv_dim) + (size_t)(j - nq - nkv) * 256;
+  auto src = [&](uint32_t j) -> size_t {  // offset of job j's row in a token row
+    if (j < nq) return (size_t)j * 256;
+    if (j < nq + nkv) return q_dim + (size_t)(j - nq) * 256;
+    return (a.k_eq_v ? q_dim : q_dim + kv_dim) + (size_t)(j - nq - nkv) * 256;
   };
   const uint32_t d0 = lane * 4;
   float4 v[PFR_JOBS];
 #pragma unroll
   for (int i = 0; i < PFR_JOBS; i++) {
     const uint32_t j = min(wave + ATT_WAVES * (uint32_t)i, njobs - 1);
-    v[i] = *reinterpret_cast<const float4*>(src(j) + d0);
+    v[i] = *reinterpret_cast<const float4*>(srow + src(j) + d0);
+  }
+  for (uint32_t p = 1; p < a.nplanes; p++) {  // uniform
+    const float* prow = srow + (size_t)p * a.plane_stride;
+    float4 w[PFR_JOBS];
+#pragma unroll
+    for (int i = 0; i < PFR_JOBS; i++) {
+      const uint32_t j = min(wave + ATT_WAVES * (uint32_t)i, njobs - 1);
+      w[i] = *reinterpret_cast<const float4*>(prow + src(j) + d0);
+    }
+#pragma unroll
+    for (int i = 0; i < PFR_JOBS; i++)
+      v[i] = make_float4(v[i].x + w[i].x, v[i].y + w[i].y, v[i].z + w[i].z, v[i].w + w[i].w);
   }
   const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);  // a missing norm weight
   const float4 wq = a.q_norm ? *reinterpret_cast<const float4*>(a.q_norm + d0) : one;

@@ -376,7 +376,12 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   // products of at least 128 tokens) when splitting K lifts it to that
   const uint32_t bn_big = pair ? 64 : 128;
   const uint32_t tiles_big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128);
-  const bool big_split = !pair && T >= 128 && tiles_big < cus && 4 * tiles_big >= cus &&
+  // A caller that takes unsummed planes also gets the split for a product
+  // whose large tiles give each CU only one workgroup (the QKV projection of
+  // 512 tokens: 256 tiles of 128x128, split in 2, measured 85 us against
+  // 112 us as 512 tiles of 128x64).
+  const bool big_split = !pair && T >= 128 && 4 * tiles_big >= cus &&
+                         (tiles_big < cus || (planes && tiles_big < 2 * cus)) &&
                          getenv("GH_PF_NO_BIG_SPLIT") == nullptr;
   const bool big = tiles_big >= cus || big_split;
   // a plain product whose 128x128 tiles give each CU only one workgroup (the

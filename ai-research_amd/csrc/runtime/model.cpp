@@ -1226,10 +1226,17 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
         (st = copy_words(m, m->at<float>(m->xprev) + (size_t)l * H, m->pf_x + (size_t)(T - 1) * H,
                          H)) != GH_OK)
       return st;
-    // 2. [q|k|v] rows of every token
+    // 2. [q|k|v] rows of every token.  With head_dim 256 the norm + RoPE
+    //    kernel below sums a K split's planes itself, so the GEMM may leave
+    //    them unsummed (and take the faster split shape of a long prompt).
     const uint16_t* xh = reinterpret_cast<const uint16_t*>(m->pf_xn);
+    const bool rope4 = L.head_dim == 256 && c.num_attention_heads + 2 * L.nkv <= 64;
+    const float* qkv_planes = m->pf_qkv;
+    uint32_t qkv_nz = 1;
     if ((st = gh::launch_prefill_gemm_split(ctx, m->mode, m->at<uint8_t>(L.qkv), nullptr, xh,
-                                            m->pf_rs, m->pf_qkv, T, L.qkv_rows, H)) != GH_OK)
+                                            m->pf_rs, m->pf_qkv, T, L.qkv_rows, H,
+                                            rope4 ? &qkv_planes : nullptr,
+                                            rope4 ? &qkv_nz : nullptr)) != GH_OK)
       return st;
     // 3. q/k norm + RoPE in place, K/V into the caches, then attention
     AttnArgs a{};
@@ -1253,13 +1260,15 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     a.q_stride = L.qkv_rows;
     a.active_stride = m->pf_stride;
     a.out_stride = L.q_dim;
+    a.q_planes = qkv_planes;
+    a.nplanes = qkv_nz;
+    a.plane_stride = (uint64_t)T * L.qkv_rows;
     {
       void* args[] = {&a, &clocks, &slots};
       // head_dim 256: one workgroup per token (angles once per wave); else one
       // wavefront per (head, token)
-      st = L.head_dim == 256 && a.nq + 2 * a.nkv <= 64
-               ? ctx->launch("gh_pf_qkv_rope4_k", dim3(T), dim3(256), 0, args)
-               : ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args);
+      st = rope4 ? ctx->launch("gh_pf_qkv_rope4_k", dim3(T), dim3(256), 0, args)
+                 : ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args);
       if (st != GH_OK) return st;
     }
     {

@@ -1036,10 +1036,17 @@ __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const 
   auto row_of = [&](uint32_t i) -> uint32_t { return team + (i / GPL) * nteams; };
   auto c0_of = [&](uint32_t i) -> uint32_t { return (i % GPL) * C * TPR + lr; };
   typename F::Item buf[D];
+  // first items: unconditional in the plain streams, as in stream_rows
   stream_start<NT, NORMED>(xp, K, xs, bsum, ext, [&]() {
 #pragma unroll
-    for (int d = 0; d < D; d++)
-      if (d < n_items) F::template load<TPR>(buf[d], a, row_of(d) * row_bytes, c0_of(d), nch);
+    for (int d = 0; d < D; d++) {
+      if constexpr (NORMED) {
+        if (d < n_items) F::template load<TPR>(buf[d], a, row_of(d) * row_bytes, c0_of(d), nch);
+      } else {
+        const uint32_t r = row_of(d) < M ? row_of(d) : M - 1;
+        F::template load<TPR>(buf[d], a, r * row_bytes, c0_of(d), nch);
+      }
+    }
   });
   typename F::Acc acc;
   F::init(acc);

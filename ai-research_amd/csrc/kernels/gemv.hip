@@ -1160,6 +1160,11 @@ GH_SHAPES(GH_PLAIN_Q, 1)
 GH_SHAPES(GH_PLAIN, 2)
 GH_BF16_SHAPES(GH_BF16_PLAIN)
 GH_WIDE(32, 4, 1) GH_WIDE(64, 2, 1) GH_WIDE(64, 4, 1)  // depth 2 at 1024 threads spills
+// bf16 rows of K >= 8192 (64 lanes x 2 or 4 items of 64 weights): 1024-thread
+// workgroups as for the quantized rows (3840 x 15360: a 61 KB x staging
+// otherwise leaves two 256-thread workgroups per CU)
+GH_STREAM_KERNEL_NT_Q(gh_gemv_bf16, Bf16Fmt, GH_P_W, GH_A_W, 64, 2, 1, false, 1024, _w)
+GH_STREAM_KERNEL_NT_Q(gh_gemv_bf16, Bf16Fmt, GH_P_W, GH_A_W, 64, 4, 1, false, 1024, _w)
 
 // The token from the n block partials of a fused argmax stream: the largest
 // value, the lowest row among equals (src/kernels.zig:164-174).  One block.

@@ -58,7 +58,8 @@ GemvCfg pick_gemv(const gh_context* ctx, uint32_t M, uint32_t K, bool q8, bool w
   if (const char* env = shape_env ? shape_env : getenv("GH_GEMV_CFG")) {
     int t = 0, g = 0, w = 0, d = 0, n = 256;
     const int got = sscanf(env, "%d,%d,%d,%d,%d", &t, &g, &w, &d, &n);
-    const bool built = !bf16 || ((t == 64 || g == 1) && d == 1 && n == 256);
+    const bool built = !bf16 || ((t == 64 || g == 1) && d == 1 &&
+                                 (n == 256 || (t == 64 && (g == 2 || g == 4))));
     if (got >= 4 && built && (t == 16 || t == 32 || t == 64) && (g == 1 || g == 2 || g == 4) &&
         !(t == 16 && g > 1) && w >= 1 && w <= 32 && (uint32_t)(t * g) >= ng && d >= 1 &&
         d <= 2 && (n == 256 || (n == 1024 && wide_ok && t * g >= 128 && d == 1))) {
@@ -94,7 +95,8 @@ namespace gh {
 gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
                        StreamShape* out) {
   // 1024-thread variants exist for the plain GEMVs (long rows)
-  const bool wide_ok = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0);
+  const bool wide_ok = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0 ||
+                                   strcmp(family, "gh_gemv_bf16") == 0);
   const bool bf16 = strstr(family, "bf16") != nullptr;
   GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, wide_ok, bf16);
   // a row team covers at most 64 lanes x 4 items (of 128 quantized or 64 bf16 weights)

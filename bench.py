@@ -575,11 +575,14 @@ def main():
     log("mlp %.1f GB/s, gate_up %.2f us, down %.2f us, gemv8192x2048 %.2f us"
         % (value, gu_ms * 1e3, dn_ms * 1e3, gemv_us))
 
-    traffic = None
+    # HBM bytes per launch from the committed counter passes
+    # (ai-research_amd/traffic.py; profiles/hbm_traffic_decode_kernels.md)
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        rec = json.load(open(tpath)).get("gh_gateup_q4")
-        traffic = rec["hbm_bytes"] if rec else None
+    trec = json.load(open(tpath)) if os.path.exists(tpath) else {}
+    tbytes = lambda k: trec[k]["hbm_bytes"] if k in trec else None  # noqa: E731
+    traffic = tbytes("gh_gateup_q4")
+    attn["S544"]["traffic"] = tbytes("attention_544")
+    head["traffic"] = tbytes("lm_head_q8")
 
     cpu = cpu1 = None
     if not args.no_cpu:
@@ -623,7 +626,9 @@ def main():
                   "gemv_q4_8192x2048_roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1),
                                                  "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                                  "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-                                                 "bytes": 10526720},
+                                                 "bytes": 10526720,
+                                                 "traffic": tbytes("gemv_q4_8192x2048")},
+                  "down_proj_traffic": tbytes("gh_gemv_q4"),
                   "gemv_q4_k2048_size_fit": gemv_fit,
                   "hbm_read_ceiling": ceiling,
                   "attention_640_slots": attn,

@@ -11,6 +11,17 @@ struct XPro {
   float* xout;
   float s, eps;
   uint32_t mode;
+  // mode 4 (a gated layer's input under quiescence, src/gpu/model_dispatch.zig:
+  // 45-101): A' = (x + RMSNorm(r) * wr) * s when the previous layer ran
+  // (pmode 1, or pmode 2 with *prun != 0), else A' = xa; the GEMV consumes
+  // RMSNorm(A') * w; workgroup 0 writes A' to xout (when it differs from xa),
+  // stores it as xprev and writes *run_out = mean((A' - xprev)^2) >= thr
+  const float* xa;
+  float* xprev;
+  const uint32_t* prun;
+  uint32_t* run_out;
+  uint32_t pmode;
+  float thr;
 };
 
 struct Q4Args {  // Q4Fmt::Args / Q8Fmt::Args

@@ -416,6 +416,141 @@ __device__ __forceinline__ void pro_finish(const XPro& p, uint32_t K, ProIn& in,
   __syncthreads();
 }
 
+// Mode 4: the gated layer's input and its gate (quiescence).  Each thread
+// loads its slices of x, r, wr, w and xa and the previous layer's run flag
+// up front; one block-wide reduction gives sum r^2, x^2, x q, q^2 and xa^2,
+// from which A' and its norm follow as in mode 2 (or A' = xa).  Workgroup 0
+// alone then reads xprev, reduces mean((A' - xprev)^2), writes the run flag
+// and stores A' as xprev, so no workgroup reads an xprev another writes.
+struct ProGIn {
+  ProIn p;
+  float4 va[PRO_U];
+  uint32_t prun;
+};
+
+template <int NT>
+__device__ __forceinline__ void pro_gate_load(const XPro& p, uint32_t K, ProGIn& in) {
+  const uint32_t n4 = K >> 2;
+  const float4* x = reinterpret_cast<const float4*>(p.x);
+  const float4* r = reinterpret_cast<const float4*>(p.r);
+  const float4* wr = reinterpret_cast<const float4*>(p.wr ? p.wr : p.r);
+  const float4* w = reinterpret_cast<const float4*>(p.w);
+  const float4* xa = reinterpret_cast<const float4*>(p.xa);
+  in.prun = p.pmode == 2u ? *p.prun : 1u;
+#pragma unroll
+  for (uint32_t u = 0; u < PRO_U; u++) {
+    uint32_t i = u * NT + threadIdx.x;
+    i = i < n4 ? i : n4 - 1;
+    in.p.vx[u] = x[i];
+    in.p.vr[u] = r[i];
+    in.p.vwr[u] = wr[i];
+    in.p.vw[u] = w[i];
+    in.va[u] = xa[i];
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void pro_gate_finish(const XPro& p, uint32_t K, ProGIn& in, float* xs,
+                                                float* bsum, float* ext) {
+  const uint32_t n4 = K >> 2;
+  const bool add = p.pmode == 1u || (p.pmode == 2u && in.prun != 0u);  // uniform
+  const bool has_wr = p.wr != nullptr;
+  float4* vx = in.p.vx;
+  const float4* vr = in.p.vr;
+  const float4* vwr = in.p.vwr;
+  const float4* vw = in.p.vw;
+  float t[5] = {0.f, 0.f, 0.f, 0.f, 0.f};  // sum r^2, x^2, x q, q^2, xa^2
+#pragma unroll
+  for (uint32_t u = 0; u < PRO_U; u++) {
+    if (u * NT + threadIdx.x < n4) {
+      const float r[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+      const float x[4] = {vx[u].x, vx[u].y, vx[u].z, vx[u].w};
+      const float w[4] = {vwr[u].x, vwr[u].y, vwr[u].z, vwr[u].w};
+      const float a[4] = {in.va[u].x, in.va[u].y, in.va[u].z, in.va[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float q = has_wr ? r[e] * w[e] : r[e];
+        t[0] += r[e] * r[e];
+        t[1] += x[e] * x[e];
+        t[2] += x[e] * q;
+        t[3] += q * q;
+        t[4] += a[e] * a[e];
+      }
+    }
+  }
+  block_sums<NT, 5>(t, ext);
+  float s2;
+  if (add) {
+    const float c = has_wr ? 1.0f / sqrtf(t[0] / (float)K + p.eps) : 1.0f;
+    const float pos = t[1] + c * c * t[3];
+    s2 = p.s * p.s * (pos + 2.0f * c * t[2]);
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++) {
+      float4 rv = vr[u];
+      if (has_wr) {
+        rv.x = rv.x * c * vwr[u].x;
+        rv.y = rv.y * c * vwr[u].y;
+        rv.z = rv.z * c * vwr[u].z;
+        rv.w = rv.w * c * vwr[u].w;
+      }
+      vx[u].x = (vx[u].x + rv.x) * p.s;
+      vx[u].y = (vx[u].y + rv.y) * p.s;
+      vx[u].z = (vx[u].z + rv.z) * p.s;
+      vx[u].w = (vx[u].w + rv.w) * p.s;
+    }
+    if (!(s2 > 1e-3f * p.s * p.s * pos)) {  // cancellation (uniform branch): reduce A'^2 itself
+      float d[1] = {0.f};
+#pragma unroll
+      for (uint32_t u = 0; u < PRO_U; u++)
+        if (u * NT + threadIdx.x < n4)
+          d[0] += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
+      block_sums<NT, 1>(d, ext + 5 * (NT / 64));
+      s2 = d[0];
+    }
+  } else {
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++) vx[u] = in.va[u];
+    s2 = t[4];
+  }
+  const float inv = 1.0f / sqrtf(s2 / (float)K + p.eps);
+#pragma unroll
+  for (uint32_t u = 0; u < PRO_U; u++) {
+    const uint32_t i = u * NT + threadIdx.x;
+    float sb = 0.f;
+    if (i < n4) {
+      const uint32_t e = i << 2, g = e >> 7, o = e & 127;
+      float4 v;
+      v.x = vx[u].x * inv * vw[u].x;
+      v.y = vx[u].y * inv * vw[u].y;
+      v.z = vx[u].z * inv * vw[u].z;
+      v.w = vx[u].w * inv * vw[u].w;
+      *reinterpret_cast<float4*>(xs + g * GROUP_STRIDE + o) = v;
+      sb = (v.x + v.y) + (v.z + v.w);
+    }
+    sb = sum8(sb);
+    if (i < n4 && (i & 7) == 0) bsum[i >> 3] = sb;
+  }
+  if (blockIdx.x == 0) {  // the gate (uniform per workgroup)
+    float4* xprev = reinterpret_cast<float4*>(p.xprev);
+    float d[1] = {0.f};
+#pragma unroll
+    for (uint32_t u = 0; u < PRO_U; u++) {
+      const uint32_t i = u * NT + threadIdx.x;
+      if (i < n4) {
+        const float4 pv = xprev[i];
+        const float a = vx[u].x - pv.x, b = vx[u].y - pv.y, e = vx[u].z - pv.z,
+                    f = vx[u].w - pv.w;
+        d[0] += a * a + b * b + e * e + f * f;
+        xprev[i] = vx[u];
+        if (add) reinterpret_cast<float4*>(p.xout)[i] = vx[u];
+      }
+    }
+    block_sums<NT, 1>(d, ext + 6 * (NT / 64));
+    if (threadIdx.x == 0) *p.run_out = (d[0] / (float)K >= p.thr || p.thr <= 0.0f) ? 1u : 0u;
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------------------------------
 // Weight formats: one "item" = one 4-block group of one row.
 // init() sets the whole accumulator, zero() resets it for the next row,
@@ -902,7 +1037,7 @@ constexpr bool interleaved(long) { return false; }
 // block-wide prologue and epilogue.
 // ------------------------------------------------------------------------
 // The prologue of a stream and its first weight loads (issue()).
-template <int NT, bool NORMED, class Issue>
+template <int NT, int PRO, class Issue>
 __device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* xs, float* bsum,
                                              float* ext, Issue issue) {
   // A wave's loads complete in order, so x loads issued behind its own
@@ -910,7 +1045,12 @@ __device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* 
   // loads).  Every thread therefore issues its prologue loads (x, and for
   // the normed streams r and the norm weights) first, then its weight loads,
   // then runs the prologue (whose reductions need every thread).
-  if constexpr (NORMED) {
+  if constexpr (PRO == 2) {
+    ProGIn pin;
+    pro_gate_load<NT>(xp, K, pin);
+    issue();
+    pro_gate_finish<NT>(xp, K, pin, xs, bsum, ext);
+  } else if constexpr (PRO == 1) {
     ProIn pin;
     pro_load<NT>(xp, K, pin);
     issue();
@@ -937,7 +1077,7 @@ __device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* 
   }
 }
 
-template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
+template <class F, int TPR, int GPL, int D, int NT, int PRO>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
                                             uint32_t K) {
   extern __shared__ float lds[];
@@ -981,10 +1121,10 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
   // overlaps the first weight loads, yet they measured slower (15360 x 3840
   // gate+up 15.5 against 15.2 us, decode 370 against 372.5 tok/s).
   typename F::Item buf[D];
-  stream_start<NT, NORMED>(xp, K, xs, bsum, ext, [&]() {
+  stream_start<NT, PRO>(xp, K, xs, bsum, ext, [&]() {
 #pragma unroll
     for (int d = 0; d < D; d++) {
-      if constexpr (NORMED) {
+      if constexpr (PRO != 0) {
         if (d < n_items) F::load(buf[d], a, offset_of(d));
       } else {
         F::load(buf[d], a, offset_in(d));
@@ -1019,7 +1159,7 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 // team reads whole cache lines per load instruction.  GPL items per row per
 // lane, TPR GPL kChunks >= K / 8.
 // ------------------------------------------------------------------------
-template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
+template <class F, int TPR, int GPL, int D, int NT, int PRO>
 __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const XPro& xp,
                                                uint32_t M, uint32_t K) {
   extern __shared__ float lds[];
@@ -1037,10 +1177,10 @@ __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const 
   auto c0_of = [&](uint32_t i) -> uint32_t { return (i % GPL) * C * TPR + lr; };
   typename F::Item buf[D];
   // first items: unconditional in the plain streams, as in stream_rows
-  stream_start<NT, NORMED>(xp, K, xs, bsum, ext, [&]() {
+  stream_start<NT, PRO>(xp, K, xs, bsum, ext, [&]() {
 #pragma unroll
     for (int d = 0; d < D; d++) {
-      if constexpr (NORMED) {
+      if constexpr (PRO != 0) {
         if (d < n_items) F::template load<TPR>(buf[d], a, row_of(d) * row_bytes, c0_of(d), nch);
       } else {
         const uint32_t r = row_of(d) < M ? row_of(d) : M - 1;
@@ -1069,18 +1209,19 @@ __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const 
   F::template block_end<NT>(acc, a, ext);
 }
 
-template <class F, int TPR, int GPL, int D, int NT, bool NORMED>
+template <class F, int TPR, int GPL, int D, int NT, int PRO>
 __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp, uint32_t M,
                                        uint32_t K) {
   if constexpr (interleaved<F>(0))
-    stream_rows_il<F, TPR, GPL, D, NT, NORMED>(a, xp, M, K);
+    stream_rows_il<F, TPR, GPL, D, NT, PRO>(a, xp, M, K);
   else
-    stream_rows<F, TPR, GPL, D, NT, NORMED>(a, xp, M, K);
+    stream_rows<F, TPR, GPL, D, NT, PRO>(a, xp, M, K);
 }
 
-// Kernel names: gh_<family>[n]_t<TPR>_g<GPL>_d<D>; the "n" variants carry the
-// normed x prologue (modes 1 and 2), the others stage x as given (mode 0)
-// and keep the prologue's registers out of the stream.  Weight and output
+// Kernel names: gh_<family>[n|g]_t<TPR>_g<GPL>_d<D>; the "n" variants carry
+// the normed x prologue (modes 1 and 2, PRO = 1), the "g" variants a gated
+// layer's input and gate (mode 4, PRO = 2), the others stage x as given
+// (mode 0) and keep the prologue's registers out of the stream.  Weight and output
 // pointers are separate kernel parameters: loaded out of a by-value struct
 // parameter they lose the kernel-argument address-space and alignment facts,
 // and the stream then needs ~100 more VGPRs (220 vs 126 for the Q4 d3 form).
@@ -1088,22 +1229,22 @@ __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp
 // launch these; they take the layer's run flag and do nothing when it is 0.
 // The ungated kernels carry no gating code at all: even a null-pointer test
 // at entry measured +0.3 us per launch.
-#define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)        \
+#define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, NT, SUFFIX)        \
   extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX(     \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                               \
-    stream<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
+    stream<FMT, T, G, D, NT, PRO>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
   }
-#define GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)      \
-  GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, NT, SUFFIX)              \
+#define GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, NT, SUFFIX)      \
+  GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, NT, SUFFIX)              \
   extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX##_q( \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K, const uint32_t* run) {          \
     if (*run == 0u) return;                                                               \
-    stream<FMT, T, G, D, NT, NORMED>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
+    stream<FMT, T, G, D, NT, PRO>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
   }
-#define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED) \
-  GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, 256, )
-#define GH_STREAM_KERNEL_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED) \
-  GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, NORMED, 256, )
+#define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, PRO) \
+  GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, 256, )
+#define GH_STREAM_KERNEL_Q(NAME, FMT, PARAMS, ARGS, T, G, D, PRO) \
+  GH_STREAM_KERNEL_NT_Q(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, 256, )
 #define GH_UNPAREN(...) __VA_ARGS__
 
 #define GH_P_W (const uint8_t* W, float* Y)
@@ -1155,6 +1296,14 @@ __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp
 GH_SHAPES(GH_NORMED_Q, 1)
 GH_SHAPES(GH_NORMED, 2)
 GH_BF16_SHAPES(GH_BF16_NORMED)
+// The first projection of a gated layer (QKV) with the gate in its prologue
+// (mode 4, PRO = 2): "g" variants, depth 1, no run-flag test at entry
+#define GH_GATED_K(T, G, D)                                          \
+  GH_STREAM_KERNEL(gh_gemv_q4g, Q4Fmt, GH_P_W, GH_A_W, T, G, D, 2)   \
+  GH_STREAM_KERNEL(gh_gemv_q8g, Q8Fmt, GH_P_W, GH_A_W, T, G, D, 2)
+#define GH_GATED_BF16_K(T, G, D) GH_STREAM_KERNEL(gh_gemv_bf16g, Bf16Fmt, GH_P_W, GH_A_W, T, G, D, 2)
+GH_SHAPES(GH_GATED_K, 1)
+GH_BF16_SHAPES(GH_GATED_BF16_K)
 #else
 GH_SHAPES(GH_PLAIN_Q, 1)
 GH_SHAPES(GH_PLAIN, 2)

@@ -92,11 +92,12 @@ gh_status check_gemv(const gh_context* ctx, const void* W, const float* X, const
 
 namespace gh {
 
-gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
-                       StreamShape* out) {
+gh_status stream_shape(gh_context* ctx, const char* family, const char* var, uint32_t M,
+                       uint32_t K, StreamShape* out) {
   // 1024-thread variants exist for the plain GEMVs (long rows)
-  const bool wide_ok = !normed && (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0 ||
-                                   strcmp(family, "gh_gemv_bf16") == 0);
+  const bool wide_ok = var[0] == '\0' &&
+                       (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0 ||
+                        strcmp(family, "gh_gemv_bf16") == 0);
   const bool bf16 = strstr(family, "bf16") != nullptr;
   GemvCfg c = pick_gemv(ctx, M, K, strstr(family, "q8") != nullptr, wide_ok, bf16);
   // a row team covers at most 64 lanes x 4 items (of 128 quantized or 64 bf16 weights)
@@ -105,7 +106,7 @@ gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_
                                         std::to_string(bf16 ? 16384 : 32768) + " weights");
   out->lds = x_lds_bytes(K) + 256;  // + the prologue/epilogue scratch (64 floats)
   if (out->lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": K too large");
-  out->name = std::string(family) + (normed ? "n" : "") + "_t" + std::to_string(c.tpr) + "_g" +
+  out->name = std::string(family) + var + "_t" + std::to_string(c.tpr) + "_g" +
               std::to_string(c.gpl) + "_d" + std::to_string(c.depth) + (c.nt == 1024 ? "_w" : "");
   out->nt = (unsigned)c.nt;
   // A persistent grid larger than what the CUs hold at once would run its
@@ -131,8 +132,14 @@ gh_status launch_stream(gh_context* ctx, const char* family, std::vector<void*> 
                         const XPro& xp, uint32_t M, uint32_t K, const uint32_t* run) {
   if (xp.mode != 0 && K > 4u * 4u * 256u)  // PRO_U float4 per thread of 256
     return fail(GH_ERR_UNSUPPORTED, std::string(family) + ": normed prologue needs K <= 4096");
+  if (xp.mode == 4) {  // a gated layer's first projection computes the gate itself
+    if (run) return fail(GH_ERR_INVALID, std::string(family) + ": mode 4 takes no run flag");
+    if (!xp.x || !xp.r || !xp.w || !xp.xa || !xp.xout || !xp.xprev || !xp.run_out ||
+        (xp.pmode == 2 && !xp.prun) || xp.pmode > 2)
+      return fail(GH_ERR_INVALID, std::string(family) + ": mode-4 prologue inputs");
+  }
   StreamShape sh;
-  gh_status st = stream_shape(ctx, family, xp.mode != 0, M, K, &sh);
+  gh_status st = stream_shape(ctx, family, xp.mode == 4 ? "g" : xp.mode != 0 ? "n" : "", M, K, &sh);
   if (st != GH_OK) return st;
   XPro xpc = xp;
   std::vector<void*> args = std::move(fmt_params);

@@ -84,6 +84,9 @@ struct gh_model {
   // GH_EAGER_DECODE=1 (read at init): each token launches its kernels
   // directly instead of replaying the recorded graph (for kernel tracing).
   bool eager = false;
+  // GH_QGATE_KERNEL=1 (read at init): gated layers start with the separate
+  // gh_qgate_k launch instead of gating in their QKV stream's prologue
+  bool qgate_kernel = false;
   // layer gating (quiescence): layers >= num_layers / 3 are gated when on
   bool q_on = false;
   float q_thr = 0.f;
@@ -344,6 +347,7 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     const Layer& L = m->layers[l];
     const bool gated = l >= dense_limit;
     const uint32_t* run = gated ? flags + l : nullptr;
+    XPro gp{};  // mode 4: the gate in the QKV prologue
     if (gated) {
       uint32_t prev_mode;
       const Layer* P = l > 0 ? &m->layers[l - 1] : nullptr;
@@ -368,18 +372,38 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
       float* A = m->at<float>(bufA);
       float* xp = m->at<float>(m->xprev) + (size_t)l * H;
       uint32_t* ro = const_cast<uint32_t*>(flags) + l;
-      uint32_t Hh = H, one = 1;
-      float eps = c.rms_norm_eps, th = thr;
-      void* args[] = {&xmid, &mo, const_cast<float**>(&wpost), &sc, &prev_mode,
-                      const_cast<uint32_t**>(&prun), &A, &xp, &th, &ro, &Hh, &eps, &one};
-      if ((st = ctx->launch("gh_qgate_k", dim3(1), dim3(1024), 0, args)) != GH_OK) return st;
-      if (m->trace_on && (st = copy_words(m, m->trace + (size_t)l * H, A, H)) != GH_OK) return st;
+      if (m->qgate_kernel) {
+        uint32_t Hh = H, one = 1;
+        float eps = c.rms_norm_eps, th = thr;
+        void* args[] = {&xmid, &mo, const_cast<float**>(&wpost), &sc, &prev_mode,
+                        const_cast<uint32_t**>(&prun), &A, &xp, &th, &ro, &Hh, &eps, &one};
+        if ((st = ctx->launch("gh_qgate_k", dim3(1), dim3(1024), 0, args)) != GH_OK) return st;
+        if (m->trace_on && (st = copy_words(m, m->trace + (size_t)l * H, A, H)) != GH_OK)
+          return st;
+      } else {  // the gate runs in the QKV stream's prologue (mode 4)
+        gp.x = xmid;
+        gp.r = mo;
+        gp.wr = wpost;
+        gp.s = sc;
+        gp.xa = A;
+        gp.xout = A;
+        gp.xprev = xp;
+        gp.prun = prun;
+        gp.run_out = ro;
+        gp.pmode = prev_mode;
+        gp.thr = thr;
+        gp.mode = 4;
+      }
     }
     // 1. [q|k|v] = W_qkv . norm(x)  (layer 0: RMSNorm; later: post-FFN add + norm)
     XPro p{};
     p.eps = c.rms_norm_eps;
     p.w = m->at<float>(L.input_norm);
-    if (gated) {
+    if (gated && gp.mode == 4) {
+      p = gp;
+      p.eps = c.rms_norm_eps;
+      p.w = m->at<float>(L.input_norm);
+    } else if (gated) {
       p.x = m->at<float>(bufA);
       p.mode = 1;
     } else if (l == 0) {
@@ -396,7 +420,12 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
       std::swap(xcur, xoth);
     }
     Q4Args qa{m->at<uint8_t>(L.qkv), m->at<float>(m->qkv_out)};
-    if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H, run)) != GH_OK) return st;
+    if ((st = gh::launch_stream(ctx, gemv, &qa, p, L.qkv_rows, H, p.mode == 4 ? nullptr : run)) !=
+        GH_OK)
+      return st;
+    if (m->trace_on && p.mode == 4 &&
+        (st = copy_words(m, m->trace + (size_t)l * H, m->at<float>(bufA), H)) != GH_OK)
+      return st;
     if (m->trace_on && l > 0 && !gated &&
         (st = copy_words(m, m->trace + (size_t)l * H, m->at<float>(xcur), H)) != GH_OK)
       return st;
@@ -528,6 +557,8 @@ gh_status record_graphs(gh_model* m) {
 gh_status finish_init(gh_model* m, gh_model** out) {
   const char* eager = getenv("GH_EAGER_DECODE");
   m->eager = eager && eager[0] == '1';
+  const char* qk = getenv("GH_QGATE_KERNEL");
+  m->qgate_kernel = qk && qk[0] == '1';
   gh_status st = reset_gates(m);
   if (st == GH_OK) st = record_graphs(m);
   if (st != GH_OK) {

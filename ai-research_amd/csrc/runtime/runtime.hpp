@@ -79,8 +79,14 @@ struct StreamShape {
   std::string name;
   unsigned grid = 0, lds = 0, nt = 256;
 };
-gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M, uint32_t K,
-                       StreamShape* out);
+// var: "" x as given, "n" normed prologue (modes 1, 2), "g" a gated layer's
+// input and gate (mode 4)
+gh_status stream_shape(gh_context* ctx, const char* family, const char* var, uint32_t M,
+                       uint32_t K, StreamShape* out);
+inline gh_status stream_shape(gh_context* ctx, const char* family, bool normed, uint32_t M,
+                              uint32_t K, StreamShape* out) {
+  return stream_shape(ctx, family, normed ? "n" : "", M, K, out);
+}
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots);
 // Argument checks and the launch block of the fused q/k norm + RoPE + cache
 // write + split-K attention (gh_qkv_rope_attn and its allocation-free

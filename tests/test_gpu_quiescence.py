@@ -52,10 +52,11 @@ def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4):
     return out, layers
 
 
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_NONE])
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 def test_quiescence_gating_matches_oracle(gpu, mode):
-    # mode none: bf16 layers, the gated bf16 streams, and a prompt that goes
-    # token by token (its last token with every gate open)
+    # every weight mode's gated QKV stream (the gate in its prologue); mode
+    # none: bf16 layers, the gated bf16 streams, and a prompt that goes token
+    # by token (its last token with every gate open)
     cfg = _cfg()
     m = gh.Model(gpu, cfg, mode=mode, seed=21)
     try:

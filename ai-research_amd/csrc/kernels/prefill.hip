@@ -36,6 +36,7 @@
 #include <stdint.h>
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define PF_NT 256
@@ -47,6 +48,7 @@ typedef const uint32_t __attribute__((address_space(1)))* gword_ptr;
 struct Q4W {  // src/quant.zig:55-90: {f32 d, 4 words of nibbles}
   static constexpr uint32_t kBlockBytes = 20;
   static constexpr int kWords = 3;
+  static constexpr bool kBf16 = false;
   // half h (elements 16h .. 16h+15) of a block: scale and its 16 values
   __device__ static void load(const uint8_t* blk, uint32_t h, uint32_t* w) {
     gword_ptr p = (gword_ptr)(blk);
@@ -75,6 +77,7 @@ struct Q4W {  // src/quant.zig:55-90: {f32 d, 4 words of nibbles}
 struct Q8W {  // src/quant.zig:20-51: {f32 d, 8 words of int8}
   static constexpr uint32_t kBlockBytes = 36;
   static constexpr int kWords = 5;
+  static constexpr bool kBf16 = false;
   __device__ static void load(const uint8_t* blk, uint32_t h, uint32_t* w) {
     gword_ptr p = (gword_ptr)(blk);
     w[0] = p[0];
@@ -91,6 +94,29 @@ struct Q8W {  // src/quant.zig:20-51: {f32 d, 8 words of int8}
                       (_Float16)(int)(int8_t)((w[1 + k] >> (8 * n + 8)) & 0xFFu)};
         out[2 * k + n / 2] = __builtin_bit_cast(uint32_t, v);
       }
+  }
+};
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef const u32x4_t __attribute__((address_space(1)))* gvec_ptr;
+
+// bf16 rows as stored (mode none, the reference's --gpu weights): 32 bf16 of
+// a row per K step go to the stage as they are and feed the bf16 MFMA
+// directly; there is no unpacking and no block scale (kBf16).
+struct Bf16W {
+  static constexpr uint32_t kBlockBytes = 64;
+  static constexpr int kWords = 8;
+  static constexpr bool kBf16 = true;
+  // half h (elements 16h .. 16h+15) of a 32-element segment: 8 words
+  __device__ static void load(const uint8_t* blk, uint32_t h, uint32_t* w) {
+    gvec_ptr p = (gvec_ptr)(blk + 32 * h);
+    const u32x4_t a = p[0], b = p[1];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  }
+  __device__ static void ints(const uint32_t* w, uint32_t* out) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) out[k] = w[k];
   }
 };
 
@@ -210,7 +236,8 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
         F::ints(rb[i], v);
         *reinterpret_cast<u32x4*>(&Bs[sb][b_at(lr, 2 * (hb % 2))]) = u32x4{v[0], v[1], v[2], v[3]};
         *reinterpret_cast<u32x4*>(&Bs[sb][b_at(lr, 2 * (hb % 2) + 1)]) = u32x4{v[4], v[5], v[6], v[7]};
-        if (hb % 2 == 0) Ds[sb][lr * KB + kq] = step * KB + kq < nb ? __uint_as_float(rb[i][0]) : 0.f;
+        if constexpr (!F::kBf16)
+          if (hb % 2 == 0) Ds[sb][lr * KB + kq] = step * KB + kq < nb ? __uint_as_float(rb[i][0]) : 0.f;
       }
     }
   };
@@ -254,6 +281,22 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
           const uint32_t brow = q * BN + wn + 32 * j + lane % 32;
           const half8 b0 = *reinterpret_cast<const half8*>(&Bs[cb][b_at(brow, lane / 32)]);
           const half8 b1 = *reinterpret_cast<const half8*>(&Bs[cb][b_at(brow, 2 + lane / 32)]);
+          if constexpr (F::kBf16) {
+            // exact bf16 weights and bf16 activation halves: every product
+            // accumulates straight into the tile (one block per step, so no
+            // step lies past K)
+            const bf16x8 c0 = __builtin_bit_cast(bf16x8, b0), c1 = __builtin_bit_cast(bf16x8, b1);
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+              f32x16 t = acc[q][i][j];
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[0][i]), c0, t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al[0][i]), c0, t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ah[1][i]), c1, t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, al[1][i]), c1, t, 0, 0, 0);
+              acc[q][i][j] = t;
+            }
+            continue;
+          }
           const float d = Ds[cb][brow * KB + kq];
 #pragma unroll
           for (int i = 0; i < TM; i++) {
@@ -338,6 +381,14 @@ GH_GEMM_ALL
 // all of K one block per step, and that serial chain, not bandwidth, sets the
 // time), and the large plain tile for the narrow products of a long prompt
 // (o and down, N = 3840), which otherwise fall back to the small tile.
+GH_GEMM(gh_pf_gemm_bf16_m128_n128, Bf16W, 128, 128, 1, false, )
+GH_GEMM(gh_pf_gemm_bf16_m128_n64, Bf16W, 128, 64, 1, false, )
+GH_GEMM(gh_pf_gemm_bf16_m64_n64, Bf16W, 64, 64, 1, false, )
+GH_GEMM_PAIR(gh_pf_gateup_bf16_m128_n64, Bf16W, 128, 64, 1, false, )
+GH_GEMM_PAIR(gh_pf_gateup_bf16_m64_n64, Bf16W, 64, 64, 1, false, )
+GH_GEMM(gh_pf_gemm_bf16_m64_n64, Bf16W, 64, 64, 1, true, _s)
+GH_GEMM(gh_pf_gemm_bf16_m128_n128, Bf16W, 128, 128, 1, true, _s)
+GH_GEMM_PAIR(gh_pf_gateup_bf16_m64_n64, Bf16W, 64, 64, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, 1, true, _s)
@@ -363,14 +414,36 @@ __device__ __forceinline__ float row_scale(float m, float* inv) {
 #define PF_HALVES_G 2  // 8-element groups per thread
 #define PF_HALVES_K (8 * PF_HALVES_NT * PF_HALVES_G)
 
+// Round-to-nearest-even bf16 bits of a finite float.
+__device__ __forceinline__ uint32_t pf_bf16_bits(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
 // hi = fp16(x), lo = fp16(x - hi) of one 8-element group, stored in the ax
 // layout at dst (16-byte aligned): the group's hi halves, and 32 halves on its
-// lo halves, each as one 16-byte store (in the Q4 K order with perm).
-__device__ __forceinline__ void pf_store_group(const float (&x)[8], bool perm, _Float16* dst) {
+// lo halves, each as one 16-byte store.  fmt 0: fp16 in K order; 1: fp16 in
+// the Q4 unpacking's K order; 2: bf16 halves (hi = bf16(x), lo = bf16(x - hi),
+// about 16 significant bits) in K order, for the bf16 weights' MFMA.
+__device__ __forceinline__ void pf_store_group(const float (&x)[8], uint32_t fmt, _Float16* dst) {
   half8 hi, lo;
+  if (fmt == 2u) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+      const uint32_t h0 = pf_bf16_bits(x[k]), h1 = pf_bf16_bits(x[k + 1]);
+      const uint32_t l0 = pf_bf16_bits(x[k] - __uint_as_float(h0 << 16));
+      const uint32_t l1 = pf_bf16_bits(x[k + 1] - __uint_as_float(h1 << 16));
+      hw[k / 2] = h0 | (h1 << 16);
+      lw[k / 2] = l0 | (l1 << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<u32x4*>(dst + 32) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 8; k++) {
-    const int p = perm ? ((k & 3) << 1) | (k >> 2) : k;
+    const int p = fmt == 1u ? ((k & 3) << 1) | (k >> 2) : k;
     const _Float16 h = (_Float16)x[k];
     hi[p] = h;
     lo[p] = (_Float16)(x[k] - (float)h);
@@ -412,7 +485,7 @@ extern "C" __global__ __launch_bounds__(PF_HALVES_NT) void gh_pf_halves_k(
     if (g < n8) {
       const float x[8] = {v[u][0].x * inv, v[u][0].y * inv, v[u][0].z * inv, v[u][0].w * inv,
                           v[u][1].x * inv, v[u][1].y * inv, v[u][1].z * inv, v[u][1].w * inv};
-      pf_store_group(x, perm != 0, Ax + (size_t)t * 2 * K + pf_ax_pos(8 * g, false));
+      pf_store_group(x, perm, Ax + (size_t)t * 2 * K + pf_ax_pos(8 * g, false));
     }
   }
   if (tid == 0) rs[t] = sc;
@@ -544,7 +617,7 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     float y[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) y[k] = v[k] * sinv;
-    pf_store_group(y, perm != 0, Xa + (size_t)t * 2 * H + pf_ax_pos(e0, false));
+    pf_store_group(y, perm, Xa + (size_t)t * 2 * H + pf_ax_pos(e0, false));
   }
   if (tid == 0) rs[t] = sc;
 }

@@ -369,15 +369,18 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                     const void* W1, const void* Ax, const float* rs, float* C,
                                     uint32_t T, uint32_t N, uint32_t K, const float** planes,
                                     uint32_t* nplanes) {
-  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8)
-    return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4 or Q8");
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8 && mode != GH_QUANT_NONE)
+    return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4, Q8 or NONE (bf16)");
   if (!W0 || !Ax || !rs || !C || T == 0 || N == 0 || K == 0)
     return fail(GH_ERR_INVALID, "prefill GEMM: null pointer or zero size");
   if (K % 32 != 0) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K must be a multiple of 32");
   if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
-  if ((reinterpret_cast<uintptr_t>(Ax) & 15) || (reinterpret_cast<uintptr_t>(W0) & 3) ||
-      (W1 && (reinterpret_cast<uintptr_t>(W1) & 3)))
-    return fail(GH_ERR_INVALID, "prefill GEMM: A halves must be 16-byte and W 4-byte aligned");
+  // bf16 rows are read 16 bytes at a time, quantized blocks 4 bytes at a time
+  const uintptr_t walign = mode == GH_QUANT_NONE ? 15 : 3;
+  if ((reinterpret_cast<uintptr_t>(Ax) & 15) || (reinterpret_cast<uintptr_t>(W0) & walign) ||
+      (W1 && (reinterpret_cast<uintptr_t>(W1) & walign)))
+    return fail(GH_ERR_INVALID, "prefill GEMM: A halves must be 16-byte aligned, W 4-byte "
+                                "(16-byte for bf16 rows)");
   const bool pair = W1 != nullptr;
   if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
   const uint32_t cus = (uint32_t)ctx->num_cus;
@@ -400,7 +403,8 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                       getenv("GH_PF_NO_N64") == nullptr;
   const uint32_t bm = big ? 128 : 64, bn = big ? (narrow ? 64 : bn_big) : 64;
   std::string name = std::string(pair ? "gh_pf_gateup_" : "gh_pf_gemm_") +
-                     (mode == GH_QUANT_Q8 ? "q8" : "q4") + (big ? "_m128_n" : "_m64_n") +
+                     (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
+                     (big ? "_m128_n" : "_m64_n") +
                      std::to_string(bn) + "_k1";
 
   dim3 grid((N + bn - 1) / bn, (T + bm - 1) / bm);
@@ -456,6 +460,13 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   if (!A || T == 0 || K == 0 || K % 32 != 0) return fail(GH_ERR_INVALID, "prefill GEMM: bad A");
   if (K > 16384) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: K above 16384");
   if (reinterpret_cast<uintptr_t>(A) & 15) return fail(GH_ERR_INVALID, "prefill GEMM: A must be 16-byte aligned");
+  // the weight checks of the GEMM itself, before the halves are made
+  if (mode != GH_QUANT_Q4 && mode != GH_QUANT_Q8 && mode != GH_QUANT_NONE)
+    return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: mode must be Q4, Q8 or NONE (bf16)");
+  const uintptr_t walign = mode == GH_QUANT_NONE ? 15 : 3;
+  if (!W0 || (reinterpret_cast<uintptr_t>(W0) & walign) ||
+      (W1 && (reinterpret_cast<uintptr_t>(W1) & walign)))
+    return fail(GH_ERR_INVALID, "prefill GEMM: W null or misaligned (4 bytes; 16 for bf16 rows)");
   const size_t ax_bytes = (size_t)T * K * 4;  // 2 K halves per row
   gh_status st = ctx->ensure_zeroed(&ctx->half_scratch, &ctx->half_scratch_bytes,
                                     ax_bytes + (size_t)T * sizeof(float));
@@ -463,8 +474,8 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   char* hb = static_cast<char*>(ctx->half_scratch);
   void* Ax = hb;
   float* rs = reinterpret_cast<float*>(hb + ax_bytes);
-  uint32_t perm = mode == GH_QUANT_Q4 ? 1u : 0u;  // K order of the Q4 unpacking
-  void* args[] = {const_cast<float**>(&A), &Ax, &rs, &K, &perm};
+  uint32_t fmt = gh::pf_halves_format(mode);
+  void* args[] = {const_cast<float**>(&A), &Ax, &rs, &K, &fmt};
   if ((st = ctx->launch("gh_pf_halves_k", dim3(T), dim3(1024), 0, args)) != GH_OK) return st;
   return launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes);
 }

@@ -1026,20 +1026,6 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     for (uint32_t t = 0; t < T; t++)
       if (slot_idx[t] != gh_ring_slot_index(m->ring, clocks[t]))
         return fail(GH_ERR_INVALID, "gh_model_prefill: a slot is not the ring's slot for its clock");
-  if (m->mode == GH_QUANT_NONE) {
-    // bf16 layers prefill token by token through the decode graphs, as the
-    // reference prefills every mode (src/interactive.zig:33-37); the batched
-    // matrix-core prefill takes Q4_0 / Q8_0 rows
-    uint32_t tok = 0;
-    for (uint32_t t = 0; t < T; t++) {
-      gh_status ts = forward_token(m, x + (size_t)t * c.hidden_size, want_logits && t + 1 == T,
-                                   clocks[t], slot_idx[t], active + (size_t)t * active_stride,
-                                   n_active[t], &tok, true);
-      if (ts != GH_OK) return ts;
-    }
-    if (want_logits) *out_token = tok;
-    return GH_OK;
-  }
   gh_status st = ensure_prefill(m, T, active_stride);
   if (st != GH_OK) return st;
   hipStream_t s = m->ctx->stream;
@@ -1221,7 +1207,7 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   // the normed rows as the GEMM's A operand: fp16 hi/lo halves ([T][2H]) in pf_xn
   uint16_t* Xa = reinterpret_cast<uint16_t*>(m->pf_xn);
   float* rs = m->pf_rs;
-  uint32_t perm = m->mode == GH_QUANT_Q4 ? 1u : 0u;  // K order of the Q4 unpacking
+  uint32_t perm = gh::pf_halves_format(m->mode);  // the GEMM's A-operand format
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
                   &Xa, &rs, &H, &s, &eps, &mode, &perm, &rz};
   return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
@@ -1366,8 +1352,8 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     p.eps = c.rms_norm_eps;
     p.mode = 2;
     ArgmaxArgs aa{m->at<uint8_t>(m->lm_head), m->at<float>(m->logits), m->at<uint32_t>(m->amax)};
-    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token))) !=
-        GH_OK)
+    if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token),
+                                       m->mode == GH_QUANT_NONE)) != GH_OK)
       return st;
   }
   return GH_OK;

@@ -115,6 +115,12 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                     const void* W1, const void* Ax, const float* rs, float* C,
                                     uint32_t T, uint32_t N, uint32_t K,
                                     const float** planes = nullptr, uint32_t* nplanes = nullptr);
+// The A-operand halves a prefill GEMM of this weight mode reads (gh_pf_norm_k
+// and gh_pf_halves_k): 1 = fp16 in the Q4 unpacking's K order (Q4_0),
+// 0 = fp16 in K order (Q8_0), 2 = bf16 in K order (bf16 rows).
+inline uint32_t pf_halves_format(gh_quant_mode mode) {
+  return mode == GH_QUANT_Q4 ? 1u : mode == GH_QUANT_NONE ? 2u : 0u;
+}
 // Resolves the allocation-free entry point's device scratch for `device`
 // (noalloc.hip); called by gh_context_init with that device current.
 gh_status noalloc_setup(int device);

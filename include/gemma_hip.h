@@ -270,11 +270,13 @@ gh_status gh_argmax(gh_context *ctx, const float *logits, uint32_t *out_token, u
  * prefills token by token through its decode graph, src/interactive.zig:33-37,
  * src/gpu/model_dispatch.zig:144).  One projection of T prompt tokens on the
  * matrix cores: C[T][N] = A[T][K] . deq(W)[N][K]^T with A f32 row-major
- * (16-byte aligned) and W in the quant.zig row layout of mode (Q4 or Q8);
- * the weights enter exactly (integer values, f32 block scales applied to the
- * block sums), the activations as two fp16 halves of a / s with s a power of
- * two per row (no fp16 overflow), fp32 accumulation; K % 32 == 0 and
- * K <= 16384.  All pointers are device pointers. */
+ * (16-byte aligned) and W in the quant.zig row layout of mode (Q4 or Q8), or
+ * bf16 rows in mode GH_QUANT_NONE (16-byte aligned); the weights enter
+ * exactly (integer values with f32 block scales applied to the block sums,
+ * or the bf16 values), the activations as two fp16 halves of a / s with s a
+ * power of two per row (no fp16 overflow; bf16 halves for bf16 weights),
+ * fp32 accumulation; K % 32 == 0 and K <= 16384.  All pointers are device
+ * pointers. */
 gh_status gh_prefill_gemm(gh_context *ctx, gh_quant_mode mode, const void *W, const float *A,
                           float *C, uint32_t T, uint32_t N, uint32_t K);
 /* act[T][N] = gelu_tanh(A . deq(Wg)^T) * (A . deq(Wu)^T): the batched form of

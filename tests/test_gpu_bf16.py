@@ -147,9 +147,10 @@ def test_norm_gemv_argmax_bf16(gpu, V):
 
 
 def test_bf16_model_prompt_then_greedy(gpu):
-    # mode none end to end: a 12-token prompt through gh_model_prefill (token
-    # by token on the decode graphs, src/interactive.zig:33-37) and 6 greedy
+    # mode none end to end: a 12-token prompt through gh_model_prefill (the
+    # batched prefill with bf16 MFMA GEMMs on the bf16 rows) and 6 greedy
     # steps, against the oracle's sequential forward on the same bf16 rows
+    # (src/interactive.zig:33-37 prefills token by token)
     from model_ref import oracle_model
     from test_gpu_model import check_token, tiny_cfg
     cfg = tiny_cfg()

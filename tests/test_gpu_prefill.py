@@ -18,7 +18,10 @@ NT = min(16, os.cpu_count() or 1)
 
 
 def quantized(rows, cols, mode, seed):
+    """The device rows of mode (Q4_0, Q8_0, or bf16 as is) and their values in fp64."""
     w = nr.bf16_rne(gh.synth_normal(rows * cols, 0, seed, 0.0, 0.02).reshape(rows, cols))
+    if mode == gh.QUANT_NONE:
+        return w, nr.bf16_to_f32(w).astype(np.float64)
     wq = nr.quantize_q4(w) if mode == gh.QUANT_Q4 else nr.quantize_q8(w)
     deq = nr.dequant_q4(wq, cols) if mode == gh.QUANT_Q4 else nr.dequant_q8(wq, cols)
     return wq, deq
@@ -31,7 +34,7 @@ GEMM_SHAPES = [(1, 64, 128), (7, 96, 256), (64, 384, 3840), (130, 256, 512), (30
                (512, 3840, 1024), (512, 8192, 256)]
 
 
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 @pytest.mark.parametrize("T,N,K", GEMM_SHAPES)
 def test_prefill_gemm(gpu, mode, T, N, K):
     wq, deq = quantized(N, K, mode, 300 + T)
@@ -42,7 +45,7 @@ def test_prefill_gemm(gpu, mode, T, N, K):
     assert_close(got, np.asarray(a, np.float64) @ deq.T, what="prefill GEMM")
 
 
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 @pytest.mark.parametrize("T,N,K", [(1, 64, 128), (45, 192, 512), (256, 512, 3840)])
 def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     gq, gdeq = quantized(N, K, mode, 310)
@@ -60,7 +63,7 @@ def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
 # ceil(N / 64) * ceil(T / 128) reaches the CU count (256): the 12B gate/up of
 # a 512-token prompt (960 tiles) and a ragged 129-token batch of exactly 256
 # tiles (its second 128-row tile holds one token).
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8])
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 @pytest.mark.parametrize("T,N,K", [(512, 15360, 3840), (129, 8192, 512)])
 def test_prefill_gate_up_large_tiles(gpu, mode, T, N, K):
     assert -(-N // 64) * -(-T // 128) >= 256
@@ -154,7 +157,9 @@ def test_prefill_gemm_rejects_bad_shapes(gpu):
     with pytest.raises(gh.GhError):
         gpu.prefill_gemm(gh.QUANT_Q4, W, A, C, 4, 8, 100)  # K % 32
     with pytest.raises(gh.GhError):
-        gpu.prefill_gemm(gh.QUANT_NONE, W, A, C, 4, 8, 128)
+        gpu.prefill_gemm(3, W, A, C, 4, 8, 128)  # no such weight mode
+    with pytest.raises(gh.GhError):  # bf16 rows are read 16 bytes at a time
+        gpu.prefill_gemm(gh.QUANT_NONE, W.ptr + 4, A, C, 4, 8, 128)
 
 
 def tiny_cfg(**kw):

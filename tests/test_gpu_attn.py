@@ -156,12 +156,16 @@ def test_decode_attention_closed_forms(gpu):
     assert np.allclose(out[5], vc[17].reshape(nkv, D)[2], atol=1e-6)
 
 
+@pytest.mark.parametrize("theta", [1e6, 1e4])
 @pytest.mark.parametrize("k_eq_v", [False, True])
 @pytest.mark.parametrize("clock,S", [(600, 544), (639, 640), (5, 6)])
-def test_qkv_rope_attn_fused(gpu, clock, S, k_eq_v):
+def test_qkv_rope_attn_fused(gpu, clock, S, k_eq_v, theta):
     # the decode graph's per-layer attention step: q/k norm + RoPE, the cache
-    # write at slot_idx, and attention over the active list that includes it
-    nq, nkv, D, slots, rot, theta = 16, 8, 256, 640, 64, 1e6
+    # write at slot_idx, and attention over the active list that includes it.
+    # theta 1e4 with rot 64 over the 32 + 512 + 96 ring, V rows at unit RMS:
+    # the GQA attention workload exactly (partial RoPE on the first 64 dims at
+    # base 10000, positions with the window wrapped, all 640 slots at 639)
+    nq, nkv, D, slots, rot = 16, 8, 256, 640, 64
     kc, vc = make_cache(slots, nkv, D, 11)
     qraw = gh.synth_normal(nq * D, clock, 86, 0.0, 1.0)
     kraw = gh.synth_normal(nkv * D, clock, 87, 0.0, 1.0)

@@ -416,6 +416,50 @@ def bench_decode_bf16(ctx, n_prompt=512, n_decode=32):
             "prefill_path": "batched (bf16 MFMA GEMM on the bf16 rows), best of 2 calls after 1"}
 
 
+def bench_decode_q8(ctx, n_prompt=512, n_decode=64):
+    """The 12B shape with Q8_0 layers (the reference's --q8) and the Q8_0 head:
+    the 512-token prompt in one batched call (best of 2 after one untimed),
+    then n_decode greedy steps on the device ring."""
+    cfg = gh.model_config(vocab=262144, hidden=H, intermediate=I, layers=48, heads=16,
+                          kv_heads=8, head_dim=256, max_slots=640,
+                          full_layers=[l for l in range(48) if (l + 1) % 6 == 0])
+    m = gh.Model(ctx, cfg, mode=gh.QUANT_Q8, seed=0)
+    embed = m.read(-1, gh.T_EMBED, np.uint16).reshape(cfg.vocab_size, H)
+    scale = np.sqrt(np.float32(H))
+
+    def emb(t):
+        return (embed[t].astype(np.uint32) << 16).view(np.float32) * scale
+
+    m.ring_init(32, 512, 96)
+    prompt = gh.synth_uniform_u32(n_prompt, 1, 0, cfg.vocab_size)
+    xs = np.stack([emb(int(t)) for t in prompt])
+    m.ring_prefill(xs, 0, True)  # allocates the prefill buffers
+    times = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        tok = m.ring_prefill(xs, 0, True)
+        times.append(time.perf_counter() - t0)
+    prefill_s = min(times)
+    t0 = time.perf_counter()
+    for i in range(n_decode):
+        tok = m.forward_clock(emb(tok), n_prompt + i, True)
+    decode_s = time.perf_counter() - t0
+    m.close()
+    q8 = lambda k: (k // 32) * 36  # noqa: E731
+    layers = 48 * (8192 * q8(H) + H * q8(4096) + 2 * I * q8(H) + H * q8(I))
+    head = 262144 * q8(H)
+    norms = 48 * (4 * H + 2 * 256) * 4 + H * 4
+    ideal_s = sum(layers + head + norms + 262144 * 4 + min(c + 1, 544) * 8 * 256 * 4 * 2 * 48
+                  for c in range(n_prompt, n_prompt + n_decode)) / (HBM_PEAK_GBS * 1e9)
+    return {"decode_tok_s": round(n_decode / decode_s, 2),
+            "decode_ms_per_token": round(decode_s / n_decode * 1e3, 3),
+            "weight_bytes_per_token": layers + head,
+            "decode_weight_gbs": round((layers + head) * n_decode / decode_s / 1e9, 1),
+            "decode_roofline_frac": round(ideal_s / decode_s, 4),
+            "prefill_ms": round(prefill_s * 1e3, 2),
+            "prefill_path": "batched (MFMA Q8 dequant GEMM), best of 2 calls after 1"}
+
+
 def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
     """12B-shaped decode: 48 layers (global iff (l+1) % 6 == 0), hidden 3840,
     16/8 heads of 256, intermediate 15360, vocab 262144, Q4_0 layers and Q8_0
@@ -575,6 +619,7 @@ def main():
     gemv_bf16 = bench_gemv_bf16(ctx)
     dec = bench_decode(ctx, args.prompt, args.decode, cpu=not args.no_cpu) if not args.no_decode else None
     dec_bf16 = bench_decode_bf16(ctx, args.prompt) if not args.no_decode else None
+    dec_q8 = bench_decode_q8(ctx, args.prompt) if not args.no_decode else None
     if dec:
         log("decode %.1f tok/s (%.3f ms/token), prefill %.1f tok/s"
             % (dec["decode_tok_s"], dec["decode_ms_per_token"], dec["prefill_tok_s"]))
@@ -641,6 +686,7 @@ def main():
                   "lm_head_q8_argmax": head,
                   "gemv_bf16_8192x2048": gemv_bf16,
                   "decode_12b_bf16": dec_bf16,
+                  "decode_12b_q8": dec_q8,
                   "cpu_baseline_1thread": cpu1,
                   "decode_12b": dec},
     }

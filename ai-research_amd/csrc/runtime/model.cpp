@@ -87,6 +87,12 @@ struct gh_model {
   // GH_QGATE_KERNEL=1 (read at init): gated layers start with the separate
   // gh_qgate_k launch instead of gating in their QKV stream's prologue
   bool qgate_kernel = false;
+  // A prompt of at most this many tokens runs token by token through the
+  // decode graphs: at the 12B shape 1-3 tokens take 2.6 / 5.1 / 7.5 ms that
+  // way against 8.6-8.7 ms for one batched call (whose tiles are at least 64
+  // rows), and 4 tokens 9.9 against 8.8.  GH_PF_SEQ_MAX (read at init)
+  // overrides it; 0 sends every prompt to the batched kernels.
+  uint32_t seq_prefill_max = 3;
   // layer gating (quiescence): layers >= num_layers / 3 are gated when on
   bool q_on = false;
   float q_thr = 0.f;
@@ -559,6 +565,7 @@ gh_status finish_init(gh_model* m, gh_model** out) {
   m->eager = eager && eager[0] == '1';
   const char* qk = getenv("GH_QGATE_KERNEL");
   m->qgate_kernel = qk && qk[0] == '1';
+  if (const char* sq = getenv("GH_PF_SEQ_MAX")) m->seq_prefill_max = (uint32_t)strtoul(sq, nullptr, 10);
   gh_status st = reset_gates(m);
   if (st == GH_OK) st = record_graphs(m);
   if (st != GH_OK) {
@@ -946,8 +953,8 @@ gh_status gh_model_ring_prefill(gh_model* m, const float* x, uint32_t T, uint64_
   std::vector<uint64_t> clocks(T);
   std::vector<uint32_t> slots(T), n(T), lists((size_t)T * total);
   // the lists as the per-token calls would see them: slot activations of the
-  // earlier tokens of the batch included, later ones not; on a refused batch
-  // the ring keeps its state
+  // earlier tokens of the batch included, later ones not; a failed call
+  // leaves the ring as it was
   gh_ring* r = gh::ring_clone(m->ring);
   if (!r) return fail(GH_ERR_ALLOC, "gh_model_ring_prefill: ring copy");
   for (uint32_t t = 0; t < T; t++) {
@@ -1002,13 +1009,17 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   uint32_t max_n = 1;
   for (uint32_t t = 0; t < T; t++) max_n = std::max(max_n, n_active[t]);
   if (active_stride < max_n) return fail(GH_ERR_INVALID, "gh_model_prefill: active_stride < n_active");
-  // slot writers of this batch; a token may read its own and earlier tokens' slots only
+  // Slot writers of this batch.  The batched kernels write every token's K/V
+  // before any token attends, so they need each token to read only its own
+  // and earlier tokens' slots, and no slot written twice.  A batch that
+  // breaks this (a wrapped window: token t still attends to the slot token
+  // t + 1 overwrites) runs token by token instead, as does a short one.
   std::vector<int64_t> writer(c.max_slots, -1);
+  bool conflict = false;
   for (uint32_t t = 0; t < T; t++) {
     if (slot_idx[t] >= c.max_slots || clocks[t] > 0xFFFFFFFFull)
       return fail(GH_ERR_INVALID, "gh_model_prefill: slot or clock out of range");
-    if (writer[slot_idx[t]] >= 0)
-      return fail(GH_ERR_UNSUPPORTED, "gh_model_prefill: the batch writes one ring slot twice");
+    conflict = conflict || writer[slot_idx[t]] >= 0;
     writer[slot_idx[t]] = t;
   }
   for (uint32_t t = 0; t < T; t++) {
@@ -1017,15 +1028,25 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     const uint32_t* row = active + (size_t)t * active_stride;
     for (uint32_t i = 0; i < n_active[t]; i++) {
       if (row[i] >= c.max_slots) return fail(GH_ERR_INVALID, "gh_model_prefill: active slot out of range");
-      if (writer[row[i]] > (int64_t)t)
-        return fail(GH_ERR_UNSUPPORTED,
-                    "gh_model_prefill: a token attends to a slot a later token of the batch writes");
+      conflict = conflict || writer[row[i]] > (int64_t)t;
     }
   }
   if (m->ring)
     for (uint32_t t = 0; t < T; t++)
       if (slot_idx[t] != gh_ring_slot_index(m->ring, clocks[t]))
         return fail(GH_ERR_INVALID, "gh_model_prefill: a slot is not the ring's slot for its clock");
+  if (conflict || T <= m->seq_prefill_max) {
+    // token by token through the decode graphs, every gate open as in the
+    // batched call (model_gpu.zig:183); each token activates its ring slot
+    // itself
+    for (uint32_t t = 0; t < T; t++) {
+      gh_status ts = forward_token(m, x + (size_t)t * c.hidden_size, t + 1 == T && want_logits,
+                                   clocks[t], slot_idx[t], active + (size_t)t * active_stride,
+                                   n_active[t], out_token, true);
+      if (ts != GH_OK) return ts;
+    }
+    return m->ring ? ring_upload(m) : GH_OK;
+  }
   gh_status st = ensure_prefill(m, T, active_stride);
   if (st != GH_OK) return st;
   hipStream_t s = m->ctx->stream;

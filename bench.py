@@ -539,6 +539,17 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
     if cpu:
         cpu_dec = cpu_decode_baseline(m, cfg, n_prompt + n_decode + n_host,
                                       max(1, min(16, os.cpu_count() or 1)))
+    # short first-turn prompts (clocks from 0, after the run): 1-3 tokens go
+    # token by token through the decode graphs, longer ones to the batched
+    # kernels; median of 3 calls each
+    short = {}
+    for T in (1, 2, 3, 4, 8, 16):
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            m.ring_prefill(xs[:T], 0, True)
+            times.append(time.perf_counter() - t0)
+        short[str(T)] = round(sorted(times)[1] * 1e3, 2)
     m.close()
     clocks = range(n_prompt, n_prompt + n_decode)
     ideal_s = sum(decode_step_bytes(min(c + 1, 544)) for c in clocks) / (HBM_PEAK_GBS * 1e9)
@@ -559,6 +570,7 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
             "prefill_ms": round(prefill_s * 1e3, 2),
             "prefill_path": "batched (MFMA Q4 dequant GEMM), one call; median of 3 after 2 warm-up calls",
             "prefill_gemm_tflops": round(gemm_flop / prefill_s / 1e12, 1),
+            "prefill_short_ms": short,
             "model_init_s": round(init_s, 2),
             "decode_tokens_head": [int(t) for t in toks[:8]],
             "cpu_decode_baseline": cpu_dec}

@@ -380,11 +380,14 @@ gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits
  * (host); token t has position clocks[t], ring slot slot_idx[t] and active
  * list active[t * active_stride ..] of n_active[t] entries (host, as
  * ring.activateSlot / getActiveSlots give them).  Every layer writes each
- * token's K/V at its slot.  The batch must not write one slot twice, and no
- * token's active list may contain a slot that a later token of the batch
- * writes (GH_ERR_UNSUPPORTED: split the batch or use the per-token call).
- * The first call allocates the model's prefill buffers for T tokens (not
- * inside graph capture). */
+ * token's K/V at its slot.  The batched kernels write every token's K/V
+ * before any token attends, so a batch that writes one slot twice, or in
+ * which a token's active list holds a slot that a later token of the batch
+ * writes (a wrapped window), runs token by token through the decode graphs
+ * instead; so does a batch of at most 3 tokens, which is faster that way
+ * (environment GH_PF_SEQ_MAX at model init overrides the 3).  Otherwise the
+ * first call allocates the model's prefill buffers for T tokens (not inside
+ * graph capture). */
 gh_status gh_model_prefill(gh_model *m, const float *x, uint32_t T, const uint64_t *clocks,
                            const uint32_t *slot_idx, const uint32_t *active,
                            uint32_t active_stride, const uint32_t *n_active, int want_logits,
@@ -412,8 +415,8 @@ gh_status gh_model_forward_clock(gh_model *m, const float *x, int want_logits, u
                                  uint32_t *out_token);
 /* T prompt tokens at clocks first_clock .. first_clock + T - 1 through the
  * batched prefill, their slots and lists taken from the device ring (as T
- * calls of gh_model_forward_clock would see them).  A batch the prefill
- * refuses (it would write one slot twice) leaves the ring unchanged. */
+ * calls of gh_model_forward_clock would see them).  A call that fails
+ * leaves the ring unchanged. */
 gh_status gh_model_ring_prefill(gh_model *m, const float *x, uint32_t T, uint64_t first_clock,
                                 int want_logits, uint32_t *out_token);
 /* clearRecall (ring_buffer.zig:82-88) on the device ring. */

@@ -178,15 +178,20 @@ def ring_lists(ring, clocks):
     return slots, actives
 
 
-@pytest.mark.parametrize("mode,T,dup", [(gh.QUANT_Q4, 12, False), (gh.QUANT_Q8, 12, False),
-                                        (gh.QUANT_Q4, 11, False), (gh.QUANT_Q8, 9, True)])
-def test_model_prefill_matches_sequential_oracle(gpu, mode, T, dup):
+@pytest.mark.parametrize("mode,T,dup,seq_max", [
+    (gh.QUANT_Q4, 12, False, None), (gh.QUANT_Q8, 12, False, None), (gh.QUANT_Q4, 11, False, None),
+    (gh.QUANT_Q8, 9, True, None), (gh.QUANT_Q4, 3, False, None), (gh.QUANT_Q8, 2, False, None),
+    (gh.QUANT_Q4, 3, False, "0"), (gh.QUANT_Q4, 1, False, "0")])
+def test_model_prefill_matches_sequential_oracle(gpu, monkeypatch, mode, T, dup, seq_max):
     # T prompt tokens (4 anchors, then the window), one batch, then decode
     # steps through the per-token graph on the caches the prefill wrote.  T
     # not a multiple of 4 leaves a partial token group in the grouped
     # attention; dup names one slot twice in the last token's list (counted
     # twice, as the reference's loop over the list does), which keeps the
-    # batch on the per-token attention kernel
+    # batch on the per-token attention kernel.  Batches of 1-3 tokens run
+    # token by token unless GH_PF_SEQ_MAX=0 keeps them on the batched kernels
+    if seq_max is not None:
+        monkeypatch.setenv("GH_PF_SEQ_MAX", seq_max)
     cfg = tiny_cfg()
     m = gh.Model(gpu, cfg, mode=mode, seed=11)
     try:
@@ -293,14 +298,31 @@ def test_model_prefill_windowed_lists(gpu, shape):
         b.close()
 
 
-def test_model_prefill_rejects_slot_reuse(gpu):
-    cfg = tiny_cfg(layers=1, full_layers=())
+@pytest.mark.parametrize("case", ["slot twice", "reads a later write"])
+def test_model_prefill_conflicting_batch_runs_per_token(gpu, case):
+    # batches the batched kernels cannot run (every token's K/V is written
+    # before any token attends) go token by token, with the per-token calls'
+    # results: one slot written twice, or a token attending to the slot a
+    # later token overwrites; 5 tokens, above the short-prompt limit
+    cfg = tiny_cfg(layers=2, full_layers=(1,))
     m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=2)
+    p = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=2)
     try:
-        xs = np.stack([m.embed(i) for i in range(3)])
-        with pytest.raises(gh.GhError):  # one slot written twice
-            m.prefill(xs, [0, 1, 2], [5, 6, 5], [[5], [5, 6], [5, 6]], True)
-        with pytest.raises(gh.GhError):  # token 0 reads the slot token 1 writes
-            m.prefill(xs[:2], [0, 1], [5, 6], [[5, 6], [5, 6]], True)
+        xs = np.stack([m.embed(i) for i in range(5)])
+        if case == "slot twice":
+            slots = [5, 6, 7, 8, 5]
+            lists = [[5], [5, 6], [5, 6, 7], [5, 6, 7, 8], [5, 6, 7, 8]]
+        else:
+            slots = [5, 6, 7, 8, 9]
+            lists = [[5, 6], [5, 6], [5, 6, 7], [5, 6, 7, 8], [5, 6, 7, 8, 9]]
+        tok = m.prefill(xs, np.arange(5), slots, [np.array(a, np.uint32) for a in lists], True)
+        for c in range(5):
+            ptok = p.forward(xs[c], c, slots[c], np.array(lists[c], np.uint32), c == 4)
+        assert tok == ptok
+        assert np.array_equal(m.read(-1, gh.T_LOGITS, np.float32), p.read(-1, gh.T_LOGITS, np.float32))
+        for l in range(2):
+            for t in (gh.T_K_CACHE, gh.T_V_CACHE):
+                assert np.array_equal(m.read(l, t, np.float32), p.read(l, t, np.float32))
     finally:
         m.close()
+        p.close()

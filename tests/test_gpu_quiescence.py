@@ -20,7 +20,7 @@ from tol import assert_close
 pytestmark = pytest.mark.gpu
 NT = min(16, os.cpu_count() or 1)
 TOKENS = [5, 5, 5, 5, 9, 9, 9, 100, 100, 7, 7, 7, 7, 7, 300, 300, 41, 41, 41]
-PROMPT = 6  # batched prefill, then one step per token
+PROMPT = 6  # one prefill call, then one step per token
 
 
 def _cfg():
@@ -30,7 +30,7 @@ def _cfg():
                            global_head_dim=128, full_layers=(5,))
 
 
-def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4):
+def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4, prompt=PROMPT):
     """The reference sequence on the oracle: the prompt through the prefill
     graph (gates at threshold 0), then the decode steps gated at thr.
     Returns per step (token, logits, run, motions, caches) when record."""
@@ -44,19 +44,22 @@ def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4):
         slot = ring.activate_slot(0, c)
         act = ring.active_slots(0, c)
         before = xp.copy()
-        prompt = c < PROMPT
-        tok, _, lg, run = om.forward_gated(x, c, slot, act, xp, 0.0 if prompt else thr,
-                                           not prompt or c == PROMPT - 1, NT)
+        in_prompt = c < prompt
+        tok, _, lg, run = om.forward_gated(x, c, slot, act, xp, 0.0 if in_prompt else thr,
+                                           not in_prompt or c == prompt - 1, NT)
         motion = np.mean((xp.astype(np.float64) - before) ** 2, axis=1)
-        out.append((tok, lg, run.copy(), motion, c >= PROMPT))
+        out.append((tok, lg, run.copy(), motion, c >= prompt))
     return out, layers
 
 
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
-def test_quiescence_gating_matches_oracle(gpu, mode):
+@pytest.mark.parametrize("mode,prompt", [(gh.QUANT_Q4, PROMPT), (gh.QUANT_Q8, PROMPT),
+                                         (gh.QUANT_NONE, PROMPT), (gh.QUANT_Q4, 3)])
+def test_quiescence_gating_matches_oracle(gpu, mode, prompt):
     # every weight mode's gated QKV stream (the gate in its prologue); mode
-    # none: bf16 layers, the gated bf16 streams, and a prompt that goes token
-    # by token (its last token with every gate open)
+    # none: bf16 layers and the gated bf16 streams.  A 3-token prompt runs
+    # token by token through the decode graphs, its last token with every gate
+    # open, as the batched prefill runs a longer one
+    PROMPT = prompt
     cfg = _cfg()
     m = gh.Model(gpu, cfg, mode=mode, seed=21)
     try:
@@ -64,14 +67,14 @@ def test_quiescence_gating_matches_oracle(gpu, mode):
         dl = cfg.num_hidden_layers // 3
         thr = None
         for cand in (0.1, 0.07, 0.15, 0.2, 0.05, 0.3):
-            ref, _ = _oracle_run(m, cfg, embed, cand, mode=mode)
+            ref, _ = _oracle_run(m, cfg, embed, cand, mode=mode, prompt=PROMPT)
             motions = np.concatenate([r[3][dl:] for r in ref if r[4]])
             runs = np.concatenate([r[2][dl:] for r in ref if r[4]])
             if np.all(np.abs(motions - cand) > 0.05 * cand) and 0 < runs.sum() < runs.size:
                 thr = cand
                 break
         assert thr is not None, "no threshold with a 5% margin"
-        ref, layers = _oracle_run(m, cfg, embed, thr, mode=mode)
+        ref, layers = _oracle_run(m, cfg, embed, thr, mode=mode, prompt=PROMPT)
         m.set_quiescence(thr)
         ring = gh.Ring(1, 4, 24, 4)
         xs = np.stack([orc.embed(embed, t, cfg.hidden_size) for t in TOKENS])

@@ -73,7 +73,7 @@ def test_device_ring_matches_host_ring(gpu, tiers, clocks):
         mh.close()
 
 
-def test_ring_prefill_lists_and_refusal(gpu):
+def test_ring_prefill_lists_and_wrapped_batches(gpu):
     A, W, R = 4, 16, 4
     cfg = _cfg(A + W + R)
     md = gh.Model(gpu, cfg, seed=4)
@@ -81,13 +81,8 @@ def test_ring_prefill_lists_and_refusal(gpu):
     try:
         md.ring_init(A, W, R)
         ring = gh.Ring(1, A, W, R)
-        xs = np.stack([md.embed(t) for t in range(30)])
-        # 25 tokens from clock 0 would write slot 4 twice (clocks 4 and 20):
-        # refused, and the ring keeps its state
-        with pytest.raises(gh.GhError):
-            md.ring_prefill(xs[:25], 0, True)
-        assert not np.any(md.read(-1, gh.T_RING_FLAGS, np.uint32))
-        td = md.ring_prefill(xs[:12], 0, True)
+        xs = np.stack([md.embed(t % cfg.vocab_size) for t in range(48)])
+        td = md.ring_prefill(xs[:12], 0, True)  # the batched kernels
         slots = [ring.activate_slot(0, c) for c in range(12)]
         lists = [ring.active_slots(0, c) for c in range(12)]
         th = mh.prefill(xs[:12], np.arange(12), slots, lists, True)
@@ -98,9 +93,27 @@ def test_ring_prefill_lists_and_refusal(gpu):
             active = ring.active_slots(0, c)
             assert md.forward_clock(xs[c], c) == mh.forward(xs[c], c, slot, active)
             assert np.array_equal(md.read(-1, gh.T_ACTIVE, np.uint32)[:len(active)], active)
+        # a batch past the window's wraparound (token t attends to the slot
+        # token t + 1 overwrites; clocks 30 and 46 share a slot) runs token by
+        # token, exactly as per-token calls do
+        td = md.ring_prefill(xs[30:47], 30, True)
+        for c in range(30, 47):
+            slot = ring.activate_slot(0, c)
+            th = mh.forward(xs[c], c, slot, ring.active_slots(0, c), c == 46)
+        assert td == th
+        assert np.array_equal(md.read(-1, gh.T_LOGITS, np.float32), mh.read(-1, gh.T_LOGITS, np.float32))
+        for l in range(cfg.num_hidden_layers):
+            for t in (gh.T_K_CACHE, gh.T_V_CACHE):
+                assert np.array_equal(md.read(l, t, np.float32), mh.read(l, t, np.float32))
+        flags = md.read(-1, gh.T_RING_FLAGS, np.uint32)
+        assert flags[:A + W].sum() == A + W
+        slot = ring.activate_slot(0, 47)
+        active = ring.active_slots(0, 47)
+        assert md.forward_clock(xs[47], 47) == mh.forward(xs[47], 47, slot, active)
+        assert np.array_equal(md.read(-1, gh.T_ACTIVE, np.uint32)[:len(active)], active)
         # a host-list call on a ring model must name the ring's slot
         with pytest.raises(gh.GhError):
-            md.forward(xs[0], 30, 3, np.array([3], np.uint32))
+            md.forward(xs[0], 48, 3, np.array([3], np.uint32))
     finally:
         md.close()
         mh.close()

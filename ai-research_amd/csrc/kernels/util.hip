@@ -264,3 +264,17 @@ extern "C" __global__ __launch_bounds__(256) void gh_rope_table_k(const uint32_t
     tab[ROPE_TAB_HALF + i] = sn;
   }
 }
+
+// Moves the K/V rows a staged prefill batch wrote past the ring slots into
+// their slots: for cache y (base + off[y] bytes, rows of words[y] u32) and
+// pair x, row pairs[2x] := row pairs[2x + 1].  Grid (pairs, caches).  The
+// destination rows are ring slots and the sources staging rows, disjoint.
+extern "C" __global__ __launch_bounds__(256) void gh_rows_scatter_k(uint8_t* base,
+                                                                    const uint64_t* off,
+                                                                    const uint32_t* words,
+                                                                    const uint32_t* pairs) {
+  uint32_t* buf = reinterpret_cast<uint32_t*>(base + off[blockIdx.y]);
+  const uint32_t w = words[blockIdx.y];
+  const uint32_t dst = pairs[2 * blockIdx.x], src = pairs[2 * blockIdx.x + 1];
+  for (uint32_t i = threadIdx.x; i < w; i += 256) buf[(size_t)dst * w + i] = buf[(size_t)src * w + i];
+}

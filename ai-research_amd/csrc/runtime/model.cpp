@@ -5,7 +5,8 @@
 // HBM layout: one arena holding, per layer, the concatenated [q | k | v]
 // rows (one GEMV for the three projections), o, gate, up and down in the
 // reference's quant.zig blocks, the norms widened to f32, and the per-layer
-// K/V ring caches [max_slots][kv_dim]; then the Q8_0 LM head, the final
+// K/V caches [max_slots ring rows + max_slots prefill staging rows][kv_dim];
+// then the Q8_0 LM head, the final
 // norm and the activations.  The per-token graph (5 kernels a layer + the LM
 // head) is captured once into a HIP graph with the small host->device copies
 // of x, the active list and the step parameters, and replayed per token.
@@ -106,7 +107,7 @@ struct gh_model {
   uint32_t *pf_meta = nullptr, *pf_active = nullptr;
   // grouped prefill attention: per group of pf_gtok consecutive tokens, the
   // union of their active lists as (slot, token mask) pairs, and its length
-  uint32_t *pf_union = nullptr, *pf_ucount = nullptr;
+  uint32_t *pf_union = nullptr, *pf_ucount = nullptr, *pf_scatter = nullptr;
   uint32_t pf_ustride = 0, pf_gtok = 0;
   uint32_t pf_gkind = 0;  // this call: 0 per-token kernel, 1 gh_pf_attn_g_*, 2 gh_pf_attn_m_k
 
@@ -203,8 +204,10 @@ gh_status plan(gh_model* m) {
     L.post_attn = take(H * 4);
     L.pre_ffn = take(H * 4);
     L.post_ffn = take(H * 4);
-    L.k_cache = take((size_t)c.max_slots * L.kv_dim * 4);
-    L.v_cache = take((size_t)c.max_slots * L.kv_dim * 4);
+    // max_slots ring rows, then max_slots staging rows for a prefill batch
+    // whose tokens overwrite slots that earlier tokens of the batch attend to
+    L.k_cache = take((size_t)2 * c.max_slots * L.kv_dim * 4);
+    L.v_cache = take((size_t)2 * c.max_slots * L.kv_dim * 4);
     m->max_q = std::max(m->max_q, L.q_dim);
     m->max_kv = std::max(m->max_kv, L.kv_dim);
     m->layers.push_back(L);
@@ -1035,7 +1038,19 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     for (uint32_t t = 0; t < T; t++)
       if (slot_idx[t] != gh_ring_slot_index(m->ring, clocks[t]))
         return fail(GH_ERR_INVALID, "gh_model_prefill: a slot is not the ring's slot for its clock");
-  if (conflict || T <= m->seq_prefill_max) {
+  if (conflict && T > c.max_slots && T > m->seq_prefill_max) {
+    // staged batches hold at most max_slots tokens: consecutive chunks
+    for (uint32_t t0 = 0; t0 < T; t0 += c.max_slots) {
+      const uint32_t n = std::min(T - t0, c.max_slots);
+      gh_status cs = gh_model_prefill(m, x + (size_t)t0 * c.hidden_size, n, clocks + t0,
+                                      slot_idx + t0, active + (size_t)t0 * active_stride,
+                                      active_stride, n_active + t0,
+                                      t0 + n == T ? want_logits : 0, out_token);
+      if (cs != GH_OK) return cs;
+    }
+    return GH_OK;
+  }
+  if (T <= m->seq_prefill_max) {
     // token by token through the decode graphs, every gate open as in the
     // batched call (model_gpu.zig:183); each token activates its ring slot
     // itself
@@ -1050,10 +1065,35 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   gh_status st = ensure_prefill(m, T, active_stride);
   if (st != GH_OK) return st;
   hipStream_t s = m->ctx->stream;
+  // A staged batch (conflict): token t writes its K/V to staging row
+  // max_slots + t, and each list entry names the staging row of the slot's
+  // latest writer so far in the batch, else the ring slot, which still holds
+  // its value from before the batch.  After the layers, the latest writer's
+  // row of each written slot moves into the slot.
+  const uint32_t nslot = c.max_slots;
+  std::vector<uint32_t> staged_lists, pairs;
+  if (conflict) {
+    staged_lists.assign((size_t)T * active_stride, 0u);
+    std::vector<int64_t> last(nslot, -1);
+    for (uint32_t t = 0; t < T; t++) {
+      last[slot_idx[t]] = t;
+      const uint32_t* row = active + (size_t)t * active_stride;
+      uint32_t* out = &staged_lists[(size_t)t * active_stride];
+      for (uint32_t i = 0; i < n_active[t]; i++)
+        out[i] = last[row[i]] >= 0 ? nslot + (uint32_t)last[row[i]] : row[i];
+    }
+    for (uint32_t sl = 0; sl < nslot; sl++)
+      if (last[sl] >= 0) {
+        pairs.push_back(sl);
+        pairs.push_back(nslot + (uint32_t)last[sl]);
+      }
+    active = staged_lists.data();
+  }
+  const uint32_t nrows = conflict ? 2 * nslot : nslot;  // cache rows the lists may name
   std::vector<uint32_t> meta(3 * (size_t)T);
   for (uint32_t t = 0; t < T; t++) {
     meta[t] = (uint32_t)clocks[t];
-    meta[T + t] = slot_idx[t];
+    meta[T + t] = conflict ? nslot + t : slot_idx[t];
     meta[2 * T + t] = n_active[t];
   }
   std::vector<uint32_t> act((size_t)T * m->pf_stride, 0u);
@@ -1082,7 +1122,7 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     if (all256 && sameG && G0 >= 1 && G0 <= 16 && 16 % G0 == 0) {
       gkind = 2;
       gtok = 16 / G0;
-    } else if (small && c.max_slots <= (1u << 24)) {
+    } else if (small && nrows <= (1u << 24)) {
       gkind = 1;
       gtok = kPfGroup;
     }
@@ -1091,10 +1131,10 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   std::vector<uint32_t> uni, ucount;
   if (gkind) {
     const uint32_t groups = (T + gtok - 1) / gtok;
-    const uint32_t ustride = std::min(gtok * m->pf_stride, c.max_slots);
+    const uint32_t ustride = std::min(gtok * m->pf_stride, nrows);
     uni.assign((size_t)groups * ustride * 2, 0u);
     ucount.assign(groups, 0u);
-    std::vector<uint32_t> stamp(c.max_slots, 0u), pos(c.max_slots);
+    std::vector<uint32_t> stamp(nrows, 0u), pos(nrows);
     bool ok = true;
     for (uint32_t g = 0; g < groups && ok; g++) {
       uint32_t* u = &uni[(size_t)g * ustride * 2];
@@ -1130,8 +1170,33 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
         e = hipMemcpyAsync(m->pf_ucount, ucount.data(), ucount.size() * 4, hipMemcpyHostToDevice, s);
     }
   }
+  std::vector<uint8_t> table;
+  if (conflict) {  // offsets and row words of every cache, then the pairs
+    const size_t nc = 2 * m->layers.size();
+    table.resize(nc * 12 + pairs.size() * 4);
+    for (size_t l = 0; l < m->layers.size(); l++) {
+      const uint64_t off[2] = {m->layers[l].k_cache, m->layers[l].v_cache};
+      memcpy(&table[2 * l * 8], off, 16);
+      const uint32_t w[2] = {m->layers[l].kv_dim, m->layers[l].kv_dim};
+      memcpy(&table[nc * 8 + 2 * l * 4], w, 8);
+    }
+    memcpy(&table[nc * 12], pairs.data(), pairs.size() * 4);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(m->pf_scatter, table.data(), table.size(), hipMemcpyHostToDevice, s);
+  }
   if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: input copies");
   if ((st = prefill_forward(m, T, want_logits != 0)) != GH_OK) return st;
+  if (conflict) {
+    const size_t nc = 2 * m->layers.size();
+    uint8_t* base = m->arena;
+    const uint64_t* off = reinterpret_cast<const uint64_t*>(m->pf_scatter);
+    const uint32_t* words = m->pf_scatter + nc * 2;
+    const uint32_t* prs = m->pf_scatter + nc * 3;
+    void* args[] = {&base, &off, &words, &prs};
+    if ((st = m->ctx->launch("gh_rows_scatter_k", dim3((unsigned)(pairs.size() / 2), (unsigned)nc),
+                             dim3(256), 0, args)) != GH_OK)
+      return st;
+  }
   if (want_logits) {
     e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost, s);
     if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: token copy");
@@ -1191,6 +1256,10 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   const size_t o_active = take((size_t)T * stride * 4), o_rs = take((size_t)T * 4);
   // unions: at most ceil(T / g) groups of min(g * stride, max_slots) pairs, g <= 16
   const size_t o_union = take((size_t)(T + 15) * stride * 8), o_ucount = take((size_t)T * 4);
+  // staged batches: per cache (K and V of each layer) its byte offset in the
+  // arena and its row length in words, then (slot, staging row) pairs
+  const size_t n_caches = 2 * m->layers.size();
+  const size_t o_scatter = take(n_caches * 12 + (size_t)T * 8);
   if (m->pf_arena) {
     hipStreamSynchronize(m->ctx->stream);
     hipFree(m->pf_arena);
@@ -1213,6 +1282,7 @@ gh_status ensure_prefill(gh_model* m, uint32_t T, uint32_t stride) {
   m->pf_rs = f32(o_rs);
   m->pf_union = u32(o_union);
   m->pf_ucount = u32(o_ucount);
+  m->pf_scatter = u32(o_scatter);
   m->pf_cap = T;
   m->pf_stride = stride;
   return GH_OK;

@@ -539,6 +539,18 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
     if cpu:
         cpu_dec = cpu_decode_baseline(m, cfg, n_prompt + n_decode + n_host,
                                       max(1, min(16, os.cpu_count() or 1)))
+    # later-turn prompts past the window's wraparound (fresh clocks after the
+    # run): batched through staging rows, median of 3 calls each
+    wrapped = {}
+    c = n_prompt + n_decode + n_host
+    for T in (16, 64, 128):
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            m.ring_prefill(xs[:T], c, True)
+            times.append(time.perf_counter() - t0)
+            c += T
+        wrapped[str(T)] = round(sorted(times)[1] * 1e3, 2)
     # short first-turn prompts (clocks from 0, after the run): 1-3 tokens go
     # token by token through the decode graphs, longer ones to the batched
     # kernels; median of 3 calls each
@@ -571,6 +583,7 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
             "prefill_path": "batched (MFMA Q4 dequant GEMM), one call; median of 3 after 2 warm-up calls",
             "prefill_gemm_tflops": round(gemm_flop / prefill_s / 1e12, 1),
             "prefill_short_ms": short,
+            "prefill_wrapped_ms": wrapped,
             "model_init_s": round(init_s, 2),
             "decode_tokens_head": [int(t) for t in toks[:8]],
             "cpu_decode_baseline": cpu_dec}

@@ -380,14 +380,15 @@ gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits
  * (host); token t has position clocks[t], ring slot slot_idx[t] and active
  * list active[t * active_stride ..] of n_active[t] entries (host, as
  * ring.activateSlot / getActiveSlots give them).  Every layer writes each
- * token's K/V at its slot.  The batched kernels write every token's K/V
- * before any token attends, so a batch that writes one slot twice, or in
- * which a token's active list holds a slot that a later token of the batch
- * writes (a wrapped window), runs token by token through the decode graphs
- * instead; so does a batch of at most 3 tokens, which is faster that way
- * (environment GH_PF_SEQ_MAX at model init overrides the 3).  Otherwise the
- * first call allocates the model's prefill buffers for T tokens (not inside
- * graph capture). */
+ * token's K/V at its slot.  A batch that writes one slot twice, or in which
+ * a token's active list holds a slot that a later token of the batch writes
+ * (any prompt after the window has wrapped), writes its K/V to staging rows
+ * past the ring slots and moves them into the slots after the layers
+ * (batches of more than max_slots tokens run as consecutive chunks).  A
+ * batch of at most 3 tokens runs token by token through the decode graphs,
+ * which is faster at that size (environment GH_PF_SEQ_MAX at model init
+ * overrides the 3).  Otherwise the first call allocates the model's prefill
+ * buffers for T tokens (not inside graph capture). */
 gh_status gh_model_prefill(gh_model *m, const float *x, uint32_t T, const uint64_t *clocks,
                            const uint32_t *slot_idx, const uint32_t *active,
                            uint32_t active_stride, const uint32_t *n_active, int want_logits,

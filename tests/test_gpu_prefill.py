@@ -298,31 +298,55 @@ def test_model_prefill_windowed_lists(gpu, shape):
         b.close()
 
 
-@pytest.mark.parametrize("case", ["slot twice", "reads a later write"])
-def test_model_prefill_conflicting_batch_runs_per_token(gpu, case):
-    # batches the batched kernels cannot run (every token's K/V is written
-    # before any token attends) go token by token, with the per-token calls'
-    # results: one slot written twice, or a token attending to the slot a
-    # later token overwrites; 5 tokens, above the short-prompt limit
+@pytest.mark.parametrize("case", ["slot twice", "reads a later write", "wrapped window"])
+def test_model_prefill_staged_batch_matches_sequential_oracle(gpu, case):
+    # batches whose order the batched kernels cannot keep by writing in place
+    # (every token's K/V is written before any token attends): one slot
+    # written twice, a token attending to the slot a later token overwrites,
+    # and a whole prompt past the window's wraparound.  They write staging
+    # rows and move them into the slots after the layers; checked against the
+    # oracle run token by token and against the GPU's per-token path
     cfg = tiny_cfg(layers=2, full_layers=(1,))
     m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=2)
     p = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=2)
     try:
-        xs = np.stack([m.embed(i) for i in range(5)])
+        om, layers = oracle_model(m, cfg, gh.QUANT_Q4)
+        xs = np.stack([m.embed(i * 37 % cfg.vocab_size) for i in range(40)])
         if case == "slot twice":
-            slots = [5, 6, 7, 8, 5]
+            first, slots = 0, [5, 6, 7, 8, 5]
             lists = [[5], [5, 6], [5, 6, 7], [5, 6, 7, 8], [5, 6, 7, 8]]
-        else:
-            slots = [5, 6, 7, 8, 9]
+        elif case == "reads a later write":
+            first, slots = 0, [5, 6, 7, 8, 9]
             lists = [[5, 6], [5, 6], [5, 6, 7], [5, 6, 7, 8], [5, 6, 7, 8, 9]]
-        tok = m.prefill(xs, np.arange(5), slots, [np.array(a, np.uint32) for a in lists], True)
-        for c in range(5):
-            ptok = p.forward(xs[c], c, slots[c], np.array(lists[c], np.uint32), c == 4)
-        assert tok == ptok
-        assert np.array_equal(m.read(-1, gh.T_LOGITS, np.float32), p.read(-1, gh.T_LOGITS, np.float32))
-        for l in range(2):
-            for t in (gh.T_K_CACHE, gh.T_V_CACHE):
-                assert np.array_equal(m.read(l, t, np.float32), p.read(l, t, np.float32))
+        else:  # ring of 4 anchors + 16 window slots: clocks 0..19 one by one, then 20..39
+            ring = gh.Ring(1, 4, 16, 4)
+            for c in range(20):
+                slot = ring.activate_slot(0, c)
+                act = ring.active_slots(0, c)
+                m.forward(xs[c], c, slot, act, False)
+                p.forward(xs[c], c, slot, act, False)
+                om.forward(xs[c], c, slot, act, False, NT)
+            first = 20
+            slots = [ring.activate_slot(0, c) for c in range(20, 40)]
+            lists = [ring.active_slots(0, c) for c in range(20, 40)]
+        T = len(slots)
+        clocks = np.arange(first, first + T)
+        tok = m.prefill(xs[first:first + T], clocks, slots, [np.array(a, np.uint32) for a in lists], True)
+        for i in range(T):
+            want = i == T - 1
+            ptok = p.forward(xs[first + i], first + i, slots[i], np.array(lists[i], np.uint32), want)
+            rtok, _, rlog = om.forward(xs[first + i], first + i, slots[i], np.array(lists[i], np.uint32),
+                                       want, NT)
+        logits = m.read(-1, gh.T_LOGITS, np.float32)
+        assert_close(logits, rlog, what="staged prefill logits vs oracle")
+        assert_close(logits, p.read(-1, gh.T_LOGITS, np.float32), what="staged vs per-token logits")
+        assert tok == orc.argmax(logits) and ptok == orc.argmax(p.read(-1, gh.T_LOGITS, np.float32))
+        written = sorted(set(slots))
+        for l, d in enumerate(layers):
+            kvd = d["num_kv_heads"] * d["head_dim"]
+            for t, ref in ((gh.T_K_CACHE, d["k_cache"]), (gh.T_V_CACHE, d["v_cache"])):
+                got = m.read(l, t, np.float32).reshape(cfg.max_slots, kvd)
+                assert_close(got[written], ref[written], what="staged cache %d/%d" % (l, t))
     finally:
         m.close()
         p.close()

@@ -3,6 +3,23 @@
 #pragma once
 #include <stdint.h>
 
+// Decode attention splits: the grid holds nsplit splits per kv head (sized
+// from the cache capacity), and the ones that run are about one per this
+// many active slots, at most nsplit (attn_live_splits); the others exit at
+// once.  At S = 544 (the steady context of a 32 + 512 ring) that is 20
+// splits of 28 slots.
+#define ATT_SLOTS_PER_SPLIT 28u
+
+static inline
+#ifdef __HIPCC__
+    __host__ __device__
+#endif
+    uint32_t
+    attn_live_splits(uint32_t nsplit, uint32_t S) {
+  const uint32_t want = (S + ATT_SLOTS_PER_SPLIT - 1) / ATT_SLOTS_PER_SPLIT;
+  return want < 1u ? 1u : (want < nsplit ? want : nsplit);
+}
+
 struct AttnArgs {
   const float* q;          // [nq][D]: raw projections when fuse, else normalised + roped
   const float* k_in;       // fuse: raw k [nkv][D]
@@ -13,7 +30,8 @@ struct AttnArgs {
   float* v_cache;
   const uint32_t* active;  // [S] slot numbers (src/ring_buffer.zig getActiveSlots)
   const uint32_t* step;    // {clock, slot_idx, S, 0}
-  float* part;             // [nkv][nsplit][G][D + 4] split partials (o, m, l, pad)
+  float* part;             // [nkv][nsplit][G][D + 4] split partials (o, m, l, pad);
+                           // decode: splits >= attn_live_splits(nsplit, S) unused
   float* out;              // [nq][D], written by the merge kernel
   uint32_t nq, nkv, D, rot, k_eq_v, nsplit, fuse;
   float theta, eps, scale;

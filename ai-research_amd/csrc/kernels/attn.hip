@@ -449,7 +449,10 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
   const uint32_t kvh = blockIdx.x / nsplit, split = blockIdx.x % nsplit;
   const uint32_t clock = a.step[0], cur_slot = a.step[1], S = a.step[2];
   const bool fuse = a.fuse != 0;
-  const uint32_t per = (S + nsplit - 1) / nsplit;
+  // the splits that run: about ATT_SLOTS_PER_SPLIT active slots each
+  const uint32_t live = attn_live_splits(nsplit, S);
+  if (split >= live) return;  // uniform over the workgroup
+  const uint32_t per = (S + live - 1) / live;
   const uint32_t s0 = min(S, split * per), s1 = min(S, s0 + per);
   const uint32_t n = s1 - s0;
   const uint32_t d0 = lane * DPL;
@@ -958,8 +961,9 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   __shared__ float4 acc[ATT_WAVES][MAX_D / 4];
   const uint32_t D = a.D, G = a.nq / a.nkv, h = blockIdx.x, tid = threadIdx.x;
   const uint32_t lane = tid & 63, wave = tid >> 6;
-  const uint32_t kvh = h / G, g = h % G, PS = D + 4, ns = a.nsplit;
-  const float* allp = a.part + (size_t)kvh * ns * G * PS + (size_t)g * PS;
+  const uint32_t kvh = h / G, g = h % G, PS = D + 4;
+  const uint32_t ns = attn_live_splits(a.nsplit, a.step[2]);  // the splits that ran
+  const float* allp = a.part + (size_t)kvh * a.nsplit * G * PS + (size_t)g * PS;
   const size_t stride = (size_t)G * PS;  // one split to the next
   const uint32_t D4 = D / 4;
   auto row = [&](uint32_t sp, uint32_t col) {  // clamped: out-of-range reads get weight 0

@@ -522,8 +522,12 @@ gh_status fused_attn_args(gh_context* ctx, const float* Q_in, const float* K_in,
 }
 
 uint32_t attention_splits(const gh_context* ctx, uint32_t nkv, uint32_t max_slots) {
-  // about 32 slots per split (8 per wave), at most ~one workgroup per CU
-  uint32_t ns = std::max<uint32_t>(1u, (max_slots + 31) / 32);
+  // The grid's splits per kv head: enough for a full cache at about
+  // ATT_SLOTS_PER_SPLIT slots each (8 per wave), at most ~one workgroup per
+  // CU.  The kernels run only attn_live_splits(grid, S) of them, so the count
+  // at a given S does not depend on the capacity (20 at S = 544 for any
+  // capacity of 560 slots or more).  GH_ATTN_SPLITS sets the grid's count.
+  uint32_t ns = std::max<uint32_t>(1u, (max_slots + ATT_SLOTS_PER_SPLIT - 1) / ATT_SLOTS_PER_SPLIT);
   ns = std::min<uint32_t>(ns, std::max<uint32_t>(1u, (uint32_t)ctx->num_cus / std::max(1u, nkv)));
   if (const char* env = getenv("GH_ATTN_SPLITS")) {
     int v = atoi(env);

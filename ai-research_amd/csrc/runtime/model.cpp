@@ -7,9 +7,12 @@
 // reference's quant.zig blocks, the norms widened to f32, and the per-layer
 // K/V caches [max_slots ring rows + max_slots prefill staging rows][kv_dim];
 // then the Q8_0 LM head, the final
-// norm and the activations.  The per-token graph (5 kernels a layer + the LM
-// head) is captured once into a HIP graph with the small host->device copies
-// of x, the active list and the step parameters, and replayed per token.
+// norm and the activations.  Each forward pass is recorded once as a HIP
+// graph of kernels only -- the ring step, then 6 launches a layer (QKV
+// stream, attention, attention merge, o stream, gate+up stream, down stream),
+// then the LM head and its argmax -- and replayed per token; the host copies
+// x (and, on the host-list entry, the step record and the active list) in
+// before the replay and the token out after it.
 #include <stdlib.h>
 #include <string.h>
 
@@ -53,7 +56,10 @@ struct gh_model {
   uint8_t* arena = nullptr;
   size_t arena_bytes = 0;
   size_t lm_head = 0, final_norm = 0;
-  size_t x0 = 0, x1 = 0, qkv_out = 0, attn_out = 0, o_out = 0, act = 0, m_out = 0, logits = 0;
+  // x0 is the caller's x (in the io region); the residual stream runs in x1
+  // and x2, so a replay of a recorded graph sees the same x
+  size_t x0 = 0, x1 = 0, x2 = 0, qkv_out = 0, attn_out = 0, o_out = 0, act = 0, m_out = 0,
+         logits = 0;
   size_t token = 0, step = 0, active = 0, attn_part = 0, amax = 0;
   // The per-token inputs sit in one region, [x0: hidden f32 | step: 4 u32 |
   // active list], so that one host->device copy carries them (x alone and the
@@ -82,6 +88,10 @@ struct gh_model {
   // per-layer residual trace: row l = layer l's input, row L = the final residual
   float* trace = nullptr;
   bool trace_on = false;
+  // the batched prefill's trace: [L][T][hidden], layer l's input rows of
+  // every token of the last traced batch (pf_trace_T tokens)
+  float* pf_trace = nullptr;
+  uint32_t pf_trace_cap = 0, pf_trace_T = 0;
   // GH_EAGER_DECODE=1 (read at init): each token launches its kernels
   // directly instead of replaying the recorded graph (for kernel tracing).
   bool eager = false;
@@ -139,6 +149,7 @@ gh_model::~gh_model() {
   if (pf_arena) hipFree(pf_arena);
   if (embed_dev) hipFree(embed_dev);
   if (trace) hipFree(trace);
+  if (pf_trace) hipFree(pf_trace);
   if (h_io) hipHostFree(h_io);
   if (h_token) hipHostFree(h_token);
   if (ring) gh_ring_destroy(ring);
@@ -220,6 +231,7 @@ gh_status plan(gh_model* m) {
   m->step = m->io + align_up((size_t)H * 4, 256);
   m->active = m->step + 64;
   m->x1 = take(H * 4);
+  m->x2 = take(H * 4);
   m->ring_clock = take((size_t)c.max_slots * 4);
   m->ring_flag = take((size_t)c.max_slots * 4);
   m->rope_tab = take(2 * 2 * 256 * 4);
@@ -271,7 +283,12 @@ gh_status alloc_all(gh_model* m) {
   void* args[] = {&p, &zero, &words};
   gh_status st = m->ctx->launch("gh_fill_u32_k", dim3(8192), dim3(256), 0, args);
   if (st != GH_OK) return st;
-  e = hipStreamSynchronize(m->ctx->stream);
+  // the inputs a replay before any forward call sees: x = 0 at clock 0,
+  // slot 0, the one-slot list {0} (dense)
+  m->h_step[2] = 1;
+  m->h_step[3] = 2;
+  e = hipMemcpyAsync(m->arena + m->step, m->h_step, 16, hipMemcpyHostToDevice, m->ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "arena zero-fill");
   return GH_OK;
 }
@@ -482,7 +499,10 @@ gh_status record_forward(gh_model* m, bool logits, float thr) {
     g.s = 1.0f;
     g.eps = c.rms_norm_eps;
     g.mode = 2;
-    if (!gated) std::swap(xcur, xoth);
+    if (!gated) {
+      std::swap(xcur, xoth);
+      if (xoth == m->x0) xoth = m->x2;  // the caller's x stays as sent
+    }
     GateUpArgs ga{m->at<uint8_t>(L.gate), m->at<uint8_t>(L.up), m->at<float>(m->act)};
     if ((st = gh::launch_stream(ctx, gateup, &ga, g, I, H, run)) != GH_OK) return st;
     // 5. m = W_down . act
@@ -614,19 +634,17 @@ gh_status rerecord(gh_model* m) {
   return record_graphs(m);
 }
 
-// One token: the first `bytes` of the io region go up, the graph replays, and
-// with logits the token comes back.  open_gates: a prompt token with logits
-// while gating is on runs with every gate open (threshold 0), as the batched
-// prefill does; no graph holds that combination, so its kernels launch
-// directly.
-gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_token,
-                    bool open_gates = false) {
+// One token: the first `bytes` of the io region go up (none for bytes 0),
+// the graph replays, and with logits the token comes back.  The decode graph
+// gates at the threshold, the prefill graph at 0 (src/gpu/model_gpu.zig:
+// 182-183).
+gh_status run_token(gh_model* m, bool want_logits, size_t bytes, uint32_t* out_token) {
   hipStream_t s = m->ctx->stream;
-  hipError_t e = hipMemcpyAsync(m->arena + m->io, m->h_io, bytes, hipMemcpyHostToDevice, s);
+  hipError_t e = bytes ? hipMemcpyAsync(m->arena + m->io, m->h_io, bytes, hipMemcpyHostToDevice, s)
+                       : hipSuccess;
   if (e != hipSuccess) return hip_fail(e, "forward: input copy");
-  const bool direct = m->eager || (open_gates && want_logits && m->q_on);
-  gh_status st = direct ? record_forward(m, want_logits, want_logits && !open_gates ? m->q_thr : 0.0f)
-                        : gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
+  gh_status st = m->eager ? record_forward(m, want_logits, want_logits ? m->q_thr : 0.0f)
+                          : gh_graph_launch(m->ctx, want_logits ? m->graph_decode : m->graph_prefill);
   if (st != GH_OK) return st;
   if (want_logits) {
     e = hipMemcpyAsync(m->h_token, m->at<uint32_t>(m->token), 4, hipMemcpyDeviceToHost, s);
@@ -835,14 +853,13 @@ void gh_model_deinit(gh_model* m) { delete m; }
 namespace {
 gh_status forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
                         uint32_t slot_idx, const uint32_t* active_slots, uint32_t n_active,
-                        uint32_t* out_token, bool open_gates);
+                        uint32_t* out_token);
 }  // namespace
 
 gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
                                     uint32_t slot_idx, const uint32_t* active_slots,
                                     uint32_t n_active, uint32_t* out_token) {
-  return forward_token(m, x, want_logits, clock, slot_idx, active_slots, n_active, out_token,
-                       false);
+  return forward_token(m, x, want_logits, clock, slot_idx, active_slots, n_active, out_token);
 }
 
 }  // extern "C"
@@ -850,7 +867,7 @@ gh_status gh_dispatch_forward_token(gh_model* m, const float* x, int want_logits
 namespace {
 gh_status forward_token(gh_model* m, const float* x, int want_logits, uint64_t clock,
                         uint32_t slot_idx, const uint32_t* active_slots, uint32_t n_active,
-                        uint32_t* out_token, bool open_gates) {
+                        uint32_t* out_token) {
   if (!m || !x || !active_slots || !out_token)
     return fail(GH_ERR_INVALID, "gh_dispatch_forward_token: null argument");
   *out_token = 0;
@@ -876,8 +893,7 @@ gh_status forward_token(gh_model* m, const float* x, int want_logits, uint64_t c
                                   "for this clock");
     gh_ring_activate_slot(m->ring, 0, clock);
   }
-  return run_token(m, want_logits != 0, (m->active - m->io) + (size_t)n_active * 4, out_token,
-                   open_gates);
+  return run_token(m, want_logits != 0, (m->active - m->io) + (size_t)n_active * 4, out_token);
 }
 }  // namespace
 
@@ -916,6 +932,14 @@ gh_status gh_model_forward_clock(gh_model* m, const float* x, int want_logits, u
   m->h_step[3] = 1;  // the ring kernel activates the slot and builds the list
   gh_ring_activate_slot(m->ring, 0, clock);
   return run_token(m, want_logits != 0, (m->step - m->io) + 16, out_token);
+}
+
+gh_status gh_model_submit_prerecorded(gh_model* m, gh_graph_kind which) {
+  if (!m) return fail(GH_ERR_INVALID, "gh_model_submit_prerecorded: null model");
+  if (which != GH_GRAPH_DECODE && which != GH_GRAPH_PREFILL)
+    return fail(GH_ERR_INVALID, "gh_model_submit_prerecorded: unknown graph");
+  uint32_t tok = 0;
+  return run_token(m, which == GH_GRAPH_DECODE, 0, &tok);
 }
 
 gh_status gh_model_ring_clear_recall(gh_model* m) {
@@ -965,14 +989,23 @@ gh_status gh_model_ring_prefill(gh_model* m, const float* x, uint32_t T, uint64_
     slots[t] = gh_ring_activate_slot(r, 0, clocks[t]);
     n[t] = gh_ring_active_slots(r, 0, clocks[t], &lists[(size_t)t * total], total);
   }
+  // gh_model_prefill advances m->ring as its tokens or chunks finish: keep
+  // the state from before the call to put back on failure
+  gh_ring* before = gh::ring_clone(m->ring);
+  if (!before) {
+    gh_ring_destroy(r);
+    return fail(GH_ERR_ALLOC, "gh_model_ring_prefill: ring copy");
+  }
   gh_status st = gh_model_prefill(m, x, T, clocks.data(), slots.data(), lists.data(), total,
                                   n.data(), want_logits, out_token);
-  if (st != GH_OK) {
-    gh_ring_destroy(r);
-    return st;
-  }
+  gh_ring_destroy(st == GH_OK ? before : r);
   gh_ring_destroy(m->ring);
-  m->ring = r;
+  m->ring = st == GH_OK ? r : before;
+  if (st != GH_OK) {
+    const std::string why = gh_last_error();
+    ring_upload(m);
+    return fail(st, why);
+  }
   return ring_upload(m);
 }
 
@@ -1038,6 +1071,22 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     for (uint32_t t = 0; t < T; t++)
       if (slot_idx[t] != gh_ring_slot_index(m->ring, clocks[t]))
         return fail(GH_ERR_INVALID, "gh_model_prefill: a slot is not the ring's slot for its clock");
+  // Gating on: the last prompt token computes the logits, and forwardToken's
+  // GPU branch sends such a token through the decode graph, which gates at
+  // the threshold (compute_logits, src/model/forward.zig:41-45; recorded with
+  // quiescence_thresh, src/gpu/model_gpu.zig:182).  The tokens before it go
+  // through the prefill path, whose gates run at threshold 0 (model_gpu.zig:
+  // 183).
+  if (m->q_on && want_logits) {
+    if (T > 1) {
+      gh_status ps = gh_model_prefill(m, x, T - 1, clocks, slot_idx, active, active_stride,
+                                      n_active, 0, out_token);
+      if (ps != GH_OK) return ps;
+    }
+    const uint32_t t = T - 1;
+    return forward_token(m, x + (size_t)t * c.hidden_size, 1, clocks[t], slot_idx[t],
+                         active + (size_t)t * active_stride, n_active[t], out_token);
+  }
   if (conflict && T > c.max_slots && T > m->seq_prefill_max) {
     // staged batches hold at most max_slots tokens: consecutive chunks
     for (uint32_t t0 = 0; t0 < T; t0 += c.max_slots) {
@@ -1051,13 +1100,13 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     return GH_OK;
   }
   if (T <= m->seq_prefill_max) {
-    // token by token through the decode graphs, every gate open as in the
-    // batched call (model_gpu.zig:183); each token activates its ring slot
-    // itself
+    // token by token through the recorded graphs, as the reference prefills
+    // (src/interactive.zig:33-37): the prefill graph, then the decode graph
+    // for a last token with logits; each token activates its ring slot itself
     for (uint32_t t = 0; t < T; t++) {
       gh_status ts = forward_token(m, x + (size_t)t * c.hidden_size, t + 1 == T && want_logits,
                                    clocks[t], slot_idx[t], active + (size_t)t * active_stride,
-                                   n_active[t], out_token, true);
+                                   n_active[t], out_token);
       if (ts != GH_OK) return ts;
     }
     return m->ring ? ring_upload(m) : GH_OK;
@@ -1185,6 +1234,16 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
       e = hipMemcpyAsync(m->pf_scatter, table.data(), table.size(), hipMemcpyHostToDevice, s);
   }
   if (e != hipSuccess) return hip_fail(e, "gh_model_prefill: input copies");
+  if (m->trace_on && m->pf_trace_cap < T) {  // the batch trace, [L][T][hidden]
+    hipStreamSynchronize(s);
+    if (m->pf_trace) hipFree(m->pf_trace);
+    m->pf_trace = nullptr;
+    m->pf_trace_cap = m->pf_trace_T = 0;
+    e = hipMalloc(&m->pf_trace, (size_t)c.num_hidden_layers * T * c.hidden_size * 4);
+    if (e != hipSuccess) return fail(GH_ERR_ALLOC, std::string("prefill trace: ") + hipGetErrorString(e));
+    m->pf_trace_cap = T;
+  }
+  if (m->trace_on) m->pf_trace_T = T;
   if ((st = prefill_forward(m, T, want_logits != 0)) != GH_OK) return st;
   if (conflict) {
     const size_t nc = 2 * m->layers.size();
@@ -1327,6 +1386,12 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
                           m->at<float>(L.input_norm), P.scalar, 2, m_nz);
     }
     if (st != GH_OK) return st;
+    // residual trace: row l = the last token's input to layer l, and every
+    // token's in the batch trace
+    if (m->trace_on &&
+        ((st = copy_words(m, m->trace + (size_t)l * H, m->pf_x + (size_t)(T - 1) * H, H)) != GH_OK ||
+         (st = copy_words(m, m->pf_trace + (size_t)l * T * H, m->pf_x, (uint64_t)T * H)) != GH_OK))
+      return st;
     // with gating on, the per-token prefill graph runs every gate at
     // threshold 0 (model_gpu.zig:183): each gated layer ends holding the last
     // token's input as its previous input, and every layer has run
@@ -1446,6 +1511,9 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     if ((st = gh::launch_argmax_stream(ctx, &aa, p, c.vocab_size, H, m->at<uint32_t>(m->token),
                                        m->mode == GH_QUANT_NONE)) != GH_OK)
       return st;
+    if (m->trace_on && (st = copy_words(m, m->trace + (size_t)c.num_hidden_layers * H,
+                                        m->at<float>(m->x1), H)) != GH_OK)
+      return st;
   }
   return GH_OK;
 }
@@ -1484,6 +1552,12 @@ std::pair<uint8_t*, size_t> tensor_ref(const gh_model* m, int layer, gh_tensor t
   if (t == GH_T_TRACE) {  // row `layer` of the residual trace, 0..num_layers
     if (!m->trace || layer < 0 || layer > (int)m->layers.size()) return {nullptr, 0};
     return {reinterpret_cast<uint8_t*>(m->trace + (size_t)layer * H), (size_t)H * 4};
+  }
+  if (t == GH_T_PREFILL_TRACE) {  // layer `layer`'s input rows of the last traced batch
+    if (!m->pf_trace || m->pf_trace_T == 0 || layer < 0 || layer >= (int)m->layers.size())
+      return {nullptr, 0};
+    const size_t n = (size_t)m->pf_trace_T * H;
+    return {reinterpret_cast<uint8_t*>(m->pf_trace + (size_t)layer * n), n * 4};
   }
   if (layer < 0 || layer >= (int)m->layers.size()) return {nullptr, 0};
   const Layer& L = m->layers[layer];

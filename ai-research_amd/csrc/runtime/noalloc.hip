@@ -32,16 +32,21 @@ static __device__ __align__(256) float scratch[kScratchFloats];
 
 namespace gh {
 
+// A failure is kept in g_setup_error only, for the entry point to report: the
+// caller (gh_context_init) succeeds regardless, so the thread's last-error
+// message is left as it was.
 gh_status noalloc_setup(int device) {
-  if (device < 0 || device >= kMaxDevices)
-    return fail(GH_ERR_UNSUPPORTED, "allocation-free scratch: device ordinal above 63");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (device < 0 || device >= kMaxDevices) {
+    g_setup_error = "device ordinal above 63";
+    return GH_ERR_UNSUPPORTED;
+  }
   if (g_scratch[device]) return GH_OK;
   void* p = nullptr;
   hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess || !p) {
     g_setup_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
-    return fail(GH_ERR_HIP, g_setup_error);
+    return GH_ERR_HIP;
   }
   g_scratch[device] = static_cast<float*>(p);
   return GH_OK;

@@ -128,6 +128,7 @@ _SIGS.update({
     "gh_model_forward_clock": (_i, [_vp, _vp, _i, _u64, C.POINTER(_u32)]),
     "gh_model_ring_prefill": (_i, [_vp, _vp, _u32, _u64, _i, C.POINTER(_u32)]),
     "gh_model_ring_clear_recall": (_i, [_vp]),
+    "gh_model_submit_prerecorded": (_i, [_vp, _i]),
     "gh_model_write_recall_kv": (_i, [_vp, _u32, _u32, _vp, _vp, _u64]),
     "gh_model_set_trace": (_i, [_vp, _i]),
     "gh_model_set_quiescence": (_i, [_vp, _f32]),
@@ -141,7 +142,9 @@ _SIGS.update({
  T_PRE_FFN_NORM, T_POST_FFN_NORM, T_K_CACHE, T_V_CACHE) = range(13)
 T_LM_HEAD, T_FINAL_NORM, T_EMBED, T_LOGITS, T_HIDDEN = 20, 21, 22, 23, 24
 T_STEP, T_ACTIVE, T_RING_CLOCKS, T_RING_FLAGS, T_TRACE = 25, 26, 27, 28, 29
-T_GATE_FLAGS, T_GATE_PREV = 30, 31
+T_GATE_FLAGS, T_GATE_PREV, T_PREFILL_TRACE = 30, 31, 32
+# gh_graph_kind
+GRAPH_DECODE, GRAPH_PREFILL = 0, 1
 
 _lib = None
 
@@ -556,6 +559,11 @@ class Model:
         _check(lib().gh_model_ring_prefill(self.h, _ptr(x), x.shape[0], first_clock,
                                            int(want_logits), C.byref(tok)), "gh_model_ring_prefill")
         return tok.value
+
+    def submit_prerecorded(self, which=0):
+        """Replays the decode (0) or prefill (1) graph on the inputs the
+        device holds (src/model/bench.zig:12-15's submitPreRecorded)."""
+        _check(lib().gh_model_submit_prerecorded(self.h, which), "gh_model_submit_prerecorded")
 
     def ring_clear_recall(self):
         _check(lib().gh_model_ring_clear_recall(self.h), "gh_model_ring_clear_recall")

@@ -155,8 +155,10 @@ def bench_gemv(ctx, reps=256):
         ctx.synth_normal_dev(staging, M * K, 0, 500 + c, 0.0, 0.02, bf16=True)
         ctx.quantize_dev(arena.ptr + c * mat, staging, M, K, gh.QUANT_Q4)
     staging.free()
-    X = ctx.upload(gh.synth_normal(K, 0, 3, 0.0, 1.0))
+    x = gh.synth_normal(K, 0, 3, 0.0, 1.0)
+    X = ctx.upload(x)
     Y = ctx.alloc(32768 * 4)
+    host_w = arena.read(np.uint32, mat // 4).reshape(M, -1)  # copy 0, for the CPU baseline
     sizes = {}
     for rows in (8192, 2048, 32768):
         nb = rows * Q4_ROW(K)
@@ -170,7 +172,7 @@ def bench_gemv(ctx, reps=256):
     fit = {"us_2048_rows": round(t0, 3), "us_8192_rows": round(us, 3), "us_32768_rows": round(t1, 3),
            "marginal_gbs": round(marginal, 1),
            "fixed_us": round(t0 - b0 / (marginal * 1e9) * 1e6, 3)}
-    return nbytes / (us * 1e-6) / 1e9, us, fit
+    return nbytes / (us * 1e-6) / 1e9, us, fit, (host_w, x)
 
 
 def bench_gemv_bf16(ctx, reps=96):
@@ -277,7 +279,9 @@ def bench_attention(ctx, reps=96):
     out = ctx.alloc(nq * D * 4)
     res = {}
     tab = ctx.alloc(512 * 4)
-    for S, clock in ((544, 600), (640, 639)):
+    # (S, clock, cache capacity): the capacity sets the launch's grid of splits
+    # (32 per kv head at 1024, 23 at 640), S the splits that run (20 at 544)
+    for S, clock, cap in ((544, 600, 640), (640, 639, 640), (544, 600, 1024)):
         slot = 32 + (clock - 32) % 512
         act = ctx.upload(np.arange(S, dtype=np.uint32))
         # as the decode graph runs it: the list 0 .. S-1 declared in the step
@@ -290,24 +294,33 @@ def bench_attention(ctx, reps=96):
         def launch(i):
             kc, vc = caches[i % nl]
             ctx.qkv_rope_attn(q, k, v, qn, kn, kc, vc, act, st, out, nq, nkv, D, 256, False, 1e4,
-                              table=tab)
+                              table=tab, max_slots=cap)
 
         def launch_plain(i):
             kc, vc = caches[i % nl]
             ctx.qkv_rope_attn(q, k, v, qn, kn, kc, vc, act, st_plain, out, nq, nkv, D, 256, False,
-                              1e4)
+                              1e4, max_slots=cap)
 
         ms = timed_graph(ctx, launch, reps)
-        ms_plain = timed_graph(ctx, launch_plain, reps)
         nbytes = S * nkv * D * 4 * 2 + 2 * nq * D * 4 + 2 * nkv * D * 4 + S * 4
-        res["S%d" % S] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
-                          "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                          "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                          "us_list_read_angles_computed": round(ms_plain * 1e3, 3)}
+        row = {"us": round(ms * 1e3, 3), "bytes": nbytes,
+               "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+               "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if cap == 640:
+            row["us_list_read_angles_computed"] = round(timed_graph(ctx, launch_plain, reps) * 1e3, 3)
+            res["S%d" % S] = row
+        else:
+            res["S%d_capacity%d" % (S, cap)] = row
+    # what the CPU baseline runs: the same inputs and layer 0's caches
+    sample = {"q": q.read(np.float32, nq * D), "k": k.read(np.float32, nkv * D),
+              "v": v.read(np.float32, nkv * D), "q_norm": qn.read(np.float32, D),
+              "k_norm": kn.read(np.float32, D),
+              "k_cache": caches[0][0].read(np.float32).reshape(slots, nkv * D),
+              "v_cache": caches[0][1].read(np.float32).reshape(slots, nkv * D)}
     for kc, vc in caches:
         kc.free()
         vc.free()
-    return res
+    return res, sample
 
 
 def bench_lm_head(ctx, reps=20):
@@ -325,10 +338,13 @@ def bench_lm_head(ctx, reps=20):
     L, TOK = ctx.alloc(V * 4), ctx.alloc(4)
     pro = ctx.prologue(X, mode=1, norm=NW)
     ms = timed_graph(ctx, lambda i: ctx.norm_gemv_argmax_q8(W, L, TOK, V, H, pro), reps)
+    # what the CPU baseline runs: the same head, input, norm and the token
+    sample = {"w": W.read(np.uint32).reshape(V, -1), "x": X.read(np.float32, H),
+              "norm": NW.read(np.float32, H), "token": int(TOK.read(np.uint32, 1)[0])}
     W.free()
     nbytes = V * (H // 32) * 36 + 2 * H * 4 + V * 4 + 4
     return {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}, sample
 
 
 def decode_step_bytes(S):
@@ -589,6 +605,87 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
             "cpu_decode_baseline": cpu_dec}
 
 
+def _median_time(fn, budget_s, min_runs=3):
+    """Median seconds of fn() over at least min_runs runs and budget_s
+    seconds, after one untimed run."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_kernel_baselines(gemv_sample, attn_sample, head_sample, budget_s=2.0):
+    """The oracle's restatement of the reference CPU path for the other
+    workloads, timed on this host on the same bytes the GPU legs read, each
+    the median of at least 3 runs after one untimed:
+      * Q4_0 GEMV 8192 x 2048: the src/test_q4_exec.zig:56-74 dequant loop
+        inside gemvParallel's 16-job row split (src/kernels.zig:76-92), on
+        16 threads (or the host's count) and on one;
+      * decode attention at S = 544 and 640: q/k RMSNorm + RoPE and the cache
+        write, then runAttentionHeads (src/model/forward.zig:77-104,125-143),
+        which the reference runs on one thread;
+      * the Q8_0 LM head + argmax: final RMSNorm, the Q8_0 GEMV
+        (shaders/gemv_q8.wgsl's dequant order; the reference CPU path is
+        bf16-only) split 16 ways, and sampleArgmax (src/kernels.zig:164-174).
+    GB/s on the same algorithmic bytes as the GPU figures."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    nt = max(1, min(16, os.cpu_count() or 1))
+    res = {}
+    w, x = gemv_sample
+    M, K = w.shape[0], x.size
+    nbytes = M * Q4_ROW(K) + K * 4 + M * 4
+    t16, n16 = _median_time(lambda: orc.gemv_q4(w, x, K, nt), budget_s)
+    t1, n1 = _median_time(lambda: orc.gemv_q4(w, x, K, 1), budget_s)
+    res["gemv_q4_8192x2048"] = {
+        "value": round(nbytes / t16 / 1e9, 3), "unit": "GB/s", "cores": nt,
+        "host_cpus": os.cpu_count(), "kind": "port",
+        "sample": "%d calls, median %.3f ms, 16-job row split" % (n16, t16 * 1e3),
+        "one_thread": {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                       "sample": "%d calls, median %.3f ms" % (n1, t1 * 1e3)}}
+    a = attn_sample
+    nq, nkv, D = 16, 8, 256
+    for S, clock in ((544, 600), (640, 639)):
+        slot = 32 + (clock - 32) % 512
+        active = np.arange(S, dtype=np.uint32)
+        kc, vc = a["k_cache"].copy(), a["v_cache"].copy()
+
+        def step():
+            q, k, v = orc.qkv_norm_rope(a["q"], a["k"], a["v"], a["q_norm"], a["k_norm"], nq, nkv,
+                                        D, 256, False, 1e4, 1e-6, clock)
+            kc[slot], vc[slot] = k, v
+            return orc.attention(q, kc, vc, active, nq, nkv, D)
+
+        t, n = _median_time(step, budget_s)
+        nb = S * nkv * D * 4 * 2 + 2 * nq * D * 4 + 2 * nkv * D * 4 + S * 4
+        res["attention_S%d" % S] = {
+            "value": round(nb / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "us": round(t * 1e6, 1),
+            "sample": "%d calls (q/k norm + RoPE, cache write, 16 heads over %d slots), median "
+                      "%.3f ms" % (n, S, t * 1e3)}
+    h = head_sample
+    V = h["w"].shape[0]
+
+    def head():
+        xn = orc.rmsnorm(h["x"], h["norm"])
+        return orc.argmax(orc.gemv_q8(h["w"], xn, H, nt))
+
+    tok = head()
+    t, n = _median_time(head, budget_s * 1.5)
+    nb = V * (H // 32) * 36 + 2 * H * 4 + V * 4 + 4
+    res["lm_head_q8_argmax"] = {
+        "value": round(nb / t / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+        "ms": round(t * 1e3, 2), "token": tok, "token_equals_gpu": tok == h["token"],
+        "sample": "%d calls (RMSNorm, Q8_0 GEMV 262144 x 3840 split 16 ways, argmax), median "
+                  "%.1f ms" % (n, t * 1e3)}
+    return res
+
+
 def cpu_baseline(x, host_w, budget_s=10.0, threads=None):
     """The oracle's restatement of the reference CPU path (src/test_q4_exec.zig
     dequant loop inside gatedMlp's 16-job row split, src/kernels.zig:100-129)
@@ -637,10 +734,10 @@ def main():
     step_bytes = gu_bytes + dn_bytes
     value = step_bytes * args.steps / wall / 1e9
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-    gemv_gbs, gemv_us, gemv_fit = bench_gemv(ctx)
+    gemv_gbs, gemv_us, gemv_fit, gemv_sample = bench_gemv(ctx)
     ceiling = bench_read_ceiling(ctx)
-    attn = bench_attention(ctx)
-    head = bench_lm_head(ctx)
+    attn, attn_sample = bench_attention(ctx)
+    head, head_sample = bench_lm_head(ctx)
     gemv_bf16 = bench_gemv_bf16(ctx)
     dec = bench_decode(ctx, args.prompt, args.decode, cpu=not args.no_cpu) if not args.no_decode else None
     dec_bf16 = bench_decode_bf16(ctx, args.prompt) if not args.no_decode else None
@@ -651,8 +748,9 @@ def main():
     log("mlp %.1f GB/s, gate_up %.2f us, down %.2f us, gemv8192x2048 %.2f us"
         % (value, gu_ms * 1e3, dn_ms * 1e3, gemv_us))
 
-    # HBM bytes per launch from the committed counter passes
-    # (ai-research_amd/traffic.py; profiles/hbm_traffic_decode_kernels.md)
+    # HBM bytes per launch: not measured in this run, but read from the
+    # committed counter passes (traffic.py: rocprofv3 --pmc FETCH_SIZE, then
+    # WRITE_SIZE, scaled by a copy kernel's reading; profiles/traffic.json)
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     trec = json.load(open(tpath)) if os.path.exists(tpath) else {}
     tbytes = lambda k: trec[k]["hbm_bytes"] if k in trec else None  # noqa: E731
@@ -660,7 +758,13 @@ def main():
     attn["S544"]["traffic"] = tbytes("attention_544")
     head["traffic"] = tbytes("lm_head_q8")
 
-    cpu = cpu1 = None
+    cpu = cpu1 = cpu_kernels = None
+    if not args.no_cpu:
+        cpu_kernels = cpu_kernel_baselines(gemv_sample, attn_sample, head_sample)
+        attn["S544"]["cpu_baseline"] = cpu_kernels["attention_S544"]
+        attn["S640"]["cpu_baseline"] = cpu_kernels["attention_S640"]
+        head["cpu_baseline"] = cpu_kernels["lm_head_q8_argmax"]
+    del gemv_sample, attn_sample, head_sample
     if not args.no_cpu:
         n, dt, nt = cpu_baseline(x, host_w)
         cpu = {"value": round(step_bytes * n / dt / 1e9, 3), "unit": "GB/s", "cores": nt,
@@ -690,7 +794,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "kernel": "gh_gateup_q4",
-                     "avg_launch_us": round(gu_ms * 1e3, 3)},
+                     "avg_launch_us": round(gu_ms * 1e3, 3),
+                     "traffic_source": "committed counter pass (profiles/traffic.json), "
+                                       "not measured in this run"},
         "cpu_baseline": cpu,
         "extra": {"mlp_frac_of_peak": round(value / HBM_PEAK_GBS, 4),
                   "clock_warmup_ms": round(CLOCK_WARM_S * 1e3),
@@ -704,6 +810,9 @@ def main():
                                                  "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
                                                  "bytes": 10526720,
                                                  "traffic": tbytes("gemv_q4_8192x2048")},
+                  "gemv_q4_8192x2048_cpu_baseline": cpu_kernels and cpu_kernels["gemv_q4_8192x2048"],
+                  "traffic_source": "every traffic figure: the committed counter passes in "
+                                    "profiles/traffic.json (traffic.py), not this run",
                   "down_proj_traffic": tbytes("gh_gemv_q4"),
                   "gemv_q4_k2048_size_fit": gemv_fit,
                   "hbm_read_ceiling": ceiling,

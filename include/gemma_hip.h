@@ -420,6 +420,21 @@ gh_status gh_model_forward_clock(gh_model *m, const float *x, int want_logits, u
  * leaves the ring unchanged. */
 gh_status gh_model_ring_prefill(gh_model *m, const float *x, uint32_t T, uint64_t first_clock,
                                 int want_logits, uint32_t *out_token);
+/* GpuEngine.submitPreRecorded (src/gpu/kernels.zig:147-157) on the model's
+ * own graphs, as src/model/bench.zig:12-15 calls it with cmd_buf_decode:
+ * replays the recorded decode graph (GH_GRAPH_DECODE: layers, LM head and
+ * argmax, gated at the model's threshold) or prefill graph (GH_GRAPH_PREFILL)
+ * on the inputs the device already holds -- x, the step record and the list
+ * of the last forward call -- with no host copy in or out, and waits for it.
+ * Before any forward call those inputs are x = 0 at clock 0, slot 0, the
+ * one-slot list {0}.  The passes keep the caller's x as sent, so without
+ * layer gating a replay recomputes the last forward call's step bit for bit
+ * (its K/V row rewritten with the same values); with gating on, a replay
+ * also moves each gated layer's previous input, as every pass does.  After
+ * gh_model_ring_init a replay records the step's activation in the device
+ * ring again. */
+typedef enum gh_graph_kind { GH_GRAPH_DECODE = 0, GH_GRAPH_PREFILL = 1 } gh_graph_kind;
+gh_status gh_model_submit_prerecorded(gh_model *m, gh_graph_kind which);
 /* clearRecall (ring_buffer.zig:82-88) on the device ring. */
 gh_status gh_model_ring_clear_recall(gh_model *m);
 /* writeRecallKV (ring_buffer.zig:90-99) into the device caches: layer's
@@ -440,16 +455,20 @@ gh_status gh_model_write_recall_kv(gh_model *m, uint32_t layer, uint32_t rank, c
  * hidden, stores x as x_prev, and runs only when that mean is >= threshold
  * (or threshold <= 0); a gated-off layer is skipped whole -- x passes
  * through, and its K/V row of this token is not written.  The prefill graph
- * (want_logits 0) and gh_model_prefill run every layer but record x_prev as
- * the reference's prefill graph does (gates at threshold 0).  threshold 0
- * turns gating off.  Resets every x_prev to 0 and records the graphs again. */
+ * (want_logits 0) runs every layer but records x_prev as the reference's
+ * prefill graph does (gates at threshold 0); so does gh_model_prefill for
+ * every prompt token except a last one with logits, which runs the gated
+ * decode graph, as forwardToken sends it (compute_logits,
+ * src/model/forward.zig:41-45).  threshold 0 turns gating off.  Resets
+ * every x_prev to 0 and records the graphs again. */
 gh_status gh_model_set_quiescence(gh_model *m, float threshold);
 
 /* Per-layer residual trace (no reference counterpart; for checking): when
  * enabled, every forward call also copies the residual stream at each
  * layer's input into row l of a [num_layers + 1][hidden] buffer, and with
- * logits the final residual into row num_layers (GH_T_TRACE).  Enabling or
- * disabling records the graphs again. */
+ * logits the final residual into row num_layers (GH_T_TRACE); a batched
+ * prefill does the same for its last token.  Enabling or disabling records
+ * the graphs again. */
 gh_status gh_model_set_trace(gh_model *m, int enable);
 
 /* Tensor access for checking and cache set-up (no reference counterpart). */
@@ -479,7 +498,10 @@ typedef enum gh_tensor {
   GH_T_RING_FLAGS = 28,  /* u32 [max_slots]: device ring active flag per slot */
   GH_T_TRACE = 29,     /* f32 [hidden]: trace row `layer` (0 .. num_layers) */
   GH_T_GATE_FLAGS = 30, /* u32 [num_layers]: 1 where the last step ran the layer */
-  GH_T_GATE_PREV = 31  /* f32 [num_layers][hidden]: each gated layer's previous input */
+  GH_T_GATE_PREV = 31, /* f32 [num_layers][hidden]: each gated layer's previous input */
+  GH_T_PREFILL_TRACE = 32 /* f32 [T][hidden]: with the trace on, layer `layer`'s input
+                             rows (0 .. num_layers - 1) of every token of the last
+                             batched gh_model_prefill call (or chunk) */
 } gh_tensor;
 /* Byte size of a tensor (0 when it does not exist). */
 size_t gh_model_tensor_bytes(const gh_model *m, int layer, gh_tensor t);

@@ -9,6 +9,7 @@
  */
 #include "oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -617,6 +618,226 @@ uint32_t orc_forward_token(const orc_model *m, float *x, uint64_t clock,
   }
   scratch_free(&s);
   return tok;
+}
+
+/* ------------------------------------------------------------------------ */
+/* one layer over a batch of tokens                                         */
+/* ------------------------------------------------------------------------ */
+/* The row dots of a batch: Y[t][r] = the dot of row r of W (Q4_0 or Q8_0)
+ * with token t's vector, for rows [r0, r1).  Each dot takes the per-token
+ * GEMV's weights (q4_row_dot: (f32(nib) - 8) * d; q8_row_dot: f32(q) * s)
+ * and its sequential sum from element 0, so Y[t][r] is bit-identical to
+ * orc_gemv_q4 / orc_gemv_q8 on token t alone.  The batch only changes the
+ * loop nest: a tile of BR rows is dequantized once and meets BT tokens per
+ * pass (xt is the batch transposed, [cols][T]), with one accumulator per
+ * (row, token). */
+#define BR 4
+#define BT 16
+typedef struct {
+  const uint32_t *w;
+  const float *xt;
+  float *y;
+  size_t cols, wpr, T, ystride;
+  int mode;
+} bg_ctx;
+
+static void dequant_row(int mode, const uint32_t *row, size_t cols, float *out) {
+  size_t nb = cols / QK;
+  for (size_t b = 0; b < nb; b++) {
+    if (mode == ORC_QUANT_Q4) {
+      const uint32_t *blk = row + b * 5;
+      float d = u2f(blk[0]);
+      for (int w = 0; w < 4; w++)
+        for (int n = 0; n < 8; n++)
+          out[b * QK + (size_t)w * 8 + (size_t)n] = ((float)((blk[1 + w] >> (4 * n)) & 0xFu) - 8.0f) * d;
+    } else {
+      const uint32_t *blk = row + b * 9;
+      float sc = u2f(blk[0]);
+      for (int j = 0; j < QK; j++)
+        out[b * QK + (size_t)j] = (float)(int8_t)((blk[1 + (j >> 2)] >> (8 * (j & 3))) & 0xFFu) * sc;
+    }
+  }
+}
+
+/* A full BR x BT tile (4 rows x 16 tokens) in AVX2 registers: per element
+ * j, acc[i][t] = acc[i][t] + w[i][j] * x[t][j] as one multiply and one add
+ * (no fused multiply-add), the same two roundings as the scalar loop. */
+static void bg_tile_full(const float *wt, size_t cols, const float *xt, size_t T,
+                         float acc[BR][BT]) {
+  __m256 a00 = _mm256_setzero_ps(), a01 = _mm256_setzero_ps();
+  __m256 a10 = _mm256_setzero_ps(), a11 = _mm256_setzero_ps();
+  __m256 a20 = _mm256_setzero_ps(), a21 = _mm256_setzero_ps();
+  __m256 a30 = _mm256_setzero_ps(), a31 = _mm256_setzero_ps();
+  const float *w0 = wt, *w1 = wt + cols, *w2 = wt + 2 * cols, *w3 = wt + 3 * cols;
+  for (size_t j = 0; j < cols; j++) {
+    const __m256 x0 = _mm256_loadu_ps(xt + j * T), x1 = _mm256_loadu_ps(xt + j * T + 8);
+    __m256 w = _mm256_broadcast_ss(w0 + j);
+    a00 = _mm256_add_ps(a00, _mm256_mul_ps(w, x0));
+    a01 = _mm256_add_ps(a01, _mm256_mul_ps(w, x1));
+    w = _mm256_broadcast_ss(w1 + j);
+    a10 = _mm256_add_ps(a10, _mm256_mul_ps(w, x0));
+    a11 = _mm256_add_ps(a11, _mm256_mul_ps(w, x1));
+    w = _mm256_broadcast_ss(w2 + j);
+    a20 = _mm256_add_ps(a20, _mm256_mul_ps(w, x0));
+    a21 = _mm256_add_ps(a21, _mm256_mul_ps(w, x1));
+    w = _mm256_broadcast_ss(w3 + j);
+    a30 = _mm256_add_ps(a30, _mm256_mul_ps(w, x0));
+    a31 = _mm256_add_ps(a31, _mm256_mul_ps(w, x1));
+  }
+  _mm256_storeu_ps(acc[0], a00);
+  _mm256_storeu_ps(acc[0] + 8, a01);
+  _mm256_storeu_ps(acc[1], a10);
+  _mm256_storeu_ps(acc[1] + 8, a11);
+  _mm256_storeu_ps(acc[2], a20);
+  _mm256_storeu_ps(acc[2] + 8, a21);
+  _mm256_storeu_ps(acc[3], a30);
+  _mm256_storeu_ps(acc[3] + 8, a31);
+}
+
+static void bg_rows(void *p, size_t r0, size_t r1) {
+  bg_ctx *c = (bg_ctx *)p;
+  float *wt = (float *)malloc(BR * c->cols * sizeof(float));
+  if (!wt) return;
+  float acc[BR][BT];
+  for (size_t rb = r0; rb < r1; rb += BR) {
+    size_t nr = r1 - rb < BR ? r1 - rb : BR;
+    for (size_t i = 0; i < nr; i++) dequant_row(c->mode, c->w + (rb + i) * c->wpr, c->cols, wt + i * c->cols);
+    for (size_t t0 = 0; t0 < c->T; t0 += BT) {
+      size_t nt = c->T - t0 < BT ? c->T - t0 : BT;
+      if (nr == BR && nt == BT) {
+        bg_tile_full(wt, c->cols, c->xt + t0, c->T, acc);
+      } else {
+        memset(acc, 0, sizeof(acc));
+        for (size_t j = 0; j < c->cols; j++) {
+          const float *xj = c->xt + j * c->T + t0;
+          for (size_t i = 0; i < nr; i++) {
+            const float w = wt[i * c->cols + j];
+            for (size_t t = 0; t < nt; t++) acc[i][t] = acc[i][t] + w * xj[t];
+          }
+        }
+      }
+      for (size_t t = 0; t < nt; t++)
+        for (size_t i = 0; i < nr; i++) c->y[(t0 + t) * c->ystride + rb + i] = acc[i][t];
+    }
+  }
+  free(wt);
+}
+
+/* out[c][t] = in[t][c] */
+static void transpose(const float *in, size_t T, size_t cols, float *out) {
+  for (size_t t = 0; t < T; t++)
+    for (size_t c = 0; c < cols; c++) out[c * T + t] = in[t * cols + c];
+}
+
+static void batch_gemm(int mode, const uint32_t *w, const float *xt, float *y, size_t rows,
+                       size_t cols, size_t T, int nt) {
+  bg_ctx c = {w, xt, y, cols, orc_quantized_row_words(cols, mode), T, rows, mode};
+  par_rows(rows, nt, bg_rows, &c);
+}
+
+typedef struct {
+  const float *q;
+  const orc_layer *L;
+  size_t kvd, qd, nq, stride;
+  const uint32_t *active, *n_active;
+  float *out;
+} ba_ctx;
+static void ba_tokens(void *p, size_t t0, size_t t1) {
+  ba_ctx *c = (ba_ctx *)p;
+  for (size_t t = t0; t < t1; t++)
+    orc_attention(c->q + t * c->qd, c->L->k_cache, c->L->v_cache, c->kvd, c->active + t * c->stride,
+                  c->n_active[t], c->nq, c->L->num_kv_heads, c->L->head_dim, c->out + t * c->qd);
+}
+
+int orc_forward_layer_batch(const orc_model *m, size_t layer, float *X, size_t T,
+                            const uint64_t *clocks, const uint32_t *slots, const uint32_t *active,
+                            size_t stride, const uint32_t *n_active, int nt) {
+  const orc_layer *L = &m->layers[layer];
+  size_t H = m->hidden, I = m->intermediate, nq = m->num_q_heads;
+  size_t hd = L->head_dim, qd = nq * hd, kvd = L->num_kv_heads * hd;
+  float theta = L->full_attention ? m->rope_theta_full : m->rope_theta;
+  if (T == 0) return 0;
+  if (m->layer_mode != ORC_QUANT_Q4 && m->layer_mode != ORC_QUANT_Q8) {
+    /* bf16 rows: the per-token layer, token by token */
+    orc_scratch s;
+    if (!scratch_init(m, &s)) { scratch_free(&s); return -1; }
+    for (size_t t = 0; t < T; t++)
+      forward_layer(m, L, &s, X + t * H, clocks[t], slots[t], active + t * stride, n_active[t], nt);
+    scratch_free(&s);
+    return 0;
+  }
+  size_t maxk = H > I ? H : I;
+  if (qd > maxk) maxk = qd;
+  float *xn = (float *)malloc(T * H * sizeof(float));
+  float *xt = (float *)malloc(T * maxk * sizeof(float));
+  float *q = (float *)malloc(T * qd * sizeof(float));
+  float *k = (float *)malloc(T * kvd * sizeof(float));
+  float *v = (float *)malloc(T * kvd * sizeof(float));
+  float *at = (float *)malloc(T * qd * sizeof(float));
+  float *o = (float *)malloc(T * H * sizeof(float));
+  float *g = (float *)malloc(T * I * sizeof(float));
+  float *u = (float *)malloc(T * I * sizeof(float));
+  int ok = xn && xt && q && k && v && at && o && g && u;
+  if (ok) {
+    /* normed = RMSNorm(x, input_norm); q, k, v = W normed */
+    for (size_t t = 0; t < T; t++) orc_rmsnorm(xn + t * H, X + t * H, L->input_norm, H, m->eps);
+    transpose(xn, T, H, xt);
+    batch_gemm(m->layer_mode, L->wq, xt, q, qd, H, T, nt);
+    batch_gemm(m->layer_mode, L->wk, xt, k, kvd, H, T, nt);
+    if (!L->k_eq_v) batch_gemm(m->layer_mode, L->wv, xt, v, kvd, H, T, nt);
+    for (size_t t = 0; t < T; t++)
+      orc_qkv_norm_rope(q + t * qd, k + t * kvd, v + t * kvd, L->q_norm, L->k_norm, nq,
+                        L->num_kv_heads, hd, L->rotary_dim, L->k_eq_v, theta, m->eps, clocks[t]);
+    /* K/V into the cache and attention, in token order.  When no slot is
+     * written twice and no token lists a slot a later token writes, writing
+     * every row first leaves each token the cache it sees in order, and the
+     * tokens attend in parallel. */
+    int in_order = 1;
+    for (size_t t = 0; t < T && in_order; t++) {
+      for (size_t t2 = t + 1; t2 < T && in_order; t2++) in_order = slots[t2] != slots[t];
+      for (size_t i = 0; i < n_active[t] && in_order; i++)
+        for (size_t t2 = t + 1; t2 < T && in_order; t2++)
+          in_order = active[t * stride + i] != slots[t2];
+    }
+    ba_ctx bc = {q, L, kvd, qd, nq, stride, active, n_active, at};
+    if (in_order) {
+      for (size_t t = 0; t < T; t++) {
+        memcpy(L->k_cache + slots[t] * kvd, k + t * kvd, kvd * sizeof(float));
+        memcpy(L->v_cache + slots[t] * kvd, v + t * kvd, kvd * sizeof(float));
+      }
+      par_rows(T, nt, ba_tokens, &bc);
+    } else {
+      for (size_t t = 0; t < T; t++) {
+        memcpy(L->k_cache + slots[t] * kvd, k + t * kvd, kvd * sizeof(float));
+        memcpy(L->v_cache + slots[t] * kvd, v + t * kvd, kvd * sizeof(float));
+        ba_tokens(&bc, t, t + 1);
+      }
+    }
+    /* o = Wo attn; [RMSNorm(o, post_attn)]; x = x + o */
+    transpose(at, T, qd, xt);
+    batch_gemm(m->layer_mode, L->wo, xt, o, H, qd, T, nt);
+    for (size_t t = 0; t < T; t++) {
+      float *xr = X + t * H, *orow = o + t * H;
+      if (L->post_attn_norm) orc_rmsnorm(orow, orow, L->post_attn_norm, H, m->eps);
+      for (size_t i = 0; i < H; i++) xr[i] = (xr[i] + orow[i]) * 1.0f;
+      orc_rmsnorm(xn + t * H, xr, L->pre_ffn_norm, H, m->eps);
+    }
+    /* act = gelu(Wg normed) * (Wu normed); m = Wd act */
+    transpose(xn, T, H, xt);
+    batch_gemm(m->layer_mode, L->wg, xt, g, I, H, T, nt);
+    batch_gemm(m->layer_mode, L->wu, xt, u, I, H, T, nt);
+    for (size_t i = 0; i < T * I; i++) g[i] = orc_gelu_tanh(g[i]) * u[i];
+    transpose(g, T, I, xt);
+    batch_gemm(m->layer_mode, L->wd, xt, o, H, I, T, nt);
+    /* [RMSNorm(m, post_ffn)]; x = (x + m) * layer_scalar */
+    for (size_t t = 0; t < T; t++) {
+      float *xr = X + t * H, *orow = o + t * H;
+      if (L->post_ffn_norm) orc_rmsnorm(orow, orow, L->post_ffn_norm, H, m->eps);
+      for (size_t i = 0; i < H; i++) xr[i] = (xr[i] + orow[i]) * L->layer_scalar;
+    }
+  }
+  free(xn); free(xt); free(q); free(k); free(v); free(at); free(o); free(g); free(u);
+  return ok ? 0 : -1;
 }
 
 /* quiescence_gate.wgsl:16-62: the mean over H of (x - x_prev)^2, summed the

@@ -26,6 +26,8 @@
  *   orc_ring_*                 pinned: ring_buffer.zig:149-187 KATs + wraparound
  *   orc_attention              pinned: equal scores -> mean(V), S=1 -> V,
  *                              dominant score -> that V, fp64 brute force
+ *   orc_forward_layer_batch    pinned: bit-identical to orc_forward_token run
+ *                              token by token on the layer (tests/test_oracle.py)
  *   orc_forward_token          pinned: an independent fp64 numpy forward
  *                              (tests/numpy_ref.forward64) within 1e-5, with
  *                              planted mistakes in it shown to miss by >1e-3
@@ -142,6 +144,17 @@ void orc_embed(const uint16_t *embed_bf16, uint32_t token, size_t hidden, float 
 uint32_t orc_forward_token(const orc_model *m, float *x, uint64_t clock,
                            size_t slot_idx, const uint32_t *active, size_t n_active,
                            int want_logits, float *logits, int nthreads);
+
+/* Layer `layer` of the step above for T tokens in order: token t with clock
+ * clocks[t], slot slots[t] and the active list active[t * stride ..] of
+ * n_active[t] entries; X [T][H] is updated in place, the layer's caches as T
+ * calls of orc_forward_token on that one layer would leave them, and every
+ * output bit-identical to those calls (the GEMVs become row-tile x token-tile
+ * products with the same per-dot summation order).  Returns 0, or -1 when
+ * out of memory. */
+int orc_forward_layer_batch(const orc_model *m, size_t layer, float *X, size_t T,
+                            const uint64_t *clocks, const uint32_t *slots, const uint32_t *active,
+                            size_t stride, const uint32_t *n_active, int nthreads);
 
 /* ---- layer gating ------------------------------------------------------- */
 /* quiescence_gate.wgsl: mean (x - x_prev)^2 in the shader's order; x_prev <- x */

@@ -66,6 +66,9 @@ def lib():
         L.orc_forward_token.restype = C.c_uint32
         L.orc_forward_token.argtypes = [C.c_void_p, _f32p, C.c_uint64, _sz, _u32p, _sz,
                                         C.c_int, _f32p, C.c_int]
+        L.orc_forward_layer_batch.restype = C.c_int
+        L.orc_forward_layer_batch.argtypes = [C.c_void_p, _sz, _f32p, _sz, C.POINTER(C.c_uint64),
+                                              _u32p, _u32p, _sz, _u32p, C.c_int]
         L.orc_gate_mean_sq.restype = C.c_float
         L.orc_gate_mean_sq.argtypes = [_f32p, _f32p, _sz]
         L.orc_forward_token_gated.restype = C.c_uint32
@@ -430,6 +433,29 @@ class Model:
                                       _p(act, C.c_uint32), act.size, int(want_logits),
                                       _p(logits, C.c_float), nthreads)
         return int(tok), x, (logits if want_logits else None)
+
+    def forward_layer_batch(self, layer, X, clocks, slots, actives, nthreads=1):
+        """Layer `layer` for T tokens in order (orc_forward_layer_batch): X
+        [T][H], token t at clocks[t] in slot slots[t] attending over the
+        slot list actives[t].  Returns the layer's outputs [T][H]; the
+        layer's caches are updated in place, as T forward() calls on that
+        layer alone would leave them (bit for bit)."""
+        X = np.array(X, np.float32, copy=True, order="C")
+        T = X.shape[0]
+        stride = max(1, max(len(a) for a in actives))
+        act = np.zeros((T, stride), np.uint32)
+        for t, a in enumerate(actives):
+            act[t, :len(a)] = a
+        n = np.array([len(a) for a in actives], np.uint32)
+        ck = np.ascontiguousarray(clocks, np.uint64)
+        sl = np.ascontiguousarray(slots, np.uint32)
+        rc = lib().orc_forward_layer_batch(C.byref(self._m), layer, _p(X, C.c_float), T,
+                                           ck.ctypes.data_as(C.POINTER(C.c_uint64)),
+                                           _p(sl, C.c_uint32), _p(act, C.c_uint32), stride,
+                                           _p(n, C.c_uint32), nthreads)
+        if rc != 0:
+            raise MemoryError("orc_forward_layer_batch: out of memory")
+        return X
 
     def forward_gated(self, x, clock, slot_idx, active, x_prev, thresh, want_logits=True,
                       nthreads=1):

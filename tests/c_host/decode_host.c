@@ -20,10 +20,15 @@
  *   present tensors' bf16 data in that order;
  *   bf16 embed [vocab][hidden]; bf16 final_norm [hidden]; u32 prompt[n_prompt].
  * Prints "tokens:" and the greedy tokens (the last prompt token's, then one
- * per decode step) on one line; exits 1 with the backend's message on any
- * failure. */
+ * per decode step) on one line.  Then runs the engine's --bench sequence
+ * (src/model/bench.zig:12-21: one warm-up submitPreRecorded of the decode
+ * graph, 20 timed with a host clock) through gh_model_submit_prerecorded,
+ * and prints "bench:" with the ms per token and the token the last replay
+ * left.  Exits 1 with the backend's message on any failure. */
+#define _POSIX_C_SOURCE 199309L
 #include <math.h>
 #include <stdint.h>
+#include <time.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -181,6 +186,27 @@ int main(int argc, char** argv) {
     if (want_logits) printf(" %u", token);
   }
   printf("\n");
+
+  /* --bench: g.engine.submitPreRecorded(g.cmd_buf_decode), 1 + 20 times */
+  st = gh_model_submit_prerecorded(m, GH_GRAPH_DECODE);
+  if (st != GH_OK) return fail_with("gh_model_submit_prerecorded", st);
+  struct timespec t0, t1;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  for (int i = 0; i < 20; i++) {
+    st = gh_model_submit_prerecorded(m, GH_GRAPH_DECODE);
+    if (st != GH_OK) return fail_with("gh_model_submit_prerecorded", st);
+  }
+  clock_gettime(CLOCK_MONOTONIC, &t1);
+  const double ms = ((double)(t1.tv_sec - t0.tv_sec) * 1e3 + (double)(t1.tv_nsec - t0.tv_nsec) / 1e6) / 20.0;
+  const size_t vocab_bytes = (size_t)cfg.vocab_size * 4;
+  float* logits = (float*)malloc(vocab_bytes);
+  st = gh_model_read_tensor(m, -1, GH_T_LOGITS, logits, vocab_bytes);
+  if (st != GH_OK) return fail_with("gh_model_read_tensor", st);
+  uint32_t best = 0;
+  for (uint32_t i = 1; i < cfg.vocab_size; i++)
+    if (logits[i] > logits[best]) best = i;
+  printf("bench: %.4f ms / token, token %u\n", ms, best);
+  free(logits);
 
   gh_ring_destroy(ring);
   gh_model_deinit(m);

@@ -5,7 +5,8 @@ gpuDispatchForwardToken per token -- the prompt token by token without
 logits except for its last token, then greedy decode (src/interactive.zig:
 33-48, src/gpu/model_dispatch.zig:131-147).  Its tokens must equal the
 oracle's, teacher-forced on the same sequence, and those of the same model
-driven through the Python binding."""
+driven through the Python binding.  It then runs the engine's --bench
+sequence (src/model/bench.zig:12-21) through gh_model_submit_prerecorded."""
 import os
 import struct
 import subprocess
@@ -111,5 +112,10 @@ def test_c_host_prompt_then_greedy_decode(gpu, tmp_path, mode):
                 assert_close(logits, rlog, what="C-host sequence step %d" % clock)
                 assert tok == rtok, "step %d: token %d vs oracle %d" % (clock, tok, rtok)
         assert ptoks == ctoks, "C host %s vs Python binding %s" % (ctoks, ptoks)
+        # the --bench replays (src/model/bench.zig:12-15) recompute the last
+        # decode step: its token again
+        bench = [ln for ln in run.stdout.splitlines() if ln.startswith("bench:")][0].split()
+        assert float(bench[1]) > 0.0
+        assert int(bench[-1]) == ctoks[-1], bench
     finally:
         m.close()

@@ -133,9 +133,9 @@ def test_model_init_from_host_bf16(gpu, mode):
         m.close()
 
 
-def _12b(layers, full_layers):
+def _12b(layers, full_layers, slots=640):
     return gh.model_config(vocab=262144, hidden=3840, intermediate=15360, layers=layers,
-                           heads=16, kv_heads=8, head_dim=256, max_slots=640,
+                           heads=16, kv_heads=8, head_dim=256, max_slots=slots,
                            full_layers=full_layers)
 
 
@@ -162,19 +162,23 @@ def _populated_step(gpu, cfg, mode=gh.QUANT_Q4):
     return m, om, layers, clock, slot, active
 
 
-@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_NONE])
-def test_12b_width_two_layers_strict(gpu, mode):
+@pytest.mark.parametrize("mode,slots", [(gh.QUANT_Q4, 640), (gh.QUANT_NONE, 640),
+                                        (gh.QUANT_Q4, 1024)])
+def test_12b_width_two_layers_strict(gpu, mode, slots):
     # 12B widths, one sliding and one full-attention layer, 544 active slots:
     # logits within the 2e-3 bar elementwise and the greedy token bit-exact.
-    # Mode none: bf16 layers and the bf16 262144 x 3840 head.
-    m, om, layers, clock, slot, active = _populated_step(gpu, _12b(2, [1]), mode)
+    # Mode none: bf16 layers and the bf16 262144 x 3840 head.  1024 slots:
+    # the cache depth the reference allocates per layer (src/gpu/model_gpu.zig:
+    # 86), with the 640-slot ring in its first rows; the attention grid then
+    # holds 32 splits per kv head, of which the 20 for S = 544 run.
+    m, om, layers, clock, slot, active = _populated_step(gpu, _12b(2, [1], slots), mode)
     try:
         x = m.embed(4242)
         tok = m.forward(x, clock, slot, active)
         rtok, _, rlog = om.forward(x, clock, slot, active, True, NT)
-        check_token(m, rlog, tok, rtok, "12B-width 2 layers")
+        check_token(m, rlog, tok, rtok, "12B-width 2 layers, %d slots" % slots)
         for l in (0, 1):
-            kc = m.read(l, gh.T_K_CACHE, np.float32).reshape(640, -1)
+            kc = m.read(l, gh.T_K_CACHE, np.float32).reshape(slots, -1)
             assert_close(kc[slot], layers[l]["k_cache"][slot], what="K row layer %d" % l)
     finally:
         m.close()
@@ -247,3 +251,32 @@ def test_eager_decode_matches_graph(gpu, monkeypatch):
     finally:
         mg.close()
         me.close()
+
+
+def test_submit_prerecorded_replays_the_decode_graph(gpu):
+    # src/model/bench.zig:12-15 times submitPreRecorded(cmd_buf_decode): the
+    # recorded decode graph replayed on whatever inputs the device holds.
+    # gh_model_submit_prerecorded does the same: before any forward call the
+    # inputs are x = 0 at clock 0 with the one-slot list {0}; after a step, a
+    # replay recomputes that step bit for bit (same x, list and K/V row)
+    cfg = tiny_cfg()
+    m = gh.Model(gpu, cfg, seed=9)
+    try:
+        m.submit_prerecorded(gh.GRAPH_DECODE)
+        assert np.all(np.isfinite(m.read(-1, gh.T_LOGITS, np.float32)))
+        m.submit_prerecorded(gh.GRAPH_PREFILL)
+        ring = gh.Ring(cfg.num_hidden_layers, 4, 16, 4)
+        for c in range(6):
+            slot = ring.activate_slot(0, c)
+            tok = m.forward(m.embed(c * 11 + 1), c, slot, ring.active_slots(0, c), True)
+        logits = m.read(-1, gh.T_LOGITS, np.float32)
+        kc = m.read(0, gh.T_K_CACHE, np.float32)
+        for _ in range(3):
+            m.submit_prerecorded(gh.GRAPH_DECODE)
+            assert np.array_equal(m.read(-1, gh.T_LOGITS, np.float32), logits)
+            assert np.array_equal(m.read(0, gh.T_K_CACHE, np.float32), kc)
+        assert orc.argmax(logits) == tok
+        with pytest.raises(gh.GhError):
+            m.submit_prerecorded(7)
+    finally:
+        m.close()

@@ -350,3 +350,54 @@ def test_model_prefill_staged_batch_matches_sequential_oracle(gpu, case):
     finally:
         m.close()
         p.close()
+
+
+@pytest.mark.parametrize("T", [20, 30])
+def test_model_ring_prefill_staged_head_dim_256(gpu, T):
+    # Staged batches on the matrix-core grouped attention (head_dim 256, 16
+    # query / 8 kv heads: 8 tokens per group, a K/V staging row named in the
+    # union lists): a ring of 4 anchors + 16 window + 4 recall slots, clocks
+    # 0..19 token by token, then T tokens from clock 20 in one
+    # gh_model_ring_prefill call, every one past the window's wrap.  T = 30
+    # exceeds max_slots (24), so the batch runs as two staged chunks (24 + 6
+    # tokens).  Checked against the oracle token by token and against the
+    # GPU's per-token path: the last token's logits and every cache row.
+    cfg = gh.model_config(vocab=1024, hidden=512, intermediate=1024, layers=2, heads=16,
+                          kv_heads=8, head_dim=256, max_slots=24, full_layers=(1,))
+    m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=6)
+    p = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=6)
+    try:
+        om, layers = oracle_model(m, cfg, gh.QUANT_Q4)
+        for x in (m, p):
+            x.ring_init(4, 16, 4)
+        ring = gh.Ring(1, 4, 16, 4)
+        xs = np.stack([m.embed(i * 53 % cfg.vocab_size) for i in range(20 + T)])
+        for c in range(20):
+            slot = ring.activate_slot(0, c)
+            act = ring.active_slots(0, c)
+            m.forward_clock(xs[c], c, False)
+            p.forward_clock(xs[c], c, False)
+            om.forward(xs[c], c, slot, act, False, NT)
+        tok = m.ring_prefill(xs[20:], 20, True)
+        for c in range(20, 20 + T):
+            slot = ring.activate_slot(0, c)
+            act = ring.active_slots(0, c)
+            ptok = p.forward_clock(xs[c], c, c == 20 + T - 1)
+            rtok, _, rlog = om.forward(xs[c], c, slot, act, c == 20 + T - 1, NT)
+        logits = m.read(-1, gh.T_LOGITS, np.float32)
+        plog = p.read(-1, gh.T_LOGITS, np.float32)
+        assert_close(logits, rlog, what="staged head_dim-256 prefill logits vs oracle")
+        assert_close(logits, plog, what="staged head_dim-256 prefill vs per-token logits")
+        assert tok == orc.argmax(logits) and ptok == orc.argmax(plog)
+        # the device rings agree with the host ring after the call
+        assert np.array_equal(m.read(-1, gh.T_RING_CLOCKS, np.uint32),
+                              p.read(-1, gh.T_RING_CLOCKS, np.uint32))
+        for l, d in enumerate(layers):
+            for t, ref in ((gh.T_K_CACHE, d["k_cache"]), (gh.T_V_CACHE, d["v_cache"])):
+                got = m.read(l, t, np.float32).reshape(cfg.max_slots, -1)
+                per = p.read(l, t, np.float32).reshape(cfg.max_slots, -1)
+                assert_close(got[:20], ref[:20], what="staged cache %d/%d vs oracle" % (l, t))
+                assert_close(got[:20], per[:20], what="staged cache %d/%d vs per-token" % (l, t))
+    finally:
+        m.close()
+        p.close()

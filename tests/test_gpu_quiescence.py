@@ -31,9 +31,12 @@ def _cfg():
 
 
 def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4, prompt=PROMPT):
-    """The reference sequence on the oracle: the prompt through the prefill
-    graph (gates at threshold 0), then the decode steps gated at thr.
-    Returns per step (token, logits, run, motions, caches) when record."""
+    """The reference sequence on the oracle: the prompt tokens before the
+    last through the prefill graph (gates at threshold 0), then the last
+    prompt token, which computes the logits, and the decode steps through the
+    decode graph gated at thr (forwardToken's compute_logits selects it,
+    src/model/forward.zig:41-45; src/gpu/model_gpu.zig:182-183).  Returns
+    per step (token, logits, run, motions, gated at thr)."""
     om, layers = oracle_model(m, cfg, mode)
     ring = gh.Ring(1, 4, 24, 4)
     L, H = cfg.num_hidden_layers, cfg.hidden_size
@@ -44,11 +47,10 @@ def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4, prompt=PROMPT
         slot = ring.activate_slot(0, c)
         act = ring.active_slots(0, c)
         before = xp.copy()
-        in_prompt = c < prompt
-        tok, _, lg, run = om.forward_gated(x, c, slot, act, xp, 0.0 if in_prompt else thr,
-                                           not in_prompt or c == prompt - 1, NT)
+        gated = c >= prompt - 1
+        tok, _, lg, run = om.forward_gated(x, c, slot, act, xp, thr if gated else 0.0, gated, NT)
         motion = np.mean((xp.astype(np.float64) - before) ** 2, axis=1)
-        out.append((tok, lg, run.copy(), motion, c >= prompt))
+        out.append((tok, lg, run.copy(), motion, gated))
     return out, layers
 
 
@@ -56,9 +58,10 @@ def _oracle_run(m, cfg, embed, thr, record=None, mode=gh.QUANT_Q4, prompt=PROMPT
                                          (gh.QUANT_NONE, PROMPT), (gh.QUANT_Q4, 3)])
 def test_quiescence_gating_matches_oracle(gpu, mode, prompt):
     # every weight mode's gated QKV stream (the gate in its prologue); mode
-    # none: bf16 layers and the gated bf16 streams.  A 3-token prompt runs
-    # token by token through the decode graphs, its last token with every gate
-    # open, as the batched prefill runs a longer one
+    # none: bf16 layers and the gated bf16 streams.  The prompt's tokens
+    # before the last run every layer (batched, or for a 3-token prompt token
+    # by token through the prefill graph); its last token, which computes the
+    # logits, runs the gated decode graph
     PROMPT = prompt
     cfg = _cfg()
     m = gh.Model(gpu, cfg, mode=mode, seed=21)
@@ -82,8 +85,9 @@ def test_quiescence_gating_matches_oracle(gpu, mode, prompt):
         lists = [ring.active_slots(0, c) for c in range(PROMPT)]
         tok = m.prefill(xs[:PROMPT], np.arange(PROMPT), slots, lists, True)
         check_token(m, ref[PROMPT - 1][1], tok, ref[PROMPT - 1][0], "prompt")
-        assert np.all(m.read(-1, gh.T_GATE_FLAGS, np.uint32) == 1)
-        skipped = 0
+        flags = m.read(-1, gh.T_GATE_FLAGS, np.uint32)
+        assert list(flags) == list(ref[PROMPT - 1][2]), (list(flags), list(ref[PROMPT - 1][2]))
+        skipped = int((ref[PROMPT - 1][2] == 0).sum())
         for c in range(PROMPT, len(TOKENS)):
             slot = ring.activate_slot(0, c)
             act = ring.active_slots(0, c)

@@ -482,3 +482,36 @@ def test_forward_gated_matches_ungated_and_skips_whole_layers():
     xp3[1:] += 1.0
     _, _, _, run = orc.Model(H, I, V, nq, e, head, fnorm).forward_gated(x, 7, 7, active, xp3, 1e9)
     assert list(run) == [1, 0, 0]
+
+
+@pytest.mark.parametrize("mode", ["q4", "q8", "bf16"])
+@pytest.mark.parametrize("case", ["in order", "slot rewritten"])
+def test_forward_layer_batch_equals_token_by_token(mode, case):
+    # orc_forward_layer_batch is the per-token layer run over T tokens with
+    # its GEMVs turned into row x token tiles: every output, and every cache
+    # row, must equal T orc_forward_token calls on that layer bit for bit.
+    # "slot rewritten": token 5 rewrites slot 2, which tokens 2..4 attend to
+    # (the batch must then keep token order through the cache).  T = 37 is not
+    # a multiple of the 32-token tile.
+    H, I, V, nq, layers, head, fnorm, rng = _tiny_forward_model(mode)
+    nslot = 48  # caches of 48 slots: earlier rows random, as _tiny_forward_model fills them
+    for d in layers:
+        d["k_cache"] = np.concatenate([d["k_cache"], d["k_cache"]])
+        d["v_cache"] = np.concatenate([d["v_cache"], d["v_cache"]])
+    T = 37 if case == "in order" else 9
+    slots = list(range(T)) if case == "in order" else [0, 1, 2, 3, 4, 2, 5, 6, 7]
+    clocks = np.arange(100, 100 + T, dtype=np.uint64)
+    actives = [np.unique(np.concatenate([[slots[t]], rng.choice(nslot, 7, replace=False)])).astype(np.uint32)
+               for t in range(T)]
+    X = (rng.standard_normal((T, H)) * 3).astype(np.float32)
+    for li in range(len(layers)):
+        a = _copy_layers(layers)
+        b = _copy_layers(layers)
+        om_a = orc.Model(H, I, V, nq, [a[li]], head, fnorm, layer_mode=_ORC_MODE[mode])
+        om_b = orc.Model(H, I, V, nq, [b[li]], head, fnorm, layer_mode=_ORC_MODE[mode])
+        got = om_a.forward_layer_batch(0, X, clocks, slots, actives, 4)
+        want = np.stack([om_b.forward(X[t], int(clocks[t]), slots[t], actives[t], False, 2)[1]
+                         for t in range(T)])
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (mode, case, li)
+        assert np.array_equal(a[li]["k_cache"], b[li]["k_cache"])
+        assert np.array_equal(a[li]["v_cache"], b[li]["v_cache"])

@@ -53,7 +53,7 @@ FAMILIES = (
 
 
 def run(launches=30):
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "ai-research_amd"))
     import gemma_hip as gh
 
     ctx = gh.Context()

@@ -5,7 +5,7 @@
 // HBM layout: one arena holding, per layer, the concatenated [q | k | v]
 // rows (one GEMV for the three projections), o, gate, up and down in the
 // reference's quant.zig blocks, the norms widened to f32, and the per-layer
-// K/V caches [max_slots ring rows + max_slots prefill staging rows][kv_dim];
+// K/V caches [max_slots ring rows + stage_rows prefill staging rows][kv_dim];
 // then the Q8_0 LM head, the final
 // norm and the activations.  Each forward pass is recorded once as a HIP
 // graph of kernels only -- the ring step, then 6 launches a layer (QKV
@@ -44,6 +44,10 @@ struct Layer {
 };
 
 constexpr size_t kNone = ~(size_t)0;
+// Staging rows per K/V cache (at most max_slots): a prefill batch that
+// overwrites slots it also attends to stages at most this many tokens per
+// chunk.  256 keeps a 640-slot ring's staging at 40% of its ring rows.
+constexpr uint32_t kStageRowsMax = 256;
 constexpr uint32_t kPfGroup = 4;  // tokens per gh_pf_attn_g_* workgroup (PF_GT in attn.hip)
 
 }  // namespace
@@ -74,6 +78,7 @@ struct gh_model {
   uint32_t ring_a = 0, ring_w = 0, ring_r = 0;
   gh_ring* ring = nullptr;  // host mirror of the same state (batched prefill lists)
   uint32_t nsplit = 1, max_q = 0, max_kv = 0;
+  uint32_t stage_rows = 0;  // staging rows after the ring rows of each K/V cache
   size_t hidden_decode = 0;      // where the decode graph leaves the final residual
   size_t hidden_final = 0;       // where the last call left it (kNone: not computed)
   uint16_t* embed_dev = nullptr; // synthetic models only
@@ -196,6 +201,7 @@ gh_status plan(gh_model* m) {
     return o;
   };
   m->layers.clear();
+  m->stage_rows = std::min(c.max_slots, kStageRowsMax);
   for (uint32_t l = 0; l < c.num_hidden_layers; l++) {
     Layer L = layer_shape(c, l);
     if (L.nkv == 0 || c.num_attention_heads % L.nkv || c.num_attention_heads / L.nkv > 4)
@@ -215,10 +221,10 @@ gh_status plan(gh_model* m) {
     L.post_attn = take(H * 4);
     L.pre_ffn = take(H * 4);
     L.post_ffn = take(H * 4);
-    // max_slots ring rows, then max_slots staging rows for a prefill batch
+    // max_slots ring rows, then stage_rows staging rows for a prefill batch
     // whose tokens overwrite slots that earlier tokens of the batch attend to
-    L.k_cache = take((size_t)2 * c.max_slots * L.kv_dim * 4);
-    L.v_cache = take((size_t)2 * c.max_slots * L.kv_dim * 4);
+    L.k_cache = take((size_t)(c.max_slots + m->stage_rows) * L.kv_dim * 4);
+    L.v_cache = take((size_t)(c.max_slots + m->stage_rows) * L.kv_dim * 4);
     m->max_q = std::max(m->max_q, L.q_dim);
     m->max_kv = std::max(m->max_kv, L.kv_dim);
     m->layers.push_back(L);
@@ -1087,10 +1093,10 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
     return forward_token(m, x + (size_t)t * c.hidden_size, 1, clocks[t], slot_idx[t],
                          active + (size_t)t * active_stride, n_active[t], out_token);
   }
-  if (conflict && T > c.max_slots && T > m->seq_prefill_max) {
-    // staged batches hold at most max_slots tokens: consecutive chunks
-    for (uint32_t t0 = 0; t0 < T; t0 += c.max_slots) {
-      const uint32_t n = std::min(T - t0, c.max_slots);
+  if (conflict && T > m->stage_rows && T > m->seq_prefill_max) {
+    // staged batches hold at most stage_rows tokens: consecutive chunks
+    for (uint32_t t0 = 0; t0 < T; t0 += m->stage_rows) {
+      const uint32_t n = std::min(T - t0, m->stage_rows);
       gh_status cs = gh_model_prefill(m, x + (size_t)t0 * c.hidden_size, n, clocks + t0,
                                       slot_idx + t0, active + (size_t)t0 * active_stride,
                                       active_stride, n_active + t0,
@@ -1138,7 +1144,7 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
       }
     active = staged_lists.data();
   }
-  const uint32_t nrows = conflict ? 2 * nslot : nslot;  // cache rows the lists may name
+  const uint32_t nrows = conflict ? nslot + T : nslot;  // cache rows the lists may name
   std::vector<uint32_t> meta(3 * (size_t)T);
   for (uint32_t t = 0; t < T; t++) {
     meta[t] = (uint32_t)clocks[t];

@@ -383,12 +383,14 @@ gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits
  * token's K/V at its slot.  A batch that writes one slot twice, or in which
  * a token's active list holds a slot that a later token of the batch writes
  * (any prompt after the window has wrapped), writes its K/V to staging rows
- * past the ring slots and moves them into the slots after the layers
- * (batches of more than max_slots tokens run as consecutive chunks).  A
- * batch of at most 3 tokens runs token by token through the decode graphs,
- * which is faster at that size (environment GH_PF_SEQ_MAX at model init
- * overrides the 3).  Otherwise the first call allocates the model's prefill
- * buffers for T tokens (not inside graph capture). */
+ * past the ring slots (min(max_slots, 256) per cache) and moves them into
+ * the slots after the layers (longer such batches run as consecutive chunks
+ * of that many tokens).  A batch of at most 3 tokens runs token by token
+ * through the recorded graphs, which is faster at that size (environment
+ * GH_PF_SEQ_MAX at model init overrides the 3).  With layer gating on, a
+ * last token with logits runs the gated decode graph after the others (see
+ * gh_model_set_quiescence).  Otherwise the first call allocates the model's
+ * prefill buffers for T tokens (not inside graph capture). */
 gh_status gh_model_prefill(gh_model *m, const float *x, uint32_t T, const uint64_t *clocks,
                            const uint32_t *slot_idx, const uint32_t *active,
                            uint32_t active_stride, const uint32_t *n_active, int want_logits,

@@ -401,3 +401,47 @@ def test_model_ring_prefill_staged_head_dim_256(gpu, T):
     finally:
         m.close()
         p.close()
+
+
+def test_model_ring_prefill_staged_chunks_below_ring_size(gpu):
+    # A 300-slot cache holds 256 staging rows (min(max_slots, 256)), so a
+    # staged batch of 270 tokens runs as chunks of 256 and 14.  Ring of 4
+    # anchors + 280 window + 16 recall: clocks 0..283 in one batched call (no
+    # slot rewritten), then 270 tokens from clock 284, past the wrap.  Checked
+    # against the oracle token by token and against the GPU's per-token path.
+    cfg = tiny_cfg(layers=2, full_layers=(1,), max_slots=300)
+    m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=8)
+    p = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=8)
+    try:
+        om, layers = oracle_model(m, cfg, gh.QUANT_Q4)
+        for x in (m, p):
+            x.ring_init(4, 280, 16)
+        ring = gh.Ring(1, 4, 280, 16)
+        n0, n1 = 284, 270
+        xs = np.stack([m.embed(i * 29 % cfg.vocab_size) for i in range(n0 + n1)])
+        m.ring_prefill(xs[:n0], 0, False)
+        for c in range(n0):
+            slot = ring.activate_slot(0, c)
+            act = ring.active_slots(0, c)
+            p.forward_clock(xs[c], c, False)
+            om.forward(xs[c], c, slot, act, False, NT)
+        tok = m.ring_prefill(xs[n0:], n0, True)
+        for c in range(n0, n0 + n1):
+            slot = ring.activate_slot(0, c)
+            act = ring.active_slots(0, c)
+            ptok = p.forward_clock(xs[c], c, c == n0 + n1 - 1)
+            rtok, _, rlog = om.forward(xs[c], c, slot, act, c == n0 + n1 - 1, NT)
+        logits = m.read(-1, gh.T_LOGITS, np.float32)
+        plog = p.read(-1, gh.T_LOGITS, np.float32)
+        assert_close(logits, rlog, what="chunked staged prefill logits vs oracle")
+        assert_close(logits, plog, what="chunked staged prefill vs per-token logits")
+        assert tok == orc.argmax(logits) and ptok == orc.argmax(plog)
+        for l, d in enumerate(layers):
+            kvd = d["num_kv_heads"] * d["head_dim"]
+            for t, ref in ((gh.T_K_CACHE, d["k_cache"]), (gh.T_V_CACHE, d["v_cache"])):
+                got = m.read(l, t, np.float32).reshape(cfg.max_slots, kvd)
+                assert_close(got[:284], ref[:284], what="chunked staged cache %d/%d" % (l, t))
+    finally:
+        m.close()
+        p.close()
+

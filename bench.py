@@ -11,7 +11,11 @@ of the K timed steps, recorded once as a HIP graph and replayed, as the decode
 step runs), plus the dominant kernel's roofline (gate+up, its duration from
 HIP events around K back-to-back launches of it alone), the CPU baseline (the
 oracle's restatement of the reference CPU path, timed on this host) and
-secondary figures (single Q4_0 GEMV 8192 x 2048, the 12B-shaped decode).
+secondary figures: the single Q4_0 GEMV 8192 x 2048, the decode attention at
+S = 544 / 640, the Q8_0 LM head + argmax and the 12B-shaped decode, each with
+its own CPU baseline on the same bytes (--no-cpu skips the CPU legs).  The
+`traffic` figures are read from the committed counter passes
+(profiles/traffic.json), not measured in the run.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
 """

@@ -259,8 +259,9 @@ def test_model_prefill_windowed_lists(gpu, shape):
     # 10 slots): within a token group the later tokens drop slots the earlier
     # ones still attend to, so the grouped attention's token masks decide which
     # union entries each token uses; checked against T per-token calls with the
-    # same lists, at 12B width (head_dim 256: the matrix-core kernel) and on the
-    # tiny model (head_dim 64/128: the 4-token vector-ALU kernel); g4 and g1
+    # same lists and against the oracle token by token, at 12B width (head_dim
+    # 256: the matrix-core kernel) and on the tiny model (head_dim 64/128: the
+    # 4-token vector-ALU kernel); g4 and g1
     # are head_dim-256 models with 4 and 1 query heads per kv head, so the
     # matrix-core kernel's 16 columns are 4 tokens x 4 heads and 16 tokens x 1
     if shape == "g4" or shape == "g1":
@@ -278,6 +279,7 @@ def test_model_prefill_windowed_lists(gpu, shape):
     a = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=4)
     b = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=4)
     try:
+        om, layers = oracle_model(a, cfg, gh.QUANT_Q4)
         tokens = np.random.default_rng(13).integers(0, cfg.vocab_size, T)
         xs = np.stack([a.embed(int(t)) for t in tokens])
         slots = list(range(T))
@@ -286,12 +288,16 @@ def test_model_prefill_windowed_lists(gpu, shape):
         a.prefill(xs, np.arange(T), slots, actives, True)
         for c in range(T):
             b.forward(xs[c], c, slots[c], actives[c], c == T - 1)
-        assert_close(a.read(-1, gh.T_LOGITS, np.float32), b.read(-1, gh.T_LOGITS, np.float32),
+            _, _, rlog = om.forward(xs[c], c, slots[c], actives[c], c == T - 1, NT)
+        logits = a.read(-1, gh.T_LOGITS, np.float32)
+        assert_close(logits, rlog, what="windowed prefill logits vs oracle")
+        assert_close(logits, b.read(-1, gh.T_LOGITS, np.float32),
                      what="windowed prefill vs per-token logits")
-        for l in range(cfg.num_hidden_layers):
-            for t in (gh.T_K_CACHE, gh.T_V_CACHE):
+        for l, d in enumerate(layers):
+            for t, ref in ((gh.T_K_CACHE, d["k_cache"]), (gh.T_V_CACHE, d["v_cache"])):
                 ka = a.read(l, t, np.float32).reshape(cfg.max_slots, -1)[slots]
                 kb = b.read(l, t, np.float32).reshape(cfg.max_slots, -1)[slots]
+                assert_close(ka, ref[slots], what="windowed prefill cache %d/%d vs oracle" % (l, t))
                 assert_close(ka, kb, what="windowed prefill vs per-token cache %d/%d" % (l, t))
     finally:
         a.close()

@@ -994,6 +994,22 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   L = (red[0] + red[1]) + (red[2] + red[3]);
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   // weighted column sums: lane -> float4 column, wave -> splits w, w+4, ...
+  if (D4 <= 64 && ns <= ATT_WAVES * MERGE_U) {
+    // one pass (D <= 256, up to 32 splits): the rows loaded first are all
+    // there is, summed straight-line in the order of the general loop below
+    // (0.25 us faster per launch than running that loop once)
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < MERGE_U; u++) {
+      const uint32_t sp = wave + u * ATT_WAVES;
+      const float w = sp < ns ? c[sp] : 0.f;
+      O.x += t0[u].x * w;
+      O.y += t0[u].y * w;
+      O.z += t0[u].z * w;
+      O.w += t0[u].w * w;
+    }
+    if (lane < D4) acc[wave][lane] = O;
+  } else
   for (uint32_t col = lane; col < D4; col += 64) {
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t sp0 = wave; sp0 < ns; sp0 += ATT_WAVES * MERGE_U) {

@@ -248,8 +248,17 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 //   mode 2: xn = (x + r') * s with r' = RMSNorm(r) * wr (r as given when wr
 //           is null); workgroup 0 writes xn to xout (the residual stream);
 //           the GEMV consumes RMSNorm(xn) * w                  (add + norm)
-// Every norm is in * (mean(in^2) + eps)^-1/2 * w, as src/kernels.zig:46-52.
+// Every norm is in * (mean(in^2) + eps)^-1/2 * w, as src/kernels.zig:46-52
+// (which divides 1 by the square root; here v_rsq_f32, within 1 ulp of it).
 // ------------------------------------------------------------------------
+// (mean + eps)^-1/2 of a norm: v_rsq_f32 (1 ulp) instead of the correctly
+// rounded sqrt and divide (about 40 instructions per wavefront, which every
+// wavefront of every workgroup runs on the launch's critical path; with the
+// scale folded below, 0.25 us less per normed stream launch).
+__device__ __forceinline__ float norm_rsqrt(float mean_sq_eps) {
+  return __builtin_amdgcn_rsqf(mean_sq_eps);
+}
+
 // Block-wide sums of NV values per thread; every thread gets the totals.
 // red holds (NT / 64) * NV floats and must not be reused before a barrier.
 template <int NT, int NV>
@@ -355,9 +364,11 @@ __device__ __forceinline__ void pro_finish(const XPro& p, uint32_t K, ProIn& in,
       }
     }
     block_sums<NT, 4>(t, ext);
-    const float c = has_wr ? 1.0f / sqrtf(t[0] / (float)K + p.eps) : 1.0f;
+    const float c = has_wr ? norm_rsqrt(t[0] / (float)K + p.eps) : 1.0f;
     const float pos = t[1] + c * c * t[3];
     float s2 = p.s * p.s * (pos + 2.0f * c * t[2]);
+    // vx becomes x + r' and xn = s (x + r'): the scale s is applied once, in
+    // inv below, except in workgroup 0's residual write
 #pragma unroll
     for (uint32_t u = 0; u < PRO_U; u++) {
       const uint32_t i = u * NT + threadIdx.x;
@@ -369,11 +380,13 @@ __device__ __forceinline__ void pro_finish(const XPro& p, uint32_t K, ProIn& in,
           rv.z = rv.z * c * vwr[u].z;
           rv.w = rv.w * c * vwr[u].w;
         }
-        vx[u].x = (vx[u].x + rv.x) * p.s;
-        vx[u].y = (vx[u].y + rv.y) * p.s;
-        vx[u].z = (vx[u].z + rv.z) * p.s;
-        vx[u].w = (vx[u].w + rv.w) * p.s;
-        if (blockIdx.x == 0) reinterpret_cast<float4*>(p.xout)[i] = vx[u];
+        vx[u].x += rv.x;
+        vx[u].y += rv.y;
+        vx[u].z += rv.z;
+        vx[u].w += rv.w;
+        if (blockIdx.x == 0)
+          reinterpret_cast<float4*>(p.xout)[i] =
+              make_float4(vx[u].x * p.s, vx[u].y * p.s, vx[u].z * p.s, vx[u].w * p.s);
       }
     }
     if (!(s2 > 1e-3f * p.s * p.s * pos)) {  // cancellation (uniform branch): reduce xn^2 itself
@@ -383,9 +396,9 @@ __device__ __forceinline__ void pro_finish(const XPro& p, uint32_t K, ProIn& in,
         if (u * NT + threadIdx.x < n4)
           d[0] += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
       block_sums<NT, 1>(d, ext + 4 * (NT / 64));
-      s2 = d[0];
+      s2 = p.s * p.s * d[0];
     }
-    inv = 1.0f / sqrtf(s2 / (float)K + p.eps);
+    inv = norm_rsqrt(s2 / (float)K + p.eps) * p.s;
   } else {
     float d[1] = {0.f};
 #pragma unroll
@@ -393,7 +406,7 @@ __device__ __forceinline__ void pro_finish(const XPro& p, uint32_t K, ProIn& in,
       if (u * NT + threadIdx.x < n4)
         d[0] += vx[u].x * vx[u].x + vx[u].y * vx[u].y + vx[u].z * vx[u].z + vx[u].w * vx[u].w;
     block_sums<NT, 1>(d, ext);
-    inv = 1.0f / sqrtf(d[0] / (float)K + p.eps);
+    inv = norm_rsqrt(d[0] / (float)K + p.eps);
   }
 #pragma unroll
   for (uint32_t u = 0; u < PRO_U; u++) {
@@ -481,7 +494,7 @@ __device__ __forceinline__ void pro_gate_finish(const XPro& p, uint32_t K, ProGI
   block_sums<NT, 5>(t, ext);
   float s2;
   if (add) {
-    const float c = has_wr ? 1.0f / sqrtf(t[0] / (float)K + p.eps) : 1.0f;
+    const float c = has_wr ? norm_rsqrt(t[0] / (float)K + p.eps) : 1.0f;
     const float pos = t[1] + c * c * t[3];
     s2 = p.s * p.s * (pos + 2.0f * c * t[2]);
 #pragma unroll
@@ -512,7 +525,7 @@ __device__ __forceinline__ void pro_gate_finish(const XPro& p, uint32_t K, ProGI
     for (uint32_t u = 0; u < PRO_U; u++) vx[u] = in.va[u];
     s2 = t[4];
   }
-  const float inv = 1.0f / sqrtf(s2 / (float)K + p.eps);
+  const float inv = norm_rsqrt(s2 / (float)K + p.eps);
 #pragma unroll
   for (uint32_t u = 0; u < PRO_U; u++) {
     const uint32_t i = u * NT + threadIdx.x;

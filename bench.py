@@ -93,11 +93,10 @@ def bench_mlp(ctx, steps, warmup):
         ctx.gemv_q4(dn_copies[i % len(dn_copies)], ACT, OUT, H, I)
 
     def record(n, parts):
-        ctx.graph_begin()
-        for i in range(n):
+        def launch(i):
             for f in parts:
                 f(i)
-        return ctx.graph_end()
+        return record_graph(ctx, launch, n)
 
     # The K steps are recorded once as a HIP graph (how the decode step runs
     # them) and replayed; the warmup is a replay of W steps.
@@ -111,15 +110,15 @@ def bench_mlp(ctx, steps, warmup):
     # graph is replayed, untimed, for CLOCK_WARM_S before the W warm-up steps.
     t_end = time.perf_counter() + CLOCK_WARM_S
     while time.perf_counter() < t_end:
-        ctx.graph_launch(g_warm)
+        replay(ctx, g_warm)
         ctx.sync()
-    ctx.graph_launch(g_warm)
+    replay(ctx, g_warm)
     ctx.sync()
     e0, e1 = ctx.event(), ctx.event()
     # timed region: K steps, synchronized on both sides
     t0 = time.perf_counter()
     ctx.record(e0)
-    ctx.graph_launch(g_step)
+    replay(ctx, g_step)
     ctx.record(e1)
     ctx.sync()
     wall = time.perf_counter() - t0
@@ -128,15 +127,15 @@ def bench_mlp(ctx, steps, warmup):
     # kernel alone, events on the context stream around the replay
     per_kernel = []
     for g in (g_gu, g_dn):
-        ctx.graph_launch(g)
+        replay(ctx, g)
         ctx.sync()
         ctx.record(e0)
-        ctx.graph_launch(g)
+        replay(ctx, g)
         ctx.record(e1)
         ctx.sync()
         per_kernel.append(ctx.elapsed_ms(e0, e1) / steps)
     for g in (g_warm, g_step, g_gu, g_dn):
-        ctx.graph_destroy(g)
+        drop_graph(ctx, g)
     ctx.destroy_event(e0)
     ctx.destroy_event(e1)
     out = OUT.read(np.float32, H)
@@ -199,6 +198,38 @@ def bench_gemv_bf16(ctx, reps=96):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+# --eager: every "graph" below is replayed by launching its kernels again
+# instead of recording a HIP graph.  For kernel tracing only (rocprofv3's
+# kernel tracing of graph replays ends in a segfault inside the profiler);
+# the timings then include the host's launch overhead and are not results.
+EAGER = False
+
+
+def record_graph(ctx, launch, n):
+    """launch(0) .. launch(n - 1) recorded once as a HIP graph (or, with
+    --eager, kept to be launched again at each replay)."""
+    if EAGER:
+        return (launch, n)
+    ctx.graph_begin()
+    for i in range(n):
+        launch(i)
+    return ctx.graph_end()
+
+
+def replay(ctx, g):
+    if EAGER:
+        launch, n = g
+        for i in range(n):
+            launch(i)
+    else:
+        ctx.graph_launch(g)
+
+
+def drop_graph(ctx, g):
+    if not EAGER:
+        ctx.graph_destroy(g)
+
+
 def timed_graph(ctx, launch, reps):
     """Average ms of one launch: `reps` launches recorded once as a graph,
     replayed once untimed, then timed with HIP events on the context stream.
@@ -206,19 +237,16 @@ def timed_graph(ctx, launch, reps):
     scratch, which a capture refuses."""
     launch(0)
     ctx.sync()
-    ctx.graph_begin()
-    for i in range(reps):
-        launch(i)
-    g = ctx.graph_end()
-    ctx.graph_launch(g)
+    g = record_graph(ctx, launch, reps)
+    replay(ctx, g)
     ctx.sync()
     e0, e1 = ctx.event(), ctx.event()
     ctx.record(e0)
-    ctx.graph_launch(g)
+    replay(ctx, g)
     ctx.record(e1)
     ctx.sync()
     ms = ctx.elapsed_ms(e0, e1) / reps
-    ctx.graph_destroy(g)
+    drop_graph(ctx, g)
     ctx.destroy_event(e0)
     ctx.destroy_event(e1)
     return ms
@@ -720,7 +748,12 @@ def main():
                     help="run only the 12B decode leg and print its figures (for profiling)")
     ap.add_argument("--prompt", type=int, default=512, help="decode leg: prompt tokens")
     ap.add_argument("--decode", type=int, default=128, help="decode leg: greedy steps")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch kernels directly instead of replaying HIP graphs (for kernel "
+                         "tracing; the timings then include launch overhead and are not results)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print("bench.py measures one MI355X: the decode backend has no multi-GPU path "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
@@ -829,6 +862,8 @@ def main():
                   "decode_12b": dec},
     }
     ctx.close()
+    if EAGER:
+        line["extra"]["timings"] = "eager launches for kernel tracing: not results"
     print(json.dumps(line), flush=True)
 
 

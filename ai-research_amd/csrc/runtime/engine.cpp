@@ -94,6 +94,14 @@ namespace gh {
 
 gh_status stream_shape(gh_context* ctx, const char* family, const char* var, uint32_t M,
                        uint32_t K, StreamShape* out) {
+  // The Q4 gate+up with x as given runs the normed form's code (its prologue
+  // in mode 0 reads only x, so the results are bit-identical): on MI355X the
+  // 15360 x 3840 stream measured 14.87-14.92 us against 15.44-15.49 us for
+  // the plain form, whose unconditional first loads let x be staged before
+  // they return.  The single-round shapes (8192 x 2048, 8192 x 3840,
+  // 3840 x 4096) measured 0.5-0.7 us slower the same way and keep the plain
+  // form.
+  if (var[0] == '\0' && strcmp(family, "gh_gateup_q4") == 0 && K <= 4u * 4u * 256u) var = "n";
   // 1024-thread variants exist for the plain GEMVs (long rows)
   const bool wide_ok = var[0] == '\0' &&
                        (strcmp(family, "gh_gemv_q4") == 0 || strcmp(family, "gh_gemv_q8") == 0 ||

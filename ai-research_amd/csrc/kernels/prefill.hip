@@ -511,6 +511,249 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 }
 
 // ---------------------------------------------------------------------------
+// Short batches (at most 16 tokens): the weight-streaming GEMM.
+//
+// With a few tokens the tile GEMM above spends each K step on one barrier
+// and one load round trip for a tile that is mostly padding, and reads its
+// weights at 0.8-1.5 TB/s.  Here every wavefront streams its own weight rows,
+// one register set of 16 rows x SB quant blocks in flight while the previous
+// set feeds the matrix cores, and the tokens take the MFMA's other
+// dimension: v_mfma_f32_16x16x32_f16 (or _bf16) with A = 16 tokens x 32 K
+// (the activation halves, as the tile GEMM reads them) and B = 32 K x 16
+// weight rows (one quant block of each row, exact integers), so one MFMA
+// pair (hi, lo) covers one block of 16 rows and the rows' block scales apply
+// to its results.
+//
+// MFMA 16x16x32 operand layout: lane l holds A[l % 16][8 (l / 16) + e] and
+// B[8 (l / 16) + e][l % 16], e = 0..7; result register r of lane l is
+// D[4 (l / 16) + r][l % 16].  So lane group g = l / 16 takes elements
+// 8g .. 8g + 7 of each block (Q4_0: word 1 + g, unpacked in the order the ax
+// layout keeps them), and D holds tokens 4g + r of weight row l % 16: one
+// block scale per lane.
+//
+// A set is loaded as the decode streams load: lane l takes PB consecutive
+// blocks (16-byte loads) of row l / 4, so each row's SB blocks arrive as one
+// contiguous run.  (Loading each lane's MFMA fragment directly, one scale and
+// one word per block from 16 rows 2400 bytes apart, reads at about 1.3 TB/s
+// against 5.4-6.0 TB/s for these runs.)  The wave then writes the set to its
+// own LDS rows (padded so the fragment reads below fall on distinct banks)
+// and reads the fragments back; LDS keeps a wave's operations in order, so
+// no barrier is involved.
+//
+// Workgroup (x, z) owns row groups [4 RGW x, 4 RGW (x + 1)) of 16 rows and
+// K blocks [z KR, z KR + KR) (KR and K / 32 multiples of 4): it stages that
+// slice of the T <= 16 activation rows in LDS once, and wave w then streams
+// row groups w, w + 4, ... with no further barrier.  gridDim.z > 1: plane z of
+// [Z][NMAT][T][N] takes the raw sums times the row scale, as the tile GEMM's
+// split form writes them; gridDim.z = 1: C takes the epilogue.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct SQ4 {  // Q4_0 (src/quant.zig:55-90): {f32 d, 4 words of nibbles}
+  static constexpr uint32_t kBlockBytes = 20;
+  static constexpr int kPB = 4;  // blocks per lane and set (80 bytes)
+  static constexpr bool kBf16 = false;
+  // the fragment of block kb from an LDS row: scale d, word 1 + g as the
+  // fp16 pairs (n_j - 8, n_{j+4} - 8), j = 0..3, as Q4W::ints unpacks it
+  __device__ static half8 frag(const uint8_t* row, uint32_t kb, uint32_t g, float* d) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + kb * kBlockBytes);
+    *d = __uint_as_float(p[0]);
+    const uint32_t w = p[1 + g];
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t pr = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+      o[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, pr) + bias);
+    }
+    return __builtin_bit_cast(half8, o);
+  }
+};
+
+struct SQ8 {  // Q8_0 (src/quant.zig:20-51): {f32 d, 8 words of int8}
+  static constexpr uint32_t kBlockBytes = 36;
+  static constexpr int kPB = 4;  // 144 bytes
+  static constexpr bool kBf16 = false;
+  __device__ static half8 frag(const uint8_t* row, uint32_t kb, uint32_t g, float* d) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(row + kb * kBlockBytes);
+    *d = __uint_as_float(p[0]);
+    const uint32_t w[2] = {p[1 + 2 * g], p[2 + 2 * g]};
+    half8 o;  // q as fp16, in K order
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+      for (int n = 0; n < 4; n++) o[4 * k + n] = (_Float16)(int)(int8_t)((w[k] >> (8 * n)) & 0xFFu);
+    return o;
+  }
+};
+
+struct SBf16 {  // bf16 rows: 32-element segments of 64 bytes, no scale
+  static constexpr uint32_t kBlockBytes = 64;
+  static constexpr int kPB = 2;  // 128 bytes
+  static constexpr bool kBf16 = true;
+  __device__ static half8 frag(const uint8_t* row, uint32_t kb, uint32_t g, float* d) {
+    *d = 1.f;
+    return *reinterpret_cast<const half8*>(row + kb * kBlockBytes + 16 * g);
+  }
+};
+
+template <class F>
+struct SSet {
+  static constexpr int SB = 4 * F::kPB;                          // blocks per set
+  static constexpr int NV = F::kPB * (int)F::kBlockBytes / 16;   // 16-byte loads per lane
+  static constexpr uint32_t RS = SB * F::kBlockBytes + 16;       // LDS row stride (bytes)
+  static constexpr uint32_t kWaveBytes = 16 * RS;                // one matrix's set
+};
+
+template <class F, int NMAT>
+__device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
+                                            const float* __restrict__ rs,
+                                            const uint8_t* __restrict__ W0,
+                                            const uint8_t* __restrict__ W1,
+                                            float* __restrict__ C, uint32_t T, uint32_t N,
+                                            uint32_t K, uint32_t KR, uint32_t RGW) {
+  using S = SSet<F>;
+  constexpr int SB = S::SB, NV = S::NV, PB = F::kPB;
+  extern __shared__ __attribute__((aligned(16))) uint8_t pf_slice[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t g = lane >> 4, li = lane & 15;
+  const uint32_t nb = K / 32, z = blockIdx.z;
+  const uint32_t b0 = z * KR, nk = min(nb - b0, KR);  // the host keeps b0 < nb, 4 | nk
+  const uint32_t stride = KR * 128 + 16;              // bytes per staged token row
+  const size_t row_bytes = (size_t)nb * F::kBlockBytes;
+  const uint32_t kchunks = (nk + SB - 1) / SB;  // sets per row group
+  const uint32_t nchunks = RGW * kchunks;
+  const uint32_t rg0 = blockIdx.x * 4 * RGW + wave;  // row group j of this wave: rg0 + 4 j
+  // this wave's set rows, after the T staged token rows
+  uint8_t* wl = pf_slice + T * stride + wave * NMAT * S::kWaveBytes;
+  // token row of this lane's A fragments: tokens past T read token T - 1
+  // (their D rows are never stored)
+  const uint8_t* al_row = pf_slice + min(li, T - 1) * stride + 16 * g;
+
+  // Set c: row group j = c / kchunks, blocks kb0 .. kb0 + SB - 1 of the
+  // slice.  Lane l loads blocks kb0 + PB (l % 4) .. + PB - 1 of row l / 4
+  // (a piece that starts past the slice loads its last piece instead; those
+  // blocks are skipped).
+  u32x4 ra[NMAT][NV], rb[NMAT][NV];
+  auto load = [&](uint32_t c, u32x4(&r)[NMAT][NV]) {
+    const uint32_t j = c / kchunks, kb0 = (c % kchunks) * SB;
+    uint32_t row = (rg0 + 4 * j) * 16 + lane / 4;
+    row = row < N ? row : N - 1;
+    const uint32_t kb = min(kb0 + PB * (lane % 4), nk - PB);
+    const size_t off = (size_t)row * row_bytes + (size_t)(b0 + kb) * F::kBlockBytes;
+#pragma unroll
+    for (int i = 0; i < NV; i++) r[0][i] = *(gvec_ptr)(W0 + off + 16 * i);
+    if constexpr (NMAT == 2) {
+#pragma unroll
+      for (int i = 0; i < NV; i++) r[1][i] = *(gvec_ptr)(W1 + off + 16 * i);
+    }
+  };
+
+  // the first set is in flight while the slice is staged
+  load(0, ra);
+  {
+    const uint32_t per_row = nk * 8;  // 16-byte chunks of one token's slice
+    const uint32_t total = T * per_row;
+#pragma unroll 4
+    for (uint32_t c = tid; c < total; c += PF_NT) {
+      const uint32_t t = c / per_row, q = c % per_row;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(Ax + (size_t)t * 2 * K + (size_t)b0 * 64 + 8 * q);
+      *reinterpret_cast<u32x4*>(pf_slice + t * stride + 16 * q) = v;
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[NMAT];
+#pragma unroll
+  for (int q = 0; q < NMAT; q++) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto epilogue = [&](uint32_t j) {
+    const uint32_t n = (rg0 + 4 * j) * 16 + li;
+    if (n >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t t = 4 * g + r;
+      if (t >= T) continue;
+      const float sr = rs[t];
+      if (gridDim.z > 1) {
+#pragma unroll
+        for (int q = 0; q < NMAT; q++) C[((size_t)(z * NMAT + q) * T + t) * N + n] = acc[q][r] * sr;
+      } else if constexpr (NMAT == 1) {
+        C[(size_t)t * N + n] = acc[0][r] * sr;
+      } else {
+        C[(size_t)t * N + n] = gelu_tanh(acc[0][r] * sr) * (acc[1][r] * sr);
+      }
+    }
+  };
+
+  auto compute = [&](uint32_t c, const u32x4(&r)[NMAT][NV]) {
+    const uint32_t j = c / kchunks, kb0 = (c % kchunks) * SB;
+    // the set into this wave's LDS rows: lane l's piece at row l / 4
+#pragma unroll
+    for (int q = 0; q < NMAT; q++)
+#pragma unroll
+      for (int i = 0; i < NV; i++)
+        *reinterpret_cast<u32x4*>(wl + q * S::kWaveBytes + (lane / 4) * S::RS +
+                                  (lane % 4) * PB * F::kBlockBytes + 16 * i) = r[q][i];
+#pragma unroll
+    for (int u = 0; u < SB; u++) {
+      const uint32_t kb = kb0 + u;
+      if (kb < nk) {  // uniform over the wave
+        const half8 ah = *reinterpret_cast<const half8*>(al_row + kb * 128);
+        const half8 al = *reinterpret_cast<const half8*>(al_row + kb * 128 + 64);
+#pragma unroll
+        for (int q = 0; q < NMAT; q++) {
+          float d;
+          const half8 b = F::frag(wl + q * S::kWaveBytes + li * S::RS, (uint32_t)u, g, &d);
+          if constexpr (F::kBf16) {
+            f32x4 t = acc[q];
+            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah),
+                                                        __builtin_bit_cast(bf16x8, b), t, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al),
+                                                        __builtin_bit_cast(bf16x8, b), t, 0, 0, 0);
+            acc[q] = t;
+          } else {
+            f32x4 blk = {0.f, 0.f, 0.f, 0.f};
+            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, blk, 0, 0, 0);
+            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, blk, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[q][e] += d * blk[e];
+          }
+        }
+      }
+    }
+    if (c % kchunks == kchunks - 1) {  // the row group's last set
+      epilogue(j);
+#pragma unroll
+      for (int q = 0; q < NMAT; q++) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  for (uint32_t c = 0; c < nchunks; c += 2) {
+    if (c + 1 < nchunks) load(c + 1, rb);
+    compute(c, ra);
+    if (c + 1 < nchunks) {
+      if (c + 2 < nchunks) load(c + 2, ra);
+      compute(c + 1, rb);
+    }
+  }
+}
+
+#define GH_SGEMM(NAME, F, NMAT)                                                              \
+  extern "C" __global__ __launch_bounds__(PF_NT) void NAME(                                 \
+      const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
+      uint32_t T, uint32_t N, uint32_t K, uint32_t KR, uint32_t RGW) {                      \
+    stream_gemm<F, NMAT>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                              \
+  }
+GH_SGEMM(gh_pf_sgemm_q4_k, SQ4, 1)
+GH_SGEMM(gh_pf_sgateup_q4_k, SQ4, 2)
+GH_SGEMM(gh_pf_sgemm_q8_k, SQ8, 1)
+GH_SGEMM(gh_pf_sgateup_q8_k, SQ8, 2)
+GH_SGEMM(gh_pf_sgemm_bf16_k, SBf16, 1)
+GH_SGEMM(gh_pf_sgateup_bf16_k, SBf16, 2)
+
+// ---------------------------------------------------------------------------
 // Row-wise x prologue for T tokens (the batched form of the decode GEMVs'
 // fused norms, src/gpu/model_dispatch.zig:21,32-34,39-41):
 //   mode 1: xn = RMSNorm(x) * w

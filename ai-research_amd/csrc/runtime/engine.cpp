@@ -373,6 +373,75 @@ gh_status launch_attention(gh_context* ctx, const AttnLaunch& L) {
                      0, args);
 }
 
+namespace {
+// The weight-streaming GEMM of a short batch (T <= 16, gh_pf_sgemm_* /
+// gh_pf_sgateup_*): workgroups of 4 waves over 4 RGW row groups of 16 and a
+// K slice of KR quant blocks.  LDS holds the slice's T activation rows (128 KR
+// + 16 bytes each) and each wave's weight set rows (16 rows of SB blocks + 16
+// bytes per matrix: SB = 16 for Q4/Q8, 8 for bf16).  Slices of 16 blocks and
+// about one round of resident workgroups (RGW row groups per wave so that
+// the grid is near the CUs' workgroup slots) measured fastest at the 12B
+// shapes (16 tokens, Q4: QKV 8192 x 3840 at RGW 2, o 3840 x 4096 at 1,
+// gate+up 2 x 15360 x 3840 and down 3840 x 15360 at 4); wider slices (24, 32)
+// and 2-4x the workgroups were slower.  GH_PF_STREAM="kr,rgw" forces both
+// (kr a multiple of 4).
+gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void* W0,
+                                const void* W1, const void* Ax, const float* rs, float* C,
+                                uint32_t T, uint32_t N, uint32_t K, const float** planes,
+                                uint32_t* nplanes) {
+  const bool pair = W1 != nullptr;
+  const uint32_t nmat = pair ? 2u : 1u;
+  const uint32_t nb = K / 32, cus = (uint32_t)ctx->num_cus, rgs = (N + 15) / 16;
+  const uint32_t block_bytes = mode == GH_QUANT_Q8 ? 36u : mode == GH_QUANT_NONE ? 64u : 20u;
+  const uint32_t set_blocks = mode == GH_QUANT_NONE ? 8u : 16u;
+  const uint32_t wave_bytes = 16u * (set_blocks * block_bytes + 16u);
+  auto lds_of = [&](uint32_t kr) { return T * (128u * kr + 16u) + 4u * nmat * wave_bytes; };
+  uint32_t KR = std::min(16u, nb);
+  // workgroups per CU that LDS allows (at most 2: a third measured no faster)
+  const uint32_t per_cu = std::max(1u, std::min(2u, (uint32_t)(ctx->max_lds / lds_of(KR))));
+  const uint32_t slots = per_cu * cus, nz16 = (nb + KR - 1) / KR;
+  uint32_t RGW = (uint32_t)(((uint64_t)rgs * nz16 + 2ull * slots) / (4ull * slots));  // rounded
+  RGW = std::max(1u, std::min(8u, RGW));
+  if (const char* env = getenv("GH_PF_STREAM")) {
+    unsigned kr = 0, rgw = 0;
+    if (sscanf(env, "%u,%u", &kr, &rgw) == 2 && kr >= 4 && kr % 4 == 0 &&
+        lds_of(std::min(kr, nb)) <= ctx->max_lds && rgw >= 1 && rgw <= 8) {
+      KR = std::min(kr, nb);
+      RGW = rgw;
+    }
+  }
+  const uint32_t nz = (nb + KR - 1) / KR;
+  if (nz > 64) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: more than 64 K slices");
+  const unsigned lds = lds_of(KR);
+  if (lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: stream slice exceeds LDS");
+  const std::string name = std::string(pair ? "gh_pf_sgateup_" : "gh_pf_sgemm_") +
+                           (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
+                           "_k";
+  float* out = C;
+  if (nz > 1) {
+    const size_t need = (size_t)nz * nmat * T * N * sizeof(float);
+    gh_status st = ctx->ensure_zeroed(&ctx->gemm_scratch, &ctx->gemm_scratch_bytes, need);
+    if (st != GH_OK) return st;
+    out = static_cast<float*>(ctx->gemm_scratch);
+  }
+  const void* W1a = pair ? W1 : W0;
+  void* args[] = {const_cast<void**>(&Ax), const_cast<float**>(&rs), const_cast<void**>(&W0),
+                  const_cast<void**>(&W1a), &out, &T, &N, &K, &KR, &RGW};
+  const dim3 grid((rgs + 4 * RGW - 1) / (4 * RGW), 1, nz);
+  gh_status st = ctx->launch(name, grid, dim3(256), lds, args);
+  if (planes) {
+    *planes = nz > 1 ? out : C;
+    *nplanes = nz;
+  }
+  if (st != GH_OK || nz == 1 || planes) return st;
+  const uint64_t tn = (uint64_t)T * N;
+  const unsigned rgrid = (unsigned)std::min<uint64_t>((tn + 255) / 256, 4ull * cus);
+  uint32_t nzz = nz;
+  void* rargs[] = {&out, &C, &T, &N, &nzz, const_cast<uint32_t*>(&nmat)};
+  return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
+}
+}  // namespace
+
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
                                     const void* W1, const void* Ax, const float* rs, float* C,
                                     uint32_t T, uint32_t N, uint32_t K, const float** planes,
@@ -391,6 +460,12 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                 "(16-byte for bf16 rows)");
   const bool pair = W1 != nullptr;
   if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
+  // Short batches stream the weights (16-byte pieces of 4-block runs: K a
+  // multiple of 128, rows 16-byte aligned)
+  if (T <= 16 && K % 128 == 0 && !((reinterpret_cast<uintptr_t>(W0) |
+                                    reinterpret_cast<uintptr_t>(pair ? W1 : W0)) & 15) &&
+      getenv("GH_PF_NO_STREAM") == nullptr)
+    return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes);
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
   // products of at least 128 tokens) when splitting K lifts it to that

@@ -104,11 +104,12 @@ struct gh_model {
   // gh_qgate_k launch instead of gating in their QKV stream's prologue
   bool qgate_kernel = false;
   // A prompt of at most this many tokens runs token by token through the
-  // decode graphs: at the 12B shape 1-3 tokens take 2.6 / 5.1 / 7.5 ms that
-  // way against 8.6-8.7 ms for one batched call (whose tiles are at least 64
-  // rows), and 4 tokens 9.9 against 8.8.  GH_PF_SEQ_MAX (read at init)
-  // overrides it; 0 sends every prompt to the batched kernels.
-  uint32_t seq_prefill_max = 3;
+  // decode graphs: at the 12B shape (Q4) 1-2 tokens take 2.6 / 5.1 ms that
+  // way against 5.8 / 6.0 ms for one batched call (whose projections stream
+  // the weights once for all tokens), and 3 tokens 7.5 against 6.1.
+  // GH_PF_SEQ_MAX (read at init) overrides it; 0 sends every prompt to the
+  // batched kernels.
+  uint32_t seq_prefill_max = 2;
   // layer gating (quiescence): layers >= num_layers / 3 are gated when on
   bool q_on = false;
   float q_thr = 0.f;

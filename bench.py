@@ -599,7 +599,7 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
             times.append(time.perf_counter() - t0)
             c += T
         wrapped[str(T)] = round(sorted(times)[1] * 1e3, 2)
-    # short first-turn prompts (clocks from 0, after the run): 1-3 tokens go
+    # short first-turn prompts (clocks from 0, after the run): 1-2 tokens go
     # token by token through the decode graphs, longer ones to the batched
     # kernels; median of 3 calls each
     short = {}

@@ -130,13 +130,69 @@ def test_prefill_gemm_weight_scale_range(gpu):
         assert_close(got[:, n], ref[:, n], what="prefill GEMM weight row %d" % n)
 
 
+# Batches of at most 16 tokens with K a multiple of 128 run the
+# weight-streaming GEMM (the tokens on the 16x16x32 MFMA, K in slices staged
+# in LDS, the slices' planes added in order).  One token; 16; a ragged N; the
+# 12B K values (3840, 4096, 15360); K of four quant blocks (one slice, a
+# partial weight set).  17 tokens and K = 160 take the tile GEMM.
+STREAM_SHAPES = [(1, 64, 128), (4, 100, 3840), (16, 256, 4096), (13, 96, 15360), (16, 48, 2048),
+                 (9, 512, 128), (17, 96, 3840), (6, 40, 160)]
+
+
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
+@pytest.mark.parametrize("T,N,K", STREAM_SHAPES)
+def test_prefill_stream_gemm(gpu, mode, T, N, K):
+    wq, deq = quantized(N, K, mode, 360 + T)
+    a = gh.synth_normal(T * K, 1, 361, 0.0, 1.0).reshape(T, K)
+    W, A, C = gpu.upload(wq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gemm(mode, W, A, C, T, N, K)
+    got = C.read(np.float32, T * N).reshape(T, N)
+    assert_close(got, np.asarray(a, np.float64) @ deq.T, what="streamed prefill GEMM")
+
+
+@pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
+@pytest.mark.parametrize("T,N,K", [(3, 200, 3840), (16, 64, 1024), (11, 16, 15360)])
+def test_prefill_stream_gate_up(gpu, mode, T, N, K):
+    gq, gdeq = quantized(N, K, mode, 370)
+    uq, udeq = quantized(N, K, mode, 371)
+    a = gh.synth_normal(T * K, 1, 372, 0.0, 1.0).reshape(T, K)
+    Wg, Wu, A, act = gpu.upload(gq), gpu.upload(uq), gpu.upload(a), gpu.alloc(T * N * 4)
+    gpu.prefill_gate_up_geglu(mode, Wg, Wu, A, act, T, N, K)
+    got = act.read(np.float32, T * N).reshape(T, N)
+    a64 = np.asarray(a, np.float64)
+    assert_close(got, nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T), what="streamed prefill GeGLU")
+
+
+@pytest.mark.parametrize("T", [7, 16])
+@pytest.mark.parametrize("shape", ["8,1", "16,2", "4,3", "4,8", "24,1", "32,2", "12,2"])
+def test_prefill_stream_slices(gpu, monkeypatch, T, shape):
+    # forced slice widths (KR quant blocks: 32 blocks of K in 1, 2, 3, 4 or 8
+    # slices; 24 and 12 leave an uneven last slice, and 12 and 4 a partial
+    # weight set) and row groups per wave (8: waves whose rows all lie past N)
+    T_, N, K = T, 300, 1024
+    monkeypatch.setenv("GH_PF_STREAM", shape)
+    gq, gdeq = quantized(N, K, gh.QUANT_Q4, 380)
+    uq, udeq = quantized(N, K, gh.QUANT_Q4, 381)
+    a = gh.synth_normal(T_ * K, 1, 382, 0.0, 1.0).reshape(T_, K)
+    A, C = gpu.upload(a), gpu.alloc(T_ * N * 4)
+    a64 = np.asarray(a, np.float64)
+    gpu.prefill_gemm(gh.QUANT_Q4, gpu.upload(gq), A, C, T_, N, K)
+    assert_close(C.read(np.float32, T_ * N).reshape(T_, N), a64 @ gdeq.T,
+                 what="streamed GEMM, slices %s" % shape)
+    gpu.prefill_gate_up_geglu(gh.QUANT_Q4, gpu.upload(gq), gpu.upload(uq), A, C, T_, N, K)
+    assert_close(C.read(np.float32, T_ * N).reshape(T_, N),
+                 nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T), what="streamed GeGLU, slices %s" % shape)
+
+
 @pytest.mark.parametrize("pair", [False, True])
 @pytest.mark.parametrize("split", ["1", "3", "200"])
 def test_prefill_split_k(gpu, monkeypatch, pair, split):
-    # a few tokens: the split-K forms (forced 1 = unsplit, 3 = an even split
-    # of 120 K steps, 200 = clamped to the 64-split cap, so one or two K steps
-    # per split) against the product
+    # a few tokens on the tile GEMM (the streaming form switched off): the
+    # split-K forms (forced 1 = unsplit, 3 = an even split of 120 K steps,
+    # 200 = clamped to the 64-split cap, so one or two K steps per split)
+    # against the product
     T, N, K = 5, 320, 3840
+    monkeypatch.setenv("GH_PF_NO_STREAM", "1")
     monkeypatch.setenv("GH_PF_SPLIT", split)
     gq, gdeq = quantized(N, K, gh.QUANT_Q4, 320)
     uq, udeq = quantized(N, K, gh.QUANT_Q4, 321)
@@ -181,15 +237,16 @@ def ring_lists(ring, clocks):
 @pytest.mark.parametrize("mode,T,dup,seq_max", [
     (gh.QUANT_Q4, 12, False, None), (gh.QUANT_Q8, 12, False, None), (gh.QUANT_Q4, 11, False, None),
     (gh.QUANT_Q8, 9, True, None), (gh.QUANT_Q4, 3, False, None), (gh.QUANT_Q8, 2, False, None),
-    (gh.QUANT_Q4, 3, False, "0"), (gh.QUANT_Q4, 1, False, "0")])
+    (gh.QUANT_Q4, 3, False, "0"), (gh.QUANT_Q4, 1, False, "0"), (gh.QUANT_Q4, 3, False, "3")])
 def test_model_prefill_matches_sequential_oracle(gpu, monkeypatch, mode, T, dup, seq_max):
     # T prompt tokens (4 anchors, then the window), one batch, then decode
     # steps through the per-token graph on the caches the prefill wrote.  T
     # not a multiple of 4 leaves a partial token group in the grouped
     # attention; dup names one slot twice in the last token's list (counted
     # twice, as the reference's loop over the list does), which keeps the
-    # batch on the per-token attention kernel.  Batches of 1-3 tokens run
+    # batch on the per-token attention kernel.  Batches of 1-2 tokens run
     # token by token unless GH_PF_SEQ_MAX=0 keeps them on the batched kernels
+    # (GH_PF_SEQ_MAX=3 sends 3 tokens token by token)
     if seq_max is not None:
         monkeypatch.setenv("GH_PF_SEQ_MAX", seq_max)
     cfg = tiny_cfg()

@@ -104,11 +104,13 @@ struct gh_model {
   // gh_qgate_k launch instead of gating in their QKV stream's prologue
   bool qgate_kernel = false;
   // A prompt of at most this many tokens runs token by token through the
-  // decode graphs: at the 12B shape (Q4) 1-2 tokens take 2.6 / 5.1 ms that
+  // decode graphs: at the 12B shape in Q4, 1-2 tokens take 2.6 / 5.1 ms that
   // way against 5.8 / 6.0 ms for one batched call (whose projections stream
-  // the weights once for all tokens), and 3 tokens 7.5 against 6.1.
-  // GH_PF_SEQ_MAX (read at init) overrides it; 0 sends every prompt to the
-  // batched kernels.
+  // the weights once for all tokens), and 3 tokens 7.5 against 6.1.  Q8 and
+  // bf16 decode steps take 3.7 and 5.0 ms, and one batched call 6.9 and
+  // 8.3 ms, so there only a single token runs that way.  Set at init from the
+  // weight mode; GH_PF_SEQ_MAX (read at init) overrides it, and 0 sends every
+  // prompt to the batched kernels.
   uint32_t seq_prefill_max = 2;
   // layer gating (quiescence): layers >= num_layers / 3 are gated when on
   bool q_on = false;
@@ -595,6 +597,7 @@ gh_status finish_init(gh_model* m, gh_model** out) {
   m->eager = eager && eager[0] == '1';
   const char* qk = getenv("GH_QGATE_KERNEL");
   m->qgate_kernel = qk && qk[0] == '1';
+  m->seq_prefill_max = m->mode == GH_QUANT_Q4 ? 2u : 1u;
   if (const char* sq = getenv("GH_PF_SEQ_MAX")) m->seq_prefill_max = (uint32_t)strtoul(sq, nullptr, 10);
   gh_status st = reset_gates(m);
   if (st == GH_OK) st = record_graphs(m);

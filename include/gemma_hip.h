@@ -385,9 +385,10 @@ gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits
  * (any prompt after the window has wrapped), writes its K/V to staging rows
  * past the ring slots (min(max_slots, 256) per cache) and moves them into
  * the slots after the layers (longer such batches run as consecutive chunks
- * of that many tokens).  A batch of at most 2 tokens runs token by token
- * through the recorded graphs, which is faster at that size (environment
- * GH_PF_SEQ_MAX at model init overrides the 2).  With layer gating on, a
+ * of that many tokens).  A batch of at most 2 tokens (Q4 weights) or 1
+ * token (Q8, bf16) runs token by token through the recorded graphs, which is
+ * faster at that size (environment GH_PF_SEQ_MAX at model init overrides
+ * it).  With layer gating on, a
  * last token with logits runs the gated decode graph after the others (see
  * gh_model_set_quiescence).  Otherwise the first call allocates the model's
  * prefill buffers for T tokens (not inside graph capture). */

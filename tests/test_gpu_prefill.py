@@ -237,16 +237,18 @@ def ring_lists(ring, clocks):
 @pytest.mark.parametrize("mode,T,dup,seq_max", [
     (gh.QUANT_Q4, 12, False, None), (gh.QUANT_Q8, 12, False, None), (gh.QUANT_Q4, 11, False, None),
     (gh.QUANT_Q8, 9, True, None), (gh.QUANT_Q4, 3, False, None), (gh.QUANT_Q8, 2, False, None),
-    (gh.QUANT_Q4, 3, False, "0"), (gh.QUANT_Q4, 1, False, "0"), (gh.QUANT_Q4, 3, False, "3")])
+    (gh.QUANT_Q4, 3, False, "0"), (gh.QUANT_Q4, 1, False, "0"), (gh.QUANT_Q4, 3, False, "3"),
+    (gh.QUANT_Q8, 1, False, None)])
 def test_model_prefill_matches_sequential_oracle(gpu, monkeypatch, mode, T, dup, seq_max):
     # T prompt tokens (4 anchors, then the window), one batch, then decode
     # steps through the per-token graph on the caches the prefill wrote.  T
     # not a multiple of 4 leaves a partial token group in the grouped
     # attention; dup names one slot twice in the last token's list (counted
     # twice, as the reference's loop over the list does), which keeps the
-    # batch on the per-token attention kernel.  Batches of 1-2 tokens run
-    # token by token unless GH_PF_SEQ_MAX=0 keeps them on the batched kernels
-    # (GH_PF_SEQ_MAX=3 sends 3 tokens token by token)
+    # batch on the per-token attention kernel.  Batches of 1-2 tokens (Q4;
+    # 1 token with Q8 weights) run token by token unless GH_PF_SEQ_MAX=0 keeps
+    # them on the batched kernels (GH_PF_SEQ_MAX=3 sends 3 tokens token by
+    # token)
     if seq_max is not None:
         monkeypatch.setenv("GH_PF_SEQ_MAX", seq_max)
     cfg = tiny_cfg()

@@ -872,25 +872,32 @@ extern "C" __global__ __launch_bounds__(64) void gh_pf_qkv_rope_k(AttnArgs a,
 }
 
 // The same for head_dim 256, one workgroup per token (grid (tokens), 256
-// threads): a token's head rows are jobs -- query heads [0, nq), key heads
-// [nq, nq + nkv), value heads after them -- and wave w takes jobs w, w + 4, ...
-// Every job's row (4 floats per lane) loads before any is used, the RoPE
-// angles are computed once per wave rather than once per head, and each head
-// is normalised in registers, rotated through the wave's LDS row
-// (rope_lds), and stored: q to a.q, k and v into the caches at slots[t].
-// With a.nplanes >= 1 the rows are the QKV GEMM's unsummed K-split planes,
-// added in plane order as they load (each plane's rows all in flight at once).
-#define PFR_JOBS 16  // jobs per wave: nq + 2 nkv <= 64
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs a,
-                                                                      const uint32_t* clocks,
-                                                                      const uint32_t* slots) {
+// threads, gridDim.y of them per token): a token's head rows are jobs --
+// query heads [0, nq), key heads [nq, nq + nkv), value heads after them --
+// and wave w of workgroup (t, y) takes jobs w + 4 (y + G i), i = 0, 1, ...
+// (G = gridDim.y, at most JOBS per wave).  Every job's row (4 floats per
+// lane) loads before any is used, the RoPE angles are computed once per wave
+// rather than once per head, and each head is normalised in registers,
+// rotated through the wave's LDS row (rope_lds), and stored: q to a.q, k and
+// v into the caches at slots[t].  With a.nplanes >= 1 the rows are the QKV
+// GEMM's unsummed K-split planes, added in plane order as they load, PLANES
+// planes in flight at a time.
+// Two forms: one workgroup per token (JOBS 16, G = 1: a long prompt's tokens
+// fill the CUs), and for a few tokens ceil((nq + 2 nkv) / 8) workgroups per
+// token with 8 planes in flight (JOBS 2): at 16 tokens and 8 planes the
+// first form took 12.6 us per layer and the second 6.0, at 512 tokens and 2
+// planes 12.8 against 15.9 us.
+template <int JOBS, int PLANES>
+__device__ __forceinline__ void pf_qkv_rope4(const AttnArgs& a, const uint32_t* clocks,
+                                             const uint32_t* slots) {
   __shared__ float hb[ATT_WAVES][256];
   const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t clock = clocks[t], slot = slots[t];
   float* row = const_cast<float*>(a.q) + (size_t)t * a.q_stride;
   const float* srow = a.nplanes ? a.q_planes + (size_t)t * a.q_stride : row;
   const uint32_t nq = a.nq, nkv = a.nkv, njobs = nq + 2 * nkv;
-  const uint32_t per = (njobs + ATT_WAVES - 1) / ATT_WAVES;  // the same for every wave
+  const uint32_t jstride = ATT_WAVES * gridDim.y, j0 = wave + ATT_WAVES * blockIdx.y;
+  const uint32_t per = (njobs + jstride - 1) / jstride;  // the same for every wave
   const size_t q_dim = (size_t)nq * 256, kv_dim = (size_t)nkv * 256;
   auto src = [&](uint32_t j) -> size_t {  // offset of job j's row in a token row
     if (j < nq) return (size_t)j * 256;
@@ -898,23 +905,31 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs 
     return (a.k_eq_v ? q_dim : q_dim + kv_dim) + (size_t)(j - nq - nkv) * 256;
   };
   const uint32_t d0 = lane * 4;
-  float4 v[PFR_JOBS];
+  float4 v[JOBS];
 #pragma unroll
-  for (int i = 0; i < PFR_JOBS; i++) {
-    const uint32_t j = min(wave + ATT_WAVES * (uint32_t)i, njobs - 1);
+  for (int i = 0; i < JOBS; i++) {
+    const uint32_t j = min(j0 + jstride * (uint32_t)i, njobs - 1);
     v[i] = *reinterpret_cast<const float4*>(srow + src(j) + d0);
   }
-  for (uint32_t p = 1; p < a.nplanes; p++) {  // uniform
-    const float* prow = srow + (size_t)p * a.plane_stride;
-    float4 w[PFR_JOBS];
+  for (uint32_t p = 1; p < a.nplanes; p += PLANES) {  // uniform
+    float4 w[PLANES][JOBS];
 #pragma unroll
-    for (int i = 0; i < PFR_JOBS; i++) {
-      const uint32_t j = min(wave + ATT_WAVES * (uint32_t)i, njobs - 1);
-      w[i] = *reinterpret_cast<const float4*>(prow + src(j) + d0);
+    for (int u = 0; u < PLANES; u++) {
+      const float* prow = srow + (size_t)min(p + u, a.nplanes - 1) * a.plane_stride;
+#pragma unroll
+      for (int i = 0; i < JOBS; i++) {
+        const uint32_t j = min(j0 + jstride * (uint32_t)i, njobs - 1);
+        w[u][i] = *reinterpret_cast<const float4*>(prow + src(j) + d0);
+      }
     }
 #pragma unroll
-    for (int i = 0; i < PFR_JOBS; i++)
-      v[i] = make_float4(v[i].x + w[i].x, v[i].y + w[i].y, v[i].z + w[i].z, v[i].w + w[i].w);
+    for (int u = 0; u < PLANES; u++)
+      if (p + u < a.nplanes) {  // uniform
+#pragma unroll
+        for (int i = 0; i < JOBS; i++)
+          v[i] = make_float4(v[i].x + w[u][i].x, v[i].y + w[u][i].y, v[i].z + w[u][i].z,
+                             v[i].w + w[u][i].w);
+      }
   }
   const float4 one = make_float4(1.f, 1.f, 1.f, 1.f);  // a missing norm weight
   const float4 wq = a.q_norm ? *reinterpret_cast<const float4*>(a.q_norm + d0) : one;
@@ -923,9 +938,9 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs 
   rope_angles(a.rot, a.theta, clock, lane, rc, rsn);
   float* h = hb[wave];
 #pragma unroll
-  for (int i = 0; i < PFR_JOBS; i++) {
+  for (int i = 0; i < JOBS; i++) {
     if ((uint32_t)i < per) {  // per is the same for the whole workgroup
-      const uint32_t j = wave + ATT_WAVES * (uint32_t)i;
+      const uint32_t j = j0 + jstride * (uint32_t)i;
       const bool isq = j < nq, isk = !isq && j < nq + nkv;
       const float4 x = v[i];
       const float ss = wave_allsum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
@@ -945,6 +960,16 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs 
       }
     }
   }
+}
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_k(AttnArgs a,
+                                                                      const uint32_t* clocks,
+                                                                      const uint32_t* slots) {
+  pf_qkv_rope4<16, 1>(a, clocks, slots);
+}
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_s_k(AttnArgs a,
+                                                                        const uint32_t* clocks,
+                                                                        const uint32_t* slots) {
+  pf_qkv_rope4<2, 8>(a, clocks, slots);
 }
 
 // Combine the split partials of one query head:

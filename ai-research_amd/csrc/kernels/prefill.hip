@@ -821,12 +821,19 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
   load8(w, wv);
   load8(wrp, wrv);
   if (add) {
+    // planes 1 .. rz - 1, 8 in flight at a time (clamped indices), added in
+    // plane order
     const size_t plane = (size_t)gridDim.x * H;
-    for (uint32_t z = 1; z < rz; z++) {
-      float pv[8];
-      load8(r + z * plane, pv);
+    for (uint32_t z = 1; z < rz; z += 8) {
+      float pv[8][8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) rv[k] += pv[k];
+      for (int u = 0; u < 8; u++) load8(r + (size_t)min(z + u, rz - 1) * plane, pv[u]);
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (z + u < rz) {  // uniform
+#pragma unroll
+          for (int k = 0; k < 8; k++) rv[k] += pv[u][k];
+        }
     }
     float ss = 0.f;
 #pragma unroll

@@ -1448,10 +1448,14 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     a.plane_stride = (uint64_t)T * L.qkv_rows;
     {
       void* args[] = {&a, &clocks, &slots};
-      // head_dim 256: one workgroup per token (angles once per wave); else one
-      // wavefront per (head, token)
-      st = rope4 ? ctx->launch("gh_pf_qkv_rope4_k", dim3(T), dim3(256), 0, args)
-                 : ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args);
+      // head_dim 256: one workgroup per token (angles once per wave), or for
+      // fewer tokens than CUs ceil(jobs / 8) per token; else one wavefront
+      // per (head, token)
+      const bool few = T < (uint32_t)ctx->num_cus;
+      st = !rope4 ? ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args)
+           : few  ? ctx->launch("gh_pf_qkv_rope4_s_k", dim3(T, (a.nq + 2 * a.nkv + 7) / 8),
+                                dim3(256), 0, args)
+                  : ctx->launch("gh_pf_qkv_rope4_k", dim3(T), dim3(256), 0, args);
       if (st != GH_OK) return st;
     }
     {

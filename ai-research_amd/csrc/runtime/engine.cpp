@@ -534,6 +534,17 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
 }
 
+gh_status launch_prefill_plane_sum(gh_context* ctx, const float* planes, float* C, uint32_t T,
+                                   uint32_t N, uint32_t nplanes) {
+  if (!planes || !C || T == 0 || N == 0 || nplanes == 0)
+    return fail(GH_ERR_INVALID, "prefill plane sum: null pointer or zero size");
+  const uint64_t tn = (uint64_t)T * N;
+  const unsigned rgrid = (unsigned)std::min<uint64_t>((tn + 255) / 256, 4ull * ctx->num_cus);
+  uint32_t one = 1;
+  void* rargs[] = {const_cast<float**>(&planes), &C, &T, &N, &nplanes, &one};
+  return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
+}
+
 // f32 A: split into fp16 hi/lo halves with a power-of-two scale per row
 // (gh_pf_halves_k, once per row rather than in every tile that reads it),
 // then the GEMM.

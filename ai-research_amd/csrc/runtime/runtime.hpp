@@ -115,6 +115,10 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                     const void* W1, const void* Ax, const float* rs, float* C,
                                     uint32_t T, uint32_t N, uint32_t K,
                                     const float** planes = nullptr, uint32_t* nplanes = nullptr);
+// C [T][N] = the sum of nplanes K-split planes ([nplanes][T][N]) in plane
+// order (gh_pf_splitk_k, spread over the CUs).
+gh_status launch_prefill_plane_sum(gh_context* ctx, const float* planes, float* C, uint32_t T,
+                                   uint32_t N, uint32_t nplanes);
 // The A-operand halves a prefill GEMM of this weight mode reads (gh_pf_norm_k
 // and gh_pf_halves_k): 1 = fp16 in the Q4 unpacking's K order (Q4_0),
 // 0 = fp16 in K order (Q8_0), 2 = bf16 in K order (bf16 rows).

@@ -546,6 +546,12 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 // row groups w, w + 4, ... with no further barrier.  gridDim.z > 1: plane z of
 // [Z][NMAT][T][N] takes the raw sums times the row scale, as the tile GEMM's
 // split form writes them; gridDim.z = 1: C takes the epilogue.
+//
+// AF (the o and down inputs, and the kernel-level f32 entry points): A comes
+// as f32 rows, and the staging splits each token's slice itself, with a
+// power-of-two scale of its own (row_scale of the slice's largest |a|, 16
+// threads per token); plane z then carries that scale instead of the row's.
+// This saves the separate split launch (gh_pf_halves_k).
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -553,6 +559,7 @@ struct SQ4 {  // Q4_0 (src/quant.zig:55-90): {f32 d, 4 words of nibbles}
   static constexpr uint32_t kBlockBytes = 20;
   static constexpr int kPB = 4;  // blocks per lane and set (80 bytes)
   static constexpr bool kBf16 = false;
+  static constexpr uint32_t kFmt = 1;  // pf_store_group format of the A halves
   // the fragment of block kb from an LDS row: scale d, word 1 + g as the
   // fp16 pairs (n_j - 8, n_{j+4} - 8), j = 0..3, as Q4W::ints unpacks it
   __device__ static half8 frag(const uint8_t* row, uint32_t kb, uint32_t g, float* d) {
@@ -575,6 +582,7 @@ struct SQ8 {  // Q8_0 (src/quant.zig:20-51): {f32 d, 8 words of int8}
   static constexpr uint32_t kBlockBytes = 36;
   static constexpr int kPB = 4;  // 144 bytes
   static constexpr bool kBf16 = false;
+  static constexpr uint32_t kFmt = 0;
   __device__ static half8 frag(const uint8_t* row, uint32_t kb, uint32_t g, float* d) {
     const uint32_t* p = reinterpret_cast<const uint32_t*>(row + kb * kBlockBytes);
     *d = __uint_as_float(p[0]);
@@ -592,6 +600,7 @@ struct SBf16 {  // bf16 rows: 32-element segments of 64 bytes, no scale
   static constexpr uint32_t kBlockBytes = 64;
   static constexpr int kPB = 2;  // 128 bytes
   static constexpr bool kBf16 = true;
+  static constexpr uint32_t kFmt = 2;
   __device__ static half8 frag(const uint8_t* row, uint32_t kb, uint32_t g, float* d) {
     *d = 1.f;
     return *reinterpret_cast<const half8*>(row + kb * kBlockBytes + 16 * g);
@@ -606,7 +615,9 @@ struct SSet {
   static constexpr uint32_t kWaveBytes = 16 * RS;                // one matrix's set
 };
 
-template <class F, int NMAT>
+#define PF_SLICE_MAX 32  // quant blocks per K slice (the AF staging holds 8 groups per thread)
+
+template <class F, int NMAT, bool AF>
 __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
                                             const float* __restrict__ rs,
                                             const uint8_t* __restrict__ W0,
@@ -652,7 +663,47 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
 
   // the first set is in flight while the slice is staged
   load(0, ra);
-  {
+  __shared__ float slice_scale[16];  // AF: each token's scale for this slice
+  if constexpr (AF) {
+    // 16 threads per token; thread `sub` takes 8-element groups sub, sub + 16,
+    // ... of the slice (nk / 4 of them: nk is a multiple of 4)
+    const float* A = reinterpret_cast<const float*>(Ax);
+    const uint32_t t = tid >> 4, sub = tid & 15, per = nk / 4;
+    const bool on = t < T;
+    const float* src = A + (size_t)min(t, T - 1) * K + (size_t)b0 * 32;
+    float xv[PF_SLICE_MAX / 4][8];
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < PF_SLICE_MAX / 4; i++) {
+      if ((uint32_t)i < per) {
+        const float4 a = *reinterpret_cast<const float4*>(src + 8 * (sub + 16 * i));
+        const float4 b = *reinterpret_cast<const float4*>(src + 8 * (sub + 16 * i) + 4);
+        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
+#pragma unroll
+        for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(xv[i][k]));
+      }
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float inv;
+    const float sc = row_scale(m, &inv);
+    if (on) {
+#pragma unroll
+      for (int i = 0; i < PF_SLICE_MAX / 4; i++) {
+        if ((uint32_t)i < per) {
+          const uint32_t gi = sub + 16 * i;  // group gi: block gi / 4, part gi % 4
+          float y[8];
+#pragma unroll
+          for (int k = 0; k < 8; k++) y[k] = xv[i][k] * inv;
+          pf_store_group(y, F::kFmt,
+                         reinterpret_cast<_Float16*>(pf_slice + t * stride + (gi >> 2) * 128 +
+                                                     (gi & 3) * 16));
+        }
+      }
+      if (sub == 0) slice_scale[t] = sc;
+    }
+  } else {
     const uint32_t per_row = nk * 8;  // 16-byte chunks of one token's slice
     const uint32_t total = T * per_row;
 #pragma unroll 4
@@ -675,7 +726,7 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
     for (int r = 0; r < 4; r++) {
       const uint32_t t = 4 * g + r;
       if (t >= T) continue;
-      const float sr = rs[t];
+      const float sr = AF ? slice_scale[t] : rs[t];
       if (gridDim.z > 1) {
 #pragma unroll
         for (int q = 0; q < NMAT; q++) C[((size_t)(z * NMAT + q) * T + t) * N + n] = acc[q][r] * sr;
@@ -740,18 +791,24 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   }
 }
 
-#define GH_SGEMM(NAME, F, NMAT)                                                              \
+#define GH_SGEMM(NAME, F, NMAT, AF)                                                          \
   extern "C" __global__ __launch_bounds__(PF_NT) void NAME(                                 \
       const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
       uint32_t T, uint32_t N, uint32_t K, uint32_t KR, uint32_t RGW) {                      \
-    stream_gemm<F, NMAT>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                              \
+    stream_gemm<F, NMAT, AF>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                          \
   }
-GH_SGEMM(gh_pf_sgemm_q4_k, SQ4, 1)
-GH_SGEMM(gh_pf_sgateup_q4_k, SQ4, 2)
-GH_SGEMM(gh_pf_sgemm_q8_k, SQ8, 1)
-GH_SGEMM(gh_pf_sgateup_q8_k, SQ8, 2)
-GH_SGEMM(gh_pf_sgemm_bf16_k, SBf16, 1)
-GH_SGEMM(gh_pf_sgateup_bf16_k, SBf16, 2)
+GH_SGEMM(gh_pf_sgemm_q4_k, SQ4, 1, false)
+GH_SGEMM(gh_pf_sgateup_q4_k, SQ4, 2, false)
+GH_SGEMM(gh_pf_sgemm_q8_k, SQ8, 1, false)
+GH_SGEMM(gh_pf_sgateup_q8_k, SQ8, 2, false)
+GH_SGEMM(gh_pf_sgemm_bf16_k, SBf16, 1, false)
+GH_SGEMM(gh_pf_sgateup_bf16_k, SBf16, 2, false)
+GH_SGEMM(gh_pf_sgemm_q4_f_k, SQ4, 1, true)
+GH_SGEMM(gh_pf_sgateup_q4_f_k, SQ4, 2, true)
+GH_SGEMM(gh_pf_sgemm_q8_f_k, SQ8, 1, true)
+GH_SGEMM(gh_pf_sgateup_q8_f_k, SQ8, 2, true)
+GH_SGEMM(gh_pf_sgemm_bf16_f_k, SBf16, 1, true)
+GH_SGEMM(gh_pf_sgateup_bf16_f_k, SBf16, 2, true)
 
 // ---------------------------------------------------------------------------
 // Row-wise x prologue for T tokens (the batched form of the decode GEMVs'

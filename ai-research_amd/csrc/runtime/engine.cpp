@@ -384,11 +384,12 @@ namespace {
 // shapes (16 tokens, Q4: QKV 8192 x 3840 at RGW 2, o 3840 x 4096 at 1,
 // gate+up 2 x 15360 x 3840 and down 3840 x 15360 at 4); wider slices (24, 32)
 // and 2-4x the workgroups were slower.  GH_PF_STREAM="kr,rgw" forces both
-// (kr a multiple of 4).
+// (kr a multiple of 4, at most 32).  af: A is the f32 rows (Ax) and the
+// kernel splits each slice itself (gh_pf_*_f_k; rs unused).
 gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void* W0,
                                 const void* W1, const void* Ax, const float* rs, float* C,
                                 uint32_t T, uint32_t N, uint32_t K, const float** planes,
-                                uint32_t* nplanes) {
+                                uint32_t* nplanes, bool af) {
   const bool pair = W1 != nullptr;
   const uint32_t nmat = pair ? 2u : 1u;
   const uint32_t nb = K / 32, cus = (uint32_t)ctx->num_cus, rgs = (N + 15) / 16;
@@ -404,7 +405,7 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   RGW = std::max(1u, std::min(8u, RGW));
   if (const char* env = getenv("GH_PF_STREAM")) {
     unsigned kr = 0, rgw = 0;
-    if (sscanf(env, "%u,%u", &kr, &rgw) == 2 && kr >= 4 && kr % 4 == 0 &&
+    if (sscanf(env, "%u,%u", &kr, &rgw) == 2 && kr >= 4 && kr % 4 == 0 && kr <= 32 &&
         lds_of(std::min(kr, nb)) <= ctx->max_lds && rgw >= 1 && rgw <= 8) {
       KR = std::min(kr, nb);
       RGW = rgw;
@@ -416,7 +417,7 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   if (lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: stream slice exceeds LDS");
   const std::string name = std::string(pair ? "gh_pf_sgateup_" : "gh_pf_sgemm_") +
                            (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
-                           "_k";
+                           (af ? "_f_k" : "_k");
   float* out = C;
   if (nz > 1) {
     const size_t need = (size_t)nz * nmat * T * N * sizeof(float);
@@ -440,6 +441,14 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   void* rargs[] = {&out, &C, &T, &N, &nzz, const_cast<uint32_t*>(&nmat)};
   return ctx->launch("gh_pf_splitk_k", dim3(rgrid), dim3(256), 0, rargs);
 }
+
+// Short batches stream the weights (16-byte pieces of 4-block runs: K a
+// multiple of 128, rows 16-byte aligned).
+bool stream_ok(uint32_t T, uint32_t K, const void* W0, const void* W1) {
+  return T <= 16 && K % 128 == 0 &&
+         !((reinterpret_cast<uintptr_t>(W0) | reinterpret_cast<uintptr_t>(W1 ? W1 : W0)) & 15) &&
+         getenv("GH_PF_NO_STREAM") == nullptr;
+}
 }  // namespace
 
 gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const void* W0,
@@ -460,12 +469,8 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                 "(16-byte for bf16 rows)");
   const bool pair = W1 != nullptr;
   if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
-  // Short batches stream the weights (16-byte pieces of 4-block runs: K a
-  // multiple of 128, rows 16-byte aligned)
-  if (T <= 16 && K % 128 == 0 && !((reinterpret_cast<uintptr_t>(W0) |
-                                    reinterpret_cast<uintptr_t>(pair ? W1 : W0)) & 15) &&
-      getenv("GH_PF_NO_STREAM") == nullptr)
-    return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes);
+  if (stream_ok(T, K, W0, W1))
+    return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes, false);
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
   // products of at least 128 tokens) when splitting K lifts it to that
@@ -561,6 +566,10 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
   if (!W0 || (reinterpret_cast<uintptr_t>(W0) & walign) ||
       (W1 && (reinterpret_cast<uintptr_t>(W1) & walign)))
     return fail(GH_ERR_INVALID, "prefill GEMM: W null or misaligned (4 bytes; 16 for bf16 rows)");
+  if (W1 && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
+  // a short batch's streamed GEMM splits the f32 rows as it stages them
+  if (stream_ok(T, K, W0, W1))
+    return launch_prefill_stream(ctx, mode, W0, W1, A, nullptr, C, T, N, K, planes, nplanes, true);
   const size_t ax_bytes = (size_t)T * K * 4;  // 2 K halves per row
   gh_status st = ctx->ensure_zeroed(&ctx->half_scratch, &ctx->half_scratch_bytes,
                                     ax_bytes + (size_t)T * sizeof(float));

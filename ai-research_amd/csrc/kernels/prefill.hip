@@ -532,13 +532,18 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 // block scale per lane.
 //
 // A set is loaded as the decode streams load: lane l takes PB consecutive
-// blocks (16-byte loads) of row l / 4, so each row's SB blocks arrive as one
-// contiguous run.  (Loading each lane's MFMA fragment directly, one scale and
+// blocks (16-byte loads) of row l % 16, piece l / 16, so each row's SB blocks
+// arrive as one contiguous run.  (Loading each lane's MFMA fragment directly, one scale and
 // one word per block from 16 rows 2400 bytes apart, reads at about 1.3 TB/s
 // against 5.4-6.0 TB/s for these runs.)  The wave then writes the set to its
-// own LDS rows (padded so the fragment reads below fall on distinct banks)
-// and reads the fragments back; LDS keeps a wave's operations in order, so
-// no barrier is involved.
+// own LDS rows and reads the fragments back; LDS keeps a wave's operations in
+// order, so no barrier is involved.  Bank conflicts: each 16-lane phase of a
+// set write covers 16 rows (one piece), and the row strides (84, 148 and 132
+// dwords) are 4 x odd modulo the 64 banks, so those writes and the fragment
+// reads (16 rows, 4 lane groups) land on distinct banks.  (With lane l on
+// row l / 4 a phase held 4 rows x 4 pieces at bank 20 (row + piece); the
+// gate+up's conflict cycles fell by a quarter with this mapping, its time
+// did not move.)
 //
 // Workgroup (x, z) owns row groups [4 RGW x, 4 RGW (x + 1)) of 16 rows and
 // K blocks [z KR, z KR + KR) (KR and K / 32 multiples of 4): it stages that
@@ -643,15 +648,15 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   const uint8_t* al_row = pf_slice + min(li, T - 1) * stride + 16 * g;
 
   // Set c: row group j = c / kchunks, blocks kb0 .. kb0 + SB - 1 of the
-  // slice.  Lane l loads blocks kb0 + PB (l % 4) .. + PB - 1 of row l / 4
+  // slice.  Lane l loads blocks kb0 + PB (l / 16) .. + PB - 1 of row l % 16
   // (a piece that starts past the slice loads its last piece instead; those
   // blocks are skipped).
   u32x4 ra[NMAT][NV], rb[NMAT][NV];
   auto load = [&](uint32_t c, u32x4(&r)[NMAT][NV]) {
     const uint32_t j = c / kchunks, kb0 = (c % kchunks) * SB;
-    uint32_t row = (rg0 + 4 * j) * 16 + lane / 4;
+    uint32_t row = (rg0 + 4 * j) * 16 + li;
     row = row < N ? row : N - 1;
-    const uint32_t kb = min(kb0 + PB * (lane % 4), nk - PB);
+    const uint32_t kb = min(kb0 + PB * g, nk - PB);
     const size_t off = (size_t)row * row_bytes + (size_t)(b0 + kb) * F::kBlockBytes;
 #pragma unroll
     for (int i = 0; i < NV; i++) r[0][i] = *(gvec_ptr)(W0 + off + 16 * i);
@@ -740,13 +745,13 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
 
   auto compute = [&](uint32_t c, const u32x4(&r)[NMAT][NV]) {
     const uint32_t j = c / kchunks, kb0 = (c % kchunks) * SB;
-    // the set into this wave's LDS rows: lane l's piece at row l / 4
+    // the set into this wave's LDS rows: lane l's piece l / 16 of row l % 16
 #pragma unroll
     for (int q = 0; q < NMAT; q++)
 #pragma unroll
       for (int i = 0; i < NV; i++)
-        *reinterpret_cast<u32x4*>(wl + q * S::kWaveBytes + (lane / 4) * S::RS +
-                                  (lane % 4) * PB * F::kBlockBytes + 16 * i) = r[q][i];
+        *reinterpret_cast<u32x4*>(wl + q * S::kWaveBytes + li * S::RS + g * PB * F::kBlockBytes +
+                                  16 * i) = r[q][i];
 #pragma unroll
     for (int u = 0; u < SB; u++) {
       const uint32_t kb = kb0 + u;

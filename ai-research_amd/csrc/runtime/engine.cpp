@@ -398,7 +398,15 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   const uint32_t wave_bytes = 16u * (set_blocks * block_bytes + 16u);
   auto lds_of = [&](uint32_t kr) { return T * (128u * kr + 16u) + 4u * nmat * wave_bytes; };
   uint32_t KR = std::min(16u, nb);
-  // workgroups per CU that LDS allows (at most 2: a third measured no faster)
+  const std::string kname = std::string(pair ? "gh_pf_sgateup_" : "gh_pf_sgemm_") +
+                            (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
+                            (af ? "_f_k" : "_k");
+  // RGW: the grid sized for the workgroups LDS lets a CU hold, at most two.
+  // Sizing it for the 3-4 a CU could hold with a one-matrix set buffer
+  // (fewer row groups per wave, so shorter streams) measured slower: gate+up
+  // 46.3 against 36.0 us, QKV 20.4 against 16.1 (16 tokens, f32 input, plane
+  // sums included); and that buffer itself, at the same grid, 37.0 against
+  // 35.1 us for the gate+up.
   const uint32_t per_cu = std::max(1u, std::min(2u, (uint32_t)(ctx->max_lds / lds_of(KR))));
   const uint32_t slots = per_cu * cus, nz16 = (nb + KR - 1) / KR;
   uint32_t RGW = (uint32_t)(((uint64_t)rgs * nz16 + 2ull * slots) / (4ull * slots));  // rounded
@@ -415,9 +423,6 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   if (nz > 64) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: more than 64 K slices");
   const unsigned lds = lds_of(KR);
   if (lds > ctx->max_lds) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: stream slice exceeds LDS");
-  const std::string name = std::string(pair ? "gh_pf_sgateup_" : "gh_pf_sgemm_") +
-                           (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
-                           (af ? "_f_k" : "_k");
   float* out = C;
   if (nz > 1) {
     const size_t need = (size_t)nz * nmat * T * N * sizeof(float);
@@ -429,7 +434,7 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   void* args[] = {const_cast<void**>(&Ax), const_cast<float**>(&rs), const_cast<void**>(&W0),
                   const_cast<void**>(&W1a), &out, &T, &N, &K, &KR, &RGW};
   const dim3 grid((rgs + 4 * RGW - 1) / (4 * RGW), 1, nz);
-  gh_status st = ctx->launch(name, grid, dim3(256), lds, args);
+  gh_status st = ctx->launch(kname, grid, dim3(256), lds, args);
   if (planes) {
     *planes = nz > 1 ? out : C;
     *nplanes = nz;

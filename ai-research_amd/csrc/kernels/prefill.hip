@@ -511,7 +511,7 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 }
 
 // ---------------------------------------------------------------------------
-// Short batches (at most 16 tokens): the weight-streaming GEMM.
+// Short batches (at most 32 tokens): the weight-streaming GEMM.
 //
 // With a few tokens the tile GEMM above spends each K step on one barrier
 // and one load round trip for a tile that is mostly padding, and reads its
@@ -545,10 +545,10 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 // gate+up's conflict cycles fell by a quarter with this mapping, its time
 // did not move.)
 //
-// Workgroup (x, z) owns row groups [4 RGW x, 4 RGW (x + 1)) of 16 rows and
-// K blocks [z KR, z KR + KR) (KR and K / 32 multiples of 4): it stages that
-// slice of the T <= 16 activation rows in LDS once, and wave w then streams
-// row groups w, w + 4, ... with no further barrier.  gridDim.z > 1: plane z of
+// Workgroup (x, z) of NW waves owns row groups [NW RGW x, NW RGW (x + 1)) of
+// 16 rows and K blocks [z KR, z KR + KR) (KR and K / 32 multiples of 4): it
+// stages that slice of the T <= 16 TG activation rows in LDS once, and wave
+// w then streams row groups w, w + NW, ... with no further barrier.  gridDim.z > 1: plane z of
 // [Z][NMAT][T][N] takes the raw sums times the row scale, as the tile GEMM's
 // split form writes them; gridDim.z = 1: C takes the epilogue.
 //
@@ -622,7 +622,8 @@ struct SSet {
 
 #define PF_SLICE_MAX 32  // quant blocks per K slice (the AF staging holds 8 groups per thread)
 
-template <class F, int NMAT, bool AF>
+// NW waves per workgroup (NW * 64 threads), TG groups of 16 tokens (T <= 16 TG).
+template <class F, int NMAT, bool AF, int NW, int TG>
 __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
                                             const float* __restrict__ rs,
                                             const uint8_t* __restrict__ W0,
@@ -631,6 +632,7 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
                                             uint32_t K, uint32_t KR, uint32_t RGW) {
   using S = SSet<F>;
   constexpr int SB = S::SB, NV = S::NV, PB = F::kPB;
+  constexpr uint32_t NT = 64 * NW;
   extern __shared__ __attribute__((aligned(16))) uint8_t pf_slice[];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t g = lane >> 4, li = lane & 15;
@@ -640,12 +642,14 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   const size_t row_bytes = (size_t)nb * F::kBlockBytes;
   const uint32_t kchunks = (nk + SB - 1) / SB;  // sets per row group
   const uint32_t nchunks = RGW * kchunks;
-  const uint32_t rg0 = blockIdx.x * 4 * RGW + wave;  // row group j of this wave: rg0 + 4 j
+  const uint32_t rg0 = blockIdx.x * NW * RGW + wave;  // row group j of this wave: rg0 + NW j
   // this wave's set rows, after the T staged token rows
   uint8_t* wl = pf_slice + T * stride + wave * NMAT * S::kWaveBytes;
-  // token row of this lane's A fragments: tokens past T read token T - 1
-  // (their D rows are never stored)
-  const uint8_t* al_row = pf_slice + min(li, T - 1) * stride + 16 * g;
+  // token rows of this lane's A fragments (one per group of 16 tokens):
+  // tokens past T read token T - 1 (their D rows are never stored)
+  const uint8_t* al_row[TG];
+#pragma unroll
+  for (int h = 0; h < TG; h++) al_row[h] = pf_slice + min(16 * h + li, T - 1) * stride + 16 * g;
 
   // Set c: row group j = c / kchunks, blocks kb0 .. kb0 + SB - 1 of the
   // slice.  Lane l loads blocks kb0 + PB (l / 16) .. + PB - 1 of row l % 16
@@ -654,7 +658,7 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   u32x4 ra[NMAT][NV], rb[NMAT][NV];
   auto load = [&](uint32_t c, u32x4(&r)[NMAT][NV]) {
     const uint32_t j = c / kchunks, kb0 = (c % kchunks) * SB;
-    uint32_t row = (rg0 + 4 * j) * 16 + li;
+    uint32_t row = (rg0 + NW * j) * 16 + li;
     row = row < N ? row : N - 1;
     const uint32_t kb = min(kb0 + PB * g, nk - PB);
     const size_t off = (size_t)row * row_bytes + (size_t)(b0 + kb) * F::kBlockBytes;
@@ -668,10 +672,12 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
 
   // the first set is in flight while the slice is staged
   load(0, ra);
-  __shared__ float slice_scale[16];  // AF: each token's scale for this slice
+  __shared__ float slice_scale[16 * TG];  // AF: each token's scale for this slice
   if constexpr (AF) {
-    // 16 threads per token; thread `sub` takes 8-element groups sub, sub + 16,
-    // ... of the slice (nk / 4 of them: nk is a multiple of 4)
+    // 16 threads per token (NT / 16 >= 16 TG tokens); thread `sub` takes
+    // 8-element groups sub, sub + 16, ... of the slice (nk / 4 of them: nk
+    // is a multiple of 4)
+    static_assert(NT / 16 >= 16 * TG, "16 threads per staged token");
     const float* A = reinterpret_cast<const float*>(Ax);
     const uint32_t t = tid >> 4, sub = tid & 15, per = nk / 4;
     const bool on = t < T;
@@ -712,7 +718,7 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
     const uint32_t per_row = nk * 8;  // 16-byte chunks of one token's slice
     const uint32_t total = T * per_row;
 #pragma unroll 4
-    for (uint32_t c = tid; c < total; c += PF_NT) {
+    for (uint32_t c = tid; c < total; c += NT) {
       const uint32_t t = c / per_row, q = c % per_row;
       const u32x4 v = *reinterpret_cast<const u32x4*>(Ax + (size_t)t * 2 * K + (size_t)b0 * 64 + 8 * q);
       *reinterpret_cast<u32x4*>(pf_slice + t * stride + 16 * q) = v;
@@ -720,27 +726,32 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   }
   __syncthreads();
 
-  f32x4 acc[NMAT];
+  f32x4 acc[NMAT][TG];
 #pragma unroll
-  for (int q = 0; q < NMAT; q++) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < NMAT; q++)
+#pragma unroll
+    for (int h = 0; h < TG; h++) acc[q][h] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto epilogue = [&](uint32_t j) {
-    const uint32_t n = (rg0 + 4 * j) * 16 + li;
+    const uint32_t n = (rg0 + NW * j) * 16 + li;
     if (n >= N) return;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint32_t t = 4 * g + r;
-      if (t >= T) continue;
-      const float sr = AF ? slice_scale[t] : rs[t];
-      if (gridDim.z > 1) {
+    for (int h = 0; h < TG; h++)
 #pragma unroll
-        for (int q = 0; q < NMAT; q++) C[((size_t)(z * NMAT + q) * T + t) * N + n] = acc[q][r] * sr;
-      } else if constexpr (NMAT == 1) {
-        C[(size_t)t * N + n] = acc[0][r] * sr;
-      } else {
-        C[(size_t)t * N + n] = gelu_tanh(acc[0][r] * sr) * (acc[1][r] * sr);
+      for (int r = 0; r < 4; r++) {
+        const uint32_t t = 16 * h + 4 * g + r;
+        if (t >= T) continue;
+        const float sr = AF ? slice_scale[t] : rs[t];
+        if (gridDim.z > 1) {
+#pragma unroll
+          for (int q = 0; q < NMAT; q++)
+            C[((size_t)(z * NMAT + q) * T + t) * N + n] = acc[q][h][r] * sr;
+        } else if constexpr (NMAT == 1) {
+          C[(size_t)t * N + n] = acc[0][h][r] * sr;
+        } else {
+          C[(size_t)t * N + n] = gelu_tanh(acc[0][h][r] * sr) * (acc[1][h][r] * sr);
+        }
       }
-    }
   };
 
   auto compute = [&](uint32_t c, const u32x4(&r)[NMAT][NV]) {
@@ -756,25 +767,32 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
     for (int u = 0; u < SB; u++) {
       const uint32_t kb = kb0 + u;
       if (kb < nk) {  // uniform over the wave
-        const half8 ah = *reinterpret_cast<const half8*>(al_row + kb * 128);
-        const half8 al = *reinterpret_cast<const half8*>(al_row + kb * 128 + 64);
+        half8 ah[TG], al[TG];
+#pragma unroll
+        for (int h = 0; h < TG; h++) {
+          ah[h] = *reinterpret_cast<const half8*>(al_row[h] + kb * 128);
+          al[h] = *reinterpret_cast<const half8*>(al_row[h] + kb * 128 + 64);
+        }
 #pragma unroll
         for (int q = 0; q < NMAT; q++) {
           float d;
           const half8 b = F::frag(wl + q * S::kWaveBytes + li * S::RS, (uint32_t)u, g, &d);
-          if constexpr (F::kBf16) {
-            f32x4 t = acc[q];
-            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah),
-                                                        __builtin_bit_cast(bf16x8, b), t, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al),
-                                                        __builtin_bit_cast(bf16x8, b), t, 0, 0, 0);
-            acc[q] = t;
-          } else {
-            f32x4 blk = {0.f, 0.f, 0.f, 0.f};
-            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, blk, 0, 0, 0);
-            blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, blk, 0, 0, 0);
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[q][e] += d * blk[e];
+          for (int h = 0; h < TG; h++) {
+            if constexpr (F::kBf16) {
+              f32x4 t = acc[q][h];
+              t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ah[h]),
+                                                          __builtin_bit_cast(bf16x8, b), t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, al[h]),
+                                                          __builtin_bit_cast(bf16x8, b), t, 0, 0, 0);
+              acc[q][h] = t;
+            } else {
+              f32x4 blk = {0.f, 0.f, 0.f, 0.f};
+              blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[h], b, blk, 0, 0, 0);
+              blk = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[h], b, blk, 0, 0, 0);
+#pragma unroll
+              for (int e = 0; e < 4; e++) acc[q][h][e] += d * blk[e];
+            }
           }
         }
       }
@@ -782,7 +800,9 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
     if (c % kchunks == kchunks - 1) {  // the row group's last set
       epilogue(j);
 #pragma unroll
-      for (int q = 0; q < NMAT; q++) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < NMAT; q++)
+#pragma unroll
+        for (int h = 0; h < TG; h++) acc[q][h] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   };
 
@@ -796,24 +816,32 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   }
 }
 
+// 4-wave workgroups for up to 16 tokens; 8-wave workgroups for 17-32 tokens
+// (two token groups per wave sharing each weight fragment; the 32 staged
+// token rows serve 8 waves' row groups, which keeps 16-block slices in LDS).
 #define GH_SGEMM(NAME, F, NMAT, AF)                                                          \
-  extern "C" __global__ __launch_bounds__(PF_NT) void NAME(                                 \
+  extern "C" __global__ __launch_bounds__(256) void NAME##_k(                               \
       const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
       uint32_t T, uint32_t N, uint32_t K, uint32_t KR, uint32_t RGW) {                      \
-    stream_gemm<F, NMAT, AF>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                          \
+    stream_gemm<F, NMAT, AF, 4, 1>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                    \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(512) void NAME##_t2_k(                            \
+      const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
+      uint32_t T, uint32_t N, uint32_t K, uint32_t KR, uint32_t RGW) {                      \
+    stream_gemm<F, NMAT, AF, 8, 2>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                    \
   }
-GH_SGEMM(gh_pf_sgemm_q4_k, SQ4, 1, false)
-GH_SGEMM(gh_pf_sgateup_q4_k, SQ4, 2, false)
-GH_SGEMM(gh_pf_sgemm_q8_k, SQ8, 1, false)
-GH_SGEMM(gh_pf_sgateup_q8_k, SQ8, 2, false)
-GH_SGEMM(gh_pf_sgemm_bf16_k, SBf16, 1, false)
-GH_SGEMM(gh_pf_sgateup_bf16_k, SBf16, 2, false)
-GH_SGEMM(gh_pf_sgemm_q4_f_k, SQ4, 1, true)
-GH_SGEMM(gh_pf_sgateup_q4_f_k, SQ4, 2, true)
-GH_SGEMM(gh_pf_sgemm_q8_f_k, SQ8, 1, true)
-GH_SGEMM(gh_pf_sgateup_q8_f_k, SQ8, 2, true)
-GH_SGEMM(gh_pf_sgemm_bf16_f_k, SBf16, 1, true)
-GH_SGEMM(gh_pf_sgateup_bf16_f_k, SBf16, 2, true)
+GH_SGEMM(gh_pf_sgemm_q4, SQ4, 1, false)
+GH_SGEMM(gh_pf_sgateup_q4, SQ4, 2, false)
+GH_SGEMM(gh_pf_sgemm_q8, SQ8, 1, false)
+GH_SGEMM(gh_pf_sgateup_q8, SQ8, 2, false)
+GH_SGEMM(gh_pf_sgemm_bf16, SBf16, 1, false)
+GH_SGEMM(gh_pf_sgateup_bf16, SBf16, 2, false)
+GH_SGEMM(gh_pf_sgemm_q4_f, SQ4, 1, true)
+GH_SGEMM(gh_pf_sgateup_q4_f, SQ4, 2, true)
+GH_SGEMM(gh_pf_sgemm_q8_f, SQ8, 1, true)
+GH_SGEMM(gh_pf_sgateup_q8_f, SQ8, 2, true)
+GH_SGEMM(gh_pf_sgemm_bf16_f, SBf16, 1, true)
+GH_SGEMM(gh_pf_sgateup_bf16_f, SBf16, 2, true)
 
 // ---------------------------------------------------------------------------
 // Row-wise x prologue for T tokens (the batched form of the decode GEMVs'

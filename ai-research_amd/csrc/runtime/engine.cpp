@@ -386,6 +386,17 @@ namespace {
 // and 2-4x the workgroups were slower.  GH_PF_STREAM="kr,rgw" forces both
 // (kr a multiple of 4, at most 32).  af: A is the f32 rows (Ax) and the
 // kernel splits each slice itself (gh_pf_*_f_k; rs unused).
+// LDS of one workgroup of the streamed GEMM: T staged token rows of a
+// kr-block slice, and the set rows of each of its waves (4 waves for up to
+// 16 tokens, 8 for 17-32).
+uint32_t stream_lds(gh_quant_mode mode, bool pair, uint32_t T, uint32_t kr) {
+  const uint32_t block_bytes = mode == GH_QUANT_Q8 ? 36u : mode == GH_QUANT_NONE ? 64u : 20u;
+  const uint32_t set_blocks = mode == GH_QUANT_NONE ? 8u : 16u;
+  const uint32_t wave_bytes = 16u * (set_blocks * block_bytes + 16u);
+  const uint32_t nw = T <= 16 ? 4u : 8u;
+  return T * (128u * kr + 16u) + nw * (pair ? 2u : 1u) * wave_bytes;
+}
+
 gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void* W0,
                                 const void* W1, const void* Ax, const float* rs, float* C,
                                 uint32_t T, uint32_t N, uint32_t K, const float** planes,
@@ -393,14 +404,12 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   const bool pair = W1 != nullptr;
   const uint32_t nmat = pair ? 2u : 1u;
   const uint32_t nb = K / 32, cus = (uint32_t)ctx->num_cus, rgs = (N + 15) / 16;
-  const uint32_t block_bytes = mode == GH_QUANT_Q8 ? 36u : mode == GH_QUANT_NONE ? 64u : 20u;
-  const uint32_t set_blocks = mode == GH_QUANT_NONE ? 8u : 16u;
-  const uint32_t wave_bytes = 16u * (set_blocks * block_bytes + 16u);
-  auto lds_of = [&](uint32_t kr) { return T * (128u * kr + 16u) + 4u * nmat * wave_bytes; };
+  const uint32_t nw = T <= 16 ? 4u : 8u;  // waves per workgroup
+  auto lds_of = [&](uint32_t kr) { return stream_lds(mode, pair, T, kr); };
   uint32_t KR = std::min(16u, nb);
   const std::string kname = std::string(pair ? "gh_pf_sgateup_" : "gh_pf_sgemm_") +
                             (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
-                            (af ? "_f_k" : "_k");
+                            (af ? "_f" : "") + (nw == 8 ? "_t2_k" : "_k");
   // RGW: the grid sized for the workgroups LDS lets a CU hold, at most two.
   // Sizing it for the 3-4 a CU could hold with a one-matrix set buffer
   // (fewer row groups per wave, so shorter streams) measured slower: gate+up
@@ -409,7 +418,7 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   // 35.1 us for the gate+up.
   const uint32_t per_cu = std::max(1u, std::min(2u, (uint32_t)(ctx->max_lds / lds_of(KR))));
   const uint32_t slots = per_cu * cus, nz16 = (nb + KR - 1) / KR;
-  uint32_t RGW = (uint32_t)(((uint64_t)rgs * nz16 + 2ull * slots) / (4ull * slots));  // rounded
+  uint32_t RGW = (uint32_t)(((uint64_t)rgs * nz16 + (nw / 2) * slots) / (nw * (uint64_t)slots));
   RGW = std::max(1u, std::min(8u, RGW));
   if (const char* env = getenv("GH_PF_STREAM")) {
     unsigned kr = 0, rgw = 0;
@@ -433,8 +442,8 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   const void* W1a = pair ? W1 : W0;
   void* args[] = {const_cast<void**>(&Ax), const_cast<float**>(&rs), const_cast<void**>(&W0),
                   const_cast<void**>(&W1a), &out, &T, &N, &K, &KR, &RGW};
-  const dim3 grid((rgs + 4 * RGW - 1) / (4 * RGW), 1, nz);
-  gh_status st = ctx->launch(kname, grid, dim3(256), lds, args);
+  const dim3 grid((rgs + nw * RGW - 1) / (nw * RGW), 1, nz);
+  gh_status st = ctx->launch(kname, grid, dim3(64 * nw), lds, args);
   if (planes) {
     *planes = nz > 1 ? out : C;
     *nplanes = nz;
@@ -448,10 +457,13 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
 }
 
 // Short batches stream the weights (16-byte pieces of 4-block runs: K a
-// multiple of 128, rows 16-byte aligned).
-bool stream_ok(uint32_t T, uint32_t K, const void* W0, const void* W1) {
-  return T <= 16 && K % 128 == 0 &&
+// multiple of 128, rows 16-byte aligned): up to 16 tokens, and up to 32 when
+// the 8-wave workgroup's LDS fits (Q4 weights).
+bool stream_ok(const gh_context* ctx, gh_quant_mode mode, uint32_t T, uint32_t K, const void* W0,
+               const void* W1) {
+  return T <= 32 && K % 128 == 0 &&
          !((reinterpret_cast<uintptr_t>(W0) | reinterpret_cast<uintptr_t>(W1 ? W1 : W0)) & 15) &&
+         stream_lds(mode, W1 != nullptr, T, std::min(16u, K / 32)) <= ctx->max_lds &&
          getenv("GH_PF_NO_STREAM") == nullptr;
 }
 }  // namespace
@@ -474,7 +486,7 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
                                 "(16-byte for bf16 rows)");
   const bool pair = W1 != nullptr;
   if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
-  if (stream_ok(T, K, W0, W1))
+  if (stream_ok(ctx, mode, T, K, W0, W1))
     return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes, false);
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
@@ -573,7 +585,7 @@ gh_status launch_prefill_gemm(gh_context* ctx, gh_quant_mode mode, const void* W
     return fail(GH_ERR_INVALID, "prefill GEMM: W null or misaligned (4 bytes; 16 for bf16 rows)");
   if (W1 && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
   // a short batch's streamed GEMM splits the f32 rows as it stages them
-  if (stream_ok(T, K, W0, W1))
+  if (stream_ok(ctx, mode, T, K, W0, W1))
     return launch_prefill_stream(ctx, mode, W0, W1, A, nullptr, C, T, N, K, planes, nplanes, true);
   const size_t ax_bytes = (size_t)T * K * 4;  // 2 K halves per row
   gh_status st = ctx->ensure_zeroed(&ctx->half_scratch, &ctx->half_scratch_bytes,

@@ -1162,9 +1162,9 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   if (e == hipSuccess) e = hipMemcpyAsync(m->pf_meta, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(m->pf_active, act.data(), act.size() * 4, hipMemcpyHostToDevice, s);
   // Grouped attention: the matrix-core kernel when every layer has head_dim
-  // 256 and one G = nq / nkv dividing 16 (16 / G tokens per group), else the
-  // 4-token kernel when every layer has G <= 2 and head_dim <= 256, else the
-  // per-token kernel.  The union of a group's lists keeps the order of first
+  // 256 and one G = nq / nkv dividing 16 (16 / G tokens per group) and the
+  // batch has more than 64 tokens, else the 4-token kernel when every layer
+  // has G <= 2 and head_dim <= 256, else the per-token kernel.  The union of a group's lists keeps the order of first
   // appearance; a list that names one slot twice keeps the per-token kernel
   // (a union entry counts a slot once per token).
   uint32_t gkind = 0, gtok = 0;
@@ -1179,7 +1179,14 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
       small = small && G <= 2 && L.head_dim <= 256;
     }
     if (all256 && sameG && G0 >= 1 && G0 <= 16 && 16 % G0 == 0) {
-      gkind = 2;
+      // up to 64 tokens the per-token kernel (one workgroup per kv head and
+      // token) is as fast or faster: 12B shape, 16 / 32 / 64 tokens
+      // 5.66 / 6.65 / 9.95 ms against 5.83 / 6.83 / 10.05 ms; at 96 the two
+      // tie and at 128 the matrix-core kernel leads (14.67 against 14.70 ms).
+      // GH_PF_ATTN_MFMA=1 (read per call) takes the matrix-core kernel for
+      // any batch.
+      const char* fm = getenv("GH_PF_ATTN_MFMA");
+      if (T > 64 || (fm && fm[0] == '1')) gkind = 2;
       gtok = 16 / G0;
     } else if (small && nrows <= (1u << 24)) {
       gkind = 1;

@@ -317,17 +317,23 @@ def test_model_prefill_equals_per_token_path(gpu, T):
         b.close()
 
 
-@pytest.mark.parametrize("shape", ["12b", "tiny", "g4", "g1"])
-def test_model_prefill_windowed_lists(gpu, shape):
+@pytest.mark.parametrize("shape", ["12b", "tiny", "g4", "g1", "12b-pertoken"])
+def test_model_prefill_windowed_lists(gpu, monkeypatch, shape):
     # explicit lists with a sliding window (slot 0 as an anchor plus the last
     # 10 slots): within a token group the later tokens drop slots the earlier
     # ones still attend to, so the grouped attention's token masks decide which
     # union entries each token uses; checked against T per-token calls with the
     # same lists and against the oracle token by token, at 12B width (head_dim
-    # 256: the matrix-core kernel) and on the tiny model (head_dim 64/128: the
-    # 4-token vector-ALU kernel); g4 and g1
+    # 256: the matrix-core kernel, which batches of at most 64 tokens take only
+    # with GH_PF_ATTN_MFMA=1; "12b-pertoken" keeps the per-token kernel they
+    # take by default) and on the tiny model (head_dim 64/128: the 4-token
+    # vector-ALU kernel); g4 and g1
     # are head_dim-256 models with 4 and 1 query heads per kv head, so the
     # matrix-core kernel's 16 columns are 4 tokens x 4 heads and 16 tokens x 1
+    if shape in ("12b", "g4", "g1"):
+        monkeypatch.setenv("GH_PF_ATTN_MFMA", "1")
+    if shape == "12b-pertoken":
+        shape = "12b"
     if shape == "g4" or shape == "g1":
         cfg = gh.model_config(vocab=1024, hidden=1024, intermediate=2048, layers=1,
                               heads=8 if shape == "g4" else 4, kv_heads=2 if shape == "g4" else 4,
@@ -422,16 +428,20 @@ def test_model_prefill_staged_batch_matches_sequential_oracle(gpu, case):
         p.close()
 
 
+@pytest.mark.parametrize("mfma", [True, False])
 @pytest.mark.parametrize("T", [20, 30])
-def test_model_ring_prefill_staged_head_dim_256(gpu, T):
+def test_model_ring_prefill_staged_head_dim_256(gpu, monkeypatch, T, mfma):
     # Staged batches on the matrix-core grouped attention (head_dim 256, 16
     # query / 8 kv heads: 8 tokens per group, a K/V staging row named in the
-    # union lists): a ring of 4 anchors + 16 window + 4 recall slots, clocks
+    # union lists; forced by GH_PF_ATTN_MFMA=1 at these batch sizes) and on
+    # the per-token kernel: a ring of 4 anchors + 16 window + 4 recall slots, clocks
     # 0..19 token by token, then T tokens from clock 20 in one
     # gh_model_ring_prefill call, every one past the window's wrap.  T = 30
     # exceeds max_slots (24), so the batch runs as two staged chunks (24 + 6
     # tokens).  Checked against the oracle token by token and against the
     # GPU's per-token path: the last token's logits and every cache row.
+    if mfma:
+        monkeypatch.setenv("GH_PF_ATTN_MFMA", "1")
     cfg = gh.model_config(vocab=1024, hidden=512, intermediate=1024, layers=2, heads=16,
                           kv_heads=8, head_dim=256, max_slots=24, full_layers=(1,))
     m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=6)

@@ -490,14 +490,18 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
     return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes, false);
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
-  // products of at least 128 tokens) when splitting K lifts it to that
+  // products of more than 64 tokens) when splitting K lifts it to that
   const uint32_t bn_big = pair ? 64 : 128;
   const uint32_t tiles_big = ((N + bn_big - 1) / bn_big) * ((T + 127) / 128);
   // A caller that takes unsummed planes also gets the split for a product
   // whose large tiles give each CU only one workgroup (the QKV projection of
   // 512 tokens: 256 tiles of 128x128, split in 2, measured 85 us against
   // 112 us as 512 tiles of 128x64).
-  const bool big_split = !pair && T >= 128 && 4 * tiles_big >= cus &&
+  // From 65 tokens (one 128-row tile holds the batch): at 80 / 96 / 112 tokens
+  // the QKV projection's 64x64 tiles came to exactly the CU count or more and
+  // ran unsplit (86.6 us at 96 tokens against 32.4 us split at 128), and the
+  // prompt took 16.4-16.8 ms against 14.2-14.6 ms this way.
+  const bool big_split = !pair && T > 64 && 4 * tiles_big >= cus &&
                          (tiles_big < cus || (planes && tiles_big < 2 * cus)) &&
                          getenv("GH_PF_NO_BIG_SPLIT") == nullptr;
   const bool big = tiles_big >= cus || big_split;

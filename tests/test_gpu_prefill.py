@@ -29,9 +29,10 @@ def quantized(rows, cols, mode, seed):
 
 # (T, N, K): single row, ragged T and N, the 12B K, T past one 128-row tile,
 # and a long prompt's narrow product (128x128 tiles with K split 3 ways)
-# (512, 8192, 256): 256 tiles of 128x128, so the 128x64 tile runs (two per CU)
+# (512, 8192, 256): 256 tiles of 128x128, so the 128x64 tile runs (two per CU);
+# (96, 8192, 1024): one 128-row tile of 96 tokens, 64 tiles split 4 ways
 GEMM_SHAPES = [(1, 64, 128), (7, 96, 256), (64, 384, 3840), (130, 256, 512), (300, 128, 1024),
-               (512, 3840, 1024), (512, 8192, 256)]
+               (512, 3840, 1024), (512, 8192, 256), (96, 8192, 1024)]
 
 
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])

@@ -522,7 +522,8 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 // (the activation halves, as the tile GEMM reads them) and B = 32 K x 16
 // weight rows (one quant block of each row, exact integers), so one MFMA
 // pair (hi, lo) covers one block of 16 rows and the rows' block scales apply
-// to its results.
+// to its results.  With TG groups of 16 tokens each group is its own MFMA
+// pair on the same weight fragment.
 //
 // MFMA 16x16x32 operand layout: lane l holds A[l % 16][8 (l / 16) + e] and
 // B[8 (l / 16) + e][l % 16], e = 0..7; result register r of lane l is
@@ -532,10 +533,11 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 // block scale per lane.
 //
 // A set is loaded as the decode streams load: lane l takes PB consecutive
-// blocks (16-byte loads) of row l % 16, piece l / 16, so each row's SB blocks
-// arrive as one contiguous run.  (Loading each lane's MFMA fragment directly, one scale and
-// one word per block from 16 rows 2400 bytes apart, reads at about 1.3 TB/s
-// against 5.4-6.0 TB/s for these runs.)  The wave then writes the set to its
+// blocks (16-byte loads) of row l % 16, piece l / 16, so each row's SB
+// blocks arrive as one contiguous run.  (Loading each lane's MFMA fragment
+// directly, one scale and one word per block from 16 rows 2400 bytes apart,
+// reads at about 1.3 TB/s against 5.4-6.0 TB/s for these runs.)  The wave
+// then writes the set to its
 // own LDS rows and reads the fragments back; LDS keeps a wave's operations in
 // order, so no barrier is involved.  Bank conflicts: each 16-lane phase of a
 // set write covers 16 rows (one piece), and the row strides (84, 148 and 132
@@ -548,9 +550,10 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 // Workgroup (x, z) of NW waves owns row groups [NW RGW x, NW RGW (x + 1)) of
 // 16 rows and K blocks [z KR, z KR + KR) (KR and K / 32 multiples of 4): it
 // stages that slice of the T <= 16 TG activation rows in LDS once, and wave
-// w then streams row groups w, w + NW, ... with no further barrier.  gridDim.z > 1: plane z of
-// [Z][NMAT][T][N] takes the raw sums times the row scale, as the tile GEMM's
-// split form writes them; gridDim.z = 1: C takes the epilogue.
+// w then streams row groups w, w + NW, ... with no further barrier.
+// gridDim.z > 1: plane z of [Z][NMAT][T][N] takes the raw sums times the row
+// scale, as the tile GEMM's split form writes them; gridDim.z = 1: C takes
+// the epilogue.
 //
 // AF (the o and down inputs, and the kernel-level f32 entry points): A comes
 // as f32 rows, and the staging splits each token's slice itself, with a

@@ -394,6 +394,7 @@ GH_GEMM(gh_pf_gemm_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q4_m128_n128, Q4W, 128, 128, 1, true, _s)
 GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
+GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, 1, true, _s)  // 65-128 tokens
 GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
 
 // The row scale of the GEMM's A operand for a row whose largest |x| is m:

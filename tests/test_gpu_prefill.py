@@ -46,8 +46,11 @@ def test_prefill_gemm(gpu, mode, T, N, K):
     assert_close(got, np.asarray(a, np.float64) @ deq.T, what="prefill GEMM")
 
 
+# (100, 8192, 1024): Q4 takes the 128x64 pair tile with K split (64 tiles of one
+# 128-row tile, half the CU count or more)
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
-@pytest.mark.parametrize("T,N,K", [(1, 64, 128), (45, 192, 512), (256, 512, 3840)])
+@pytest.mark.parametrize("T,N,K", [(1, 64, 128), (45, 192, 512), (256, 512, 3840),
+                                   (100, 8192, 1024)])
 def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     gq, gdeq = quantized(N, K, mode, 310)
     uq, udeq = quantized(N, K, mode, 311)

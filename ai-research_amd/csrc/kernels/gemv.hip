@@ -1049,10 +1049,17 @@ constexpr bool interleaved(long) { return false; }
 // item.  Teams with no rows skip the stream but still take part in the
 // block-wide prologue and epilogue.
 // ------------------------------------------------------------------------
-// The prologue of a stream and its first weight loads (issue()).
+// The prologue of a stream and its first weight loads (issue()).  run
+// non-null (a gated layer's stream): the layer's run flag, read at entry and
+// tested once the first loads are in flight, before the prologue writes
+// anything to global memory; returns false when the layer is gated off
+// (every thread of the workgroup reads the same flag).  Testing it at entry
+// instead made every gated launch wait for the flag before its first load.
 template <int NT, int PRO, class Issue>
-__device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* xs, float* bsum,
-                                             float* ext, Issue issue) {
+__device__ __forceinline__ bool stream_start(const XPro& xp, uint32_t K, float* xs, float* bsum,
+                                             float* ext, Issue issue,
+                                             const uint32_t* run = nullptr) {
+  const uint32_t go = run ? *run : 1u;
   // A wave's loads complete in order, so x loads issued behind its own
   // weight loads would wait for them (barriers do not wait for outstanding
   // loads).  Every thread therefore issues its prologue loads (x, and for
@@ -1067,6 +1074,7 @@ __device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* 
     ProIn pin;
     pro_load<NT>(xp, K, pin);
     issue();
+    if (go == 0u) return false;
     pro_finish<NT>(xp, K, pin, xs, bsum, ext);
   } else if (K <= PRO_U * 4 * NT) {
     // x first: every thread issues its slices of x, then its first weight
@@ -1077,6 +1085,7 @@ __device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* 
     x_only.mode = 0;
     pro_load<NT>(x_only, K, pin);
     issue();
+    if (go == 0u) return false;
     pro_finish<NT>(x_only, K, pin, xs, bsum, ext);
   } else {
     // longer x than the registers hold: the first NS threads stage x while
@@ -1087,12 +1096,14 @@ __device__ __forceinline__ void stream_start(const XPro& xp, uint32_t K, float* 
     if (late) stage_x<NS>(xp.x, K, xs, bsum);
     __syncthreads();
     if (late) issue();
+    if (go == 0u) return false;
   }
+  return true;
 }
 
 template <class F, int TPR, int GPL, int D, int NT, int PRO>
 __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPro& xp, uint32_t M,
-                                            uint32_t K) {
+                                            uint32_t K, const uint32_t* run) {
   extern __shared__ float lds[];
   const uint32_t nb = K >> 5, ng = nb >> 2;
   float* xs = lds;
@@ -1134,7 +1145,7 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
   // overlaps the first weight loads, yet they measured slower (15360 x 3840
   // gate+up 15.5 against 15.2 us, decode 370 against 372.5 tok/s).
   typename F::Item buf[D];
-  stream_start<NT, PRO>(xp, K, xs, bsum, ext, [&]() {
+  if (!stream_start<NT, PRO>(xp, K, xs, bsum, ext, [&]() {
 #pragma unroll
     for (int d = 0; d < D; d++) {
       if constexpr (PRO != 0) {
@@ -1143,7 +1154,8 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
         F::load(buf[d], a, offset_in(d));
       }
     }
-  });
+  }, run))
+    return;
   typename F::Acc acc;
   F::init(acc);
 #pragma unroll 1
@@ -1174,7 +1186,7 @@ __device__ __forceinline__ void stream_rows(const typename F::Args& a, const XPr
 // ------------------------------------------------------------------------
 template <class F, int TPR, int GPL, int D, int NT, int PRO>
 __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const XPro& xp,
-                                               uint32_t M, uint32_t K) {
+                                               uint32_t M, uint32_t K, const uint32_t* run) {
   extern __shared__ float lds[];
   const uint32_t nb = K >> 5, ng = nb >> 2, nch = K >> 3;
   float* xs = lds;
@@ -1190,7 +1202,7 @@ __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const 
   auto c0_of = [&](uint32_t i) -> uint32_t { return (i % GPL) * C * TPR + lr; };
   typename F::Item buf[D];
   // first items: unconditional in the plain streams, as in stream_rows
-  stream_start<NT, PRO>(xp, K, xs, bsum, ext, [&]() {
+  if (!stream_start<NT, PRO>(xp, K, xs, bsum, ext, [&]() {
 #pragma unroll
     for (int d = 0; d < D; d++) {
       if constexpr (PRO != 0) {
@@ -1200,7 +1212,8 @@ __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const 
         F::template load<TPR>(buf[d], a, r * row_bytes, c0_of(d), nch);
       }
     }
-  });
+  }, run))
+    return;
   typename F::Acc acc;
   F::init(acc);
 #pragma unroll 1
@@ -1224,11 +1237,11 @@ __device__ __forceinline__ void stream_rows_il(const typename F::Args& a, const 
 
 template <class F, int TPR, int GPL, int D, int NT, int PRO>
 __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp, uint32_t M,
-                                       uint32_t K) {
+                                       uint32_t K, const uint32_t* run = nullptr) {
   if constexpr (interleaved<F>(0))
-    stream_rows_il<F, TPR, GPL, D, NT, PRO>(a, xp, M, K);
+    stream_rows_il<F, TPR, GPL, D, NT, PRO>(a, xp, M, K, run);
   else
-    stream_rows<F, TPR, GPL, D, NT, PRO>(a, xp, M, K);
+    stream_rows<F, TPR, GPL, D, NT, PRO>(a, xp, M, K, run);
 }
 
 // Kernel names: gh_<family>[n|g]_t<TPR>_g<GPL>_d<D>; the "n" variants carry
@@ -1239,9 +1252,10 @@ __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp
 // parameter they lose the kernel-argument address-space and alignment facts,
 // and the stream then needs ~100 more VGPRs (220 vs 126 for the Q4 d3 form).
 // Gated forms (suffix _q): the decode graph's gated layers (quiescence on)
-// launch these; they take the layer's run flag and do nothing when it is 0.
-// The ungated kernels carry no gating code at all: even a null-pointer test
-// at entry measured +0.3 us per launch.
+// launch these; they take the layer's run flag and do nothing when it is 0
+// (tested once their first loads are in flight, stream_start).  The ungated
+// kernels carry no gating code at all: even a null-pointer test at entry
+// measured +0.3 us per launch.
 #define GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, NT, SUFFIX)        \
   extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX(     \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K) {                               \
@@ -1251,8 +1265,7 @@ __device__ __forceinline__ void stream(const typename F::Args& a, const XPro& xp
   GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, NT, SUFFIX)              \
   extern "C" __global__ __launch_bounds__(NT) void NAME##_t##T##_g##G##_d##D##SUFFIX##_q( \
       GH_UNPAREN PARAMS, XPro xp, uint32_t M, uint32_t K, const uint32_t* run) {          \
-    if (*run == 0u) return;                                                               \
-    stream<FMT, T, G, D, NT, PRO>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K);               \
+    stream<FMT, T, G, D, NT, PRO>(FMT::Args{GH_UNPAREN ARGS}, xp, M, K, run);          \
   }
 #define GH_STREAM_KERNEL(NAME, FMT, PARAMS, ARGS, T, G, D, PRO) \
   GH_STREAM_KERNEL_NT(NAME, FMT, PARAMS, ARGS, T, G, D, PRO, 256, )

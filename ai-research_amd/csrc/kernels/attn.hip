@@ -432,7 +432,10 @@ struct DecodeSmem {
 
 // DENSE: the list is 0 .. S-1 (step flags bit 1) and is not read.  The two
 // forms are separate straight-line bodies, so no load sits under a branch.
-template <int DPL, int T, bool DENSE>
+// GATED: a gated layer's form; it loads the run flag at entry and tests it
+// just before its first global write, so the flag's latency hides under the
+// prologue and first-tile loads (all of which stay in bounds either way).
+template <int DPL, int T, bool DENSE, bool GATED>
 __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
   auto& qs = sm.qs;
   auto& knew = sm.knew;
@@ -449,6 +452,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
   const uint32_t kvh = blockIdx.x / nsplit, split = blockIdx.x % nsplit;
   const uint32_t clock = a.step[0], cur_slot = a.step[1], S = a.step[2];
   const bool fuse = a.fuse != 0;
+  const uint32_t go = GATED ? *a.run : 1u;
   // the splits that run: about ATT_SLOTS_PER_SPLIT active slots each
   const uint32_t live = attn_live_splits(nsplit, S);
   if (split >= live) return;  // uniform over the workgroup
@@ -542,6 +546,7 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
   if (fuse)
     for (uint32_t g = wave; g < G + 1; g += ATT_WAVES) rope_lds(g < G ? qs[g] : knew, a.rot, rc, rs, lane);
   __syncthreads();
+  if (GATED && go == 0u) return;  // a gated-off layer: uniform, nothing written yet
   if (fuse && split == 0) {  // ring_buffer.writeKV for this layer
     float* kc = a.k_cache + (size_t)cur_slot * kv_dim + (size_t)kvh * D;
     float* vc = a.v_cache + (size_t)cur_slot * kv_dim + (size_t)kvh * D;
@@ -648,13 +653,13 @@ __device__ __forceinline__ void attn_decode(const AttnArgs& a, DecodeSmem& sm) {
   }
 }
 
-template <int DPL, int T>
+template <int DPL, int T, bool GATED = false>
 __device__ __forceinline__ void attn_decode_k(const AttnArgs& a) {
   __shared__ DecodeSmem sm;
   if (a.flags != nullptr && (*a.flags & 2u) != 0u)
-    attn_decode<DPL, T, true>(a, sm);
+    attn_decode<DPL, T, true, GATED>(a, sm);
   else
-    attn_decode<DPL, T, false>(a, sm);
+    attn_decode<DPL, T, false, GATED>(a, sm);
 }
 
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d1_k(AttnArgs a) { attn_decode_k<1, 8>(a); }
@@ -664,8 +669,7 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { 
 // gated layers (quiescence on): nothing when the layer's run flag is 0
 #define GH_ATTN_GATED(DPL, T)                                                                   \
   extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d##DPL##_q_k(AttnArgs a) {       \
-    if (*a.run == 0u) return;                                                                   \
-    attn_decode_k<DPL, T>(a);                                                                   \
+    attn_decode_k<DPL, T, true>(a);                                                             \
   }
 GH_ATTN_GATED(1, 8) GH_ATTN_GATED(2, 8) GH_ATTN_GATED(4, 8) GH_ATTN_GATED(8, 4)
 
@@ -980,12 +984,16 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_s_k(AttnArg
 // indices, so the kernel costs one L2 round trip; only the weights wait for
 // the block-wide max.  The four waves' sums combine in wave order through LDS.
 #define MERGE_U 8
+// GATED: as in attn_decode, the run flag is loaded at entry and tested just
+// before the output row is written.
+template <bool GATED>
 __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   __shared__ float c[MAX_SPLIT];
   __shared__ float red[ATT_WAVES];
   __shared__ float4 acc[ATT_WAVES][MAX_D / 4];
   const uint32_t D = a.D, G = a.nq / a.nkv, h = blockIdx.x, tid = threadIdx.x;
   const uint32_t lane = tid & 63, wave = tid >> 6;
+  const uint32_t go = GATED ? *a.run : 1u;
   const uint32_t kvh = h / G, g = h % G, PS = D + 4;
   const uint32_t ns = attn_live_splits(a.nsplit, a.step[2]);  // the splits that ran
   const float* allp = a.part + (size_t)kvh * a.nsplit * G * PS + (size_t)g * PS;
@@ -1055,6 +1063,7 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
     acc[wave][col] = O;
   }
   __syncthreads();
+  if (GATED && go == 0u) return;  // a gated-off layer
   for (uint32_t col = tid; col < D4; col += ATT_NT) {
     const float4 a0 = acc[0][col], a1 = acc[1][col], a2 = acc[2][col], a3 = acc[3][col];
     float4 r;
@@ -1066,11 +1075,8 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) { attn_merge(a); }
-extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_q_k(AttnArgs a) {
-  if (*a.run == 0u) return;  // a gated-off layer
-  attn_merge(a);
-}
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) { attn_merge<false>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_q_k(AttnArgs a) { attn_merge<true>(a); }
 
 // ---------------------------------------------------------------------------
 // Matrix-core batched prefill attention, head_dim 256, fp32 throughout.

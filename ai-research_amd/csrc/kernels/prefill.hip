@@ -892,11 +892,13 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return t;
 }
 
-extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
-    float* X, const float* R, const float* wr, const float* w, _Float16* Xa,
-    float* rs, uint32_t H, float s, float eps, uint32_t mode, uint32_t perm, uint32_t rz) {
-  __shared__ float red[PF_NORM_NT / 64];
-  // thread t owns the 8-element group t of the row (H <= 8 * PF_NORM_NT)
+template <int NT>
+__device__ __forceinline__ void pf_norm_row(float* X, const float* R, const float* wr,
+                                            const float* w, _Float16* Xa, float* rs, uint32_t H,
+                                            float s, float eps, uint32_t mode, uint32_t perm,
+                                            uint32_t rz) {
+  __shared__ float red[NT / 64];
+  // thread t owns the 8-element group t of the row (H <= 8 * NT)
   const uint32_t t = blockIdx.x, tid = threadIdx.x, n8 = H / 8;
   const bool add = mode == 2, has_wr = wr != nullptr, act = tid < n8;
   const uint32_t e0 = 8 * (act ? tid : n8 - 1);
@@ -933,7 +935,7 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
 #pragma unroll
     for (int k = 0; k < 8; k++) ss += rv[k] * rv[k];
     ss = act ? ss : 0.f;
-    const float inv_r = has_wr ? 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps) : 1.0f;
+    const float inv_r = has_wr ? 1.0f / sqrtf(block_sum<NT>(ss, red) / (float)H + eps) : 1.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
       const float rr = has_wr ? rv[k] * inv_r * wrv[k] : rv[k];
@@ -948,7 +950,7 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
 #pragma unroll
   for (int k = 0; k < 8; k++) ss += v[k] * v[k];
   ss = act ? ss : 0.f;
-  const float inv = 1.0f / sqrtf(block_sum<PF_NORM_NT>(ss, red) / (float)H + eps);
+  const float inv = 1.0f / sqrtf(block_sum<NT>(ss, red) / (float)H + eps);
   float m = 0.f;
 #pragma unroll
   for (int k = 0; k < 8; k++) {
@@ -956,7 +958,7 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     m = fmaxf(m, fabsf(v[k]));
   }
   float sinv;
-  const float sc = row_scale(block_max<PF_NORM_NT>(act ? m : 0.f, red), &sinv);
+  const float sc = row_scale(block_max<NT>(act ? m : 0.f, red), &sinv);
   if (act) {
     float y[8];
 #pragma unroll
@@ -964,4 +966,18 @@ extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
     pf_store_group(y, perm, Xa + (size_t)t * 2 * H + pf_ax_pos(e0, false));
   }
   if (tid == 0) rs[t] = sc;
+}
+
+// 1024 threads for rows of up to 8192, 512 for rows of up to 4096 (the 12B
+// hidden 3840: 480 groups, so the 1024-thread form idles more than half its
+// threads and holds half as many rows per CU)
+extern "C" __global__ __launch_bounds__(PF_NORM_NT) void gh_pf_norm_k(
+    float* X, const float* R, const float* wr, const float* w, _Float16* Xa,
+    float* rs, uint32_t H, float s, float eps, uint32_t mode, uint32_t perm, uint32_t rz) {
+  pf_norm_row<PF_NORM_NT>(X, R, wr, w, Xa, rs, H, s, eps, mode, perm, rz);
+}
+extern "C" __global__ __launch_bounds__(512) void gh_pf_norm_512_k(
+    float* X, const float* R, const float* wr, const float* w, _Float16* Xa,
+    float* rs, uint32_t H, float s, float eps, uint32_t mode, uint32_t perm, uint32_t rz) {
+  pf_norm_row<512>(X, R, wr, w, Xa, rs, H, s, eps, mode, perm, rz);
 }

@@ -1377,7 +1377,10 @@ gh_status launch_pf_norm(gh_model* m, uint32_t T, const float* R, const float* w
   uint32_t perm = gh::pf_halves_format(m->mode);  // the GEMM's A-operand format
   void* args[] = {&X, const_cast<float**>(&R), const_cast<float**>(&wr), const_cast<float**>(&w),
                   &Xa, &rs, &H, &s, &eps, &mode, &perm, &rz};
-  return m->ctx->launch("gh_pf_norm_k", dim3(T), dim3(1024), 0, args);
+  // 512 threads for rows of up to 4096 (GH_PF_NORM_1024 keeps the 1024-thread form)
+  const bool narrow = H <= 8u * 512u && getenv("GH_PF_NORM_1024") == nullptr;
+  return m->ctx->launch(narrow ? "gh_pf_norm_512_k" : "gh_pf_norm_k", dim3(T),
+                        dim3(narrow ? 512 : 1024), 0, args);
 }
 
 gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {

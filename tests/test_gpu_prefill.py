@@ -292,6 +292,31 @@ def test_model_prefill_matches_sequential_oracle(gpu, monkeypatch, mode, T, dup,
         m.close()
 
 
+def test_model_prefill_norm_forms_bit_identical(gpu, monkeypatch):
+    # the row norm runs 512-thread workgroups for rows of up to 4096 and
+    # 1024-thread ones above; the extra waves only add zeros to the row sums,
+    # so GH_PF_NORM_1024 (the wide form on a narrow row) must change no bit
+    cfg = tiny_cfg()
+    m = gh.Model(gpu, cfg, mode=gh.QUANT_Q4, seed=13)
+    try:
+        tokens = np.random.default_rng(6).integers(0, cfg.vocab_size, 12)
+        xs = np.stack([m.embed(int(t)) for t in tokens])
+        out = []
+        for wide in (False, True):
+            if wide:
+                monkeypatch.setenv("GH_PF_NORM_1024", "1")
+            ring = gh.Ring(cfg.num_hidden_layers, 4, 16, 4)
+            slots, actives = ring_lists(ring, range(12))
+            tok = m.prefill(xs, np.arange(12), slots, actives, True)
+            out.append((tok, m.read(-1, gh.T_LOGITS, np.float32).copy(),
+                        m.read(0, gh.T_K_CACHE, np.float32).copy()))
+        assert out[0][0] == out[1][0]
+        assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+        assert np.array_equal(out[0][2].view(np.uint32), out[1][2].view(np.uint32))
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("T", [40, 37])
 def test_model_prefill_equals_per_token_path(gpu, T):
     # the batched prefill and T per-token calls leave the same caches (to

@@ -193,14 +193,16 @@ def test_prefill_stream_slices(gpu, monkeypatch, T, shape):
                  nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T), what="streamed GeGLU, slices %s" % shape)
 
 
+@pytest.mark.parametrize("N", [320, 203])
 @pytest.mark.parametrize("pair", [False, True])
 @pytest.mark.parametrize("split", ["1", "3", "200"])
-def test_prefill_split_k(gpu, monkeypatch, pair, split):
+def test_prefill_split_k(gpu, monkeypatch, pair, split, N):
     # a few tokens on the tile GEMM (the streaming form switched off): the
     # split-K forms (forced 1 = unsplit, 3 = an even split of 120 K steps,
     # 200 = clamped to the 64-split cap, so one or two K steps per split)
-    # against the product
-    T, N, K = 5, 320, 3840
+    # against the product; N = 203 leaves T N % 4 != 0, so the plane sum
+    # takes its one-output-per-thread form
+    T, K = 5, 3840
     monkeypatch.setenv("GH_PF_NO_STREAM", "1")
     monkeypatch.setenv("GH_PF_SPLIT", split)
     gq, gdeq = quantized(N, K, gh.QUANT_Q4, 320)

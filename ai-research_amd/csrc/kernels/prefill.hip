@@ -512,7 +512,7 @@ extern "C" __global__ __launch_bounds__(PF_NT) void gh_pf_splitk_k(const float* 
 }
 
 // ---------------------------------------------------------------------------
-// Short batches (at most 32 tokens): the weight-streaming GEMM.
+// Short batches (at most 48 tokens): the weight-streaming GEMM.
 //
 // With a few tokens the tile GEMM above spends each K step on one barrier
 // and one load round trip for a tile that is mostly padding, and reads its
@@ -678,45 +678,48 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
   load(0, ra);
   __shared__ float slice_scale[16 * TG];  // AF: each token's scale for this slice
   if constexpr (AF) {
-    // 16 threads per token (NT / 16 >= 16 TG tokens); thread `sub` takes
+    // 16 threads per token, NT / 16 tokens per pass; thread `sub` takes
     // 8-element groups sub, sub + 16, ... of the slice (nk / 4 of them: nk
     // is a multiple of 4)
-    static_assert(NT / 16 >= 16 * TG, "16 threads per staged token");
+    constexpr uint32_t TPP = NT / 16, PASSES = (16 * TG + TPP - 1) / TPP;
     const float* A = reinterpret_cast<const float*>(Ax);
-    const uint32_t t = tid >> 4, sub = tid & 15, per = nk / 4;
-    const bool on = t < T;
-    const float* src = A + (size_t)min(t, T - 1) * K + (size_t)b0 * 32;
-    float xv[PF_SLICE_MAX / 4][8];
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < PF_SLICE_MAX / 4; i++) {
-      if ((uint32_t)i < per) {
-        const float4 a = *reinterpret_cast<const float4*>(src + 8 * (sub + 16 * i));
-        const float4 b = *reinterpret_cast<const float4*>(src + 8 * (sub + 16 * i) + 4);
-        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
-        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
-#pragma unroll
-        for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(xv[i][k]));
-      }
-    }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    float inv;
-    const float sc = row_scale(m, &inv);
-    if (on) {
+#pragma unroll 1
+    for (uint32_t pass = 0; pass < PASSES; pass++) {
+      const uint32_t t = (tid >> 4) + pass * TPP, sub = tid & 15, per = nk / 4;
+      const bool on = t < T;
+      const float* src = A + (size_t)min(t, T - 1) * K + (size_t)b0 * 32;
+      float xv[PF_SLICE_MAX / 4][8];
+      float m = 0.f;
 #pragma unroll
       for (int i = 0; i < PF_SLICE_MAX / 4; i++) {
         if ((uint32_t)i < per) {
-          const uint32_t gi = sub + 16 * i;  // group gi: block gi / 4, part gi % 4
-          float y[8];
+          const float4 a = *reinterpret_cast<const float4*>(src + 8 * (sub + 16 * i));
+          const float4 b = *reinterpret_cast<const float4*>(src + 8 * (sub + 16 * i) + 4);
+          xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+          xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
 #pragma unroll
-          for (int k = 0; k < 8; k++) y[k] = xv[i][k] * inv;
-          pf_store_group(y, F::kFmt,
-                         reinterpret_cast<_Float16*>(pf_slice + t * stride + (gi >> 2) * 128 +
-                                                     (gi & 3) * 16));
+          for (int k = 0; k < 8; k++) m = fmaxf(m, fabsf(xv[i][k]));
         }
       }
-      if (sub == 0) slice_scale[t] = sc;
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      float inv;
+      const float sc = row_scale(m, &inv);
+      if (on) {
+#pragma unroll
+        for (int i = 0; i < PF_SLICE_MAX / 4; i++) {
+          if ((uint32_t)i < per) {
+            const uint32_t gi = sub + 16 * i;  // group gi: block gi / 4, part gi % 4
+            float y[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) y[k] = xv[i][k] * inv;
+            pf_store_group(y, F::kFmt,
+                           reinterpret_cast<_Float16*>(pf_slice + t * stride + (gi >> 2) * 128 +
+                                                       (gi & 3) * 16));
+          }
+        }
+        if (sub == 0) slice_scale[t] = sc;
+      }
     }
   } else {
     const uint32_t per_row = nk * 8;  // 16-byte chunks of one token's slice
@@ -822,7 +825,9 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
 
 // 4-wave workgroups for up to 16 tokens; 8-wave workgroups for 17-32 tokens
 // (two token groups per wave sharing each weight fragment; the 32 staged
-// token rows serve 8 waves' row groups, which keeps 16-block slices in LDS).
+// token rows serve 8 waves' row groups, which keeps 16-block slices in LDS)
+// and for 33-48 tokens (three groups per wave, narrower slices where LDS
+// needs them).
 #define GH_SGEMM(NAME, F, NMAT, AF)                                                          \
   extern "C" __global__ __launch_bounds__(256) void NAME##_k(                               \
       const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
@@ -833,6 +838,11 @@ __device__ __forceinline__ void stream_gemm(const _Float16* __restrict__ Ax,
       const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
       uint32_t T, uint32_t N, uint32_t K, uint32_t KR, uint32_t RGW) {                      \
     stream_gemm<F, NMAT, AF, 8, 2>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                    \
+  }                                                                                         \
+  extern "C" __global__ __launch_bounds__(512) void NAME##_t3_k(                            \
+      const _Float16* Ax, const float* rs, const uint8_t* W0, const uint8_t* W1, float* C,  \
+      uint32_t T, uint32_t N, uint32_t K, uint32_t KR, uint32_t RGW) {                      \
+    stream_gemm<F, NMAT, AF, 8, 3>(Ax, rs, W0, W1, C, T, N, K, KR, RGW);                    \
   }
 GH_SGEMM(gh_pf_sgemm_q4, SQ4, 1, false)
 GH_SGEMM(gh_pf_sgateup_q4, SQ4, 2, false)

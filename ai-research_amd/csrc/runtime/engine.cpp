@@ -387,14 +387,27 @@ namespace {
 // (kr a multiple of 4, at most 32).  af: A is the f32 rows (Ax) and the
 // kernel splits each slice itself (gh_pf_*_f_k; rs unused).
 // LDS of one workgroup of the streamed GEMM: T staged token rows of a
-// kr-block slice, and the set rows of each of its waves (4 waves for up to
-// 16 tokens, 8 for 17-32).
+// kr-block slice, then the set rows of each of its waves (4 waves for up to
+// 16 tokens, 8 for 17-48), plus 256 bytes for its static per-token slice
+// scales.
 uint32_t stream_lds(gh_quant_mode mode, bool pair, uint32_t T, uint32_t kr) {
   const uint32_t block_bytes = mode == GH_QUANT_Q8 ? 36u : mode == GH_QUANT_NONE ? 64u : 20u;
   const uint32_t set_blocks = mode == GH_QUANT_NONE ? 8u : 16u;
   const uint32_t wave_bytes = 16u * (set_blocks * block_bytes + 16u);
   const uint32_t nw = T <= 16 ? 4u : 8u;
-  return T * (128u * kr + 16u) + nw * (pair ? 2u : 1u) * wave_bytes;
+  return T * (128u * kr + 16u) + nw * (pair ? 2u : 1u) * wave_bytes + 256u;
+}
+
+// The streamed GEMM's slice width in quant blocks: 16 (or all of K); for
+// more than 32 tokens, else 12 or 8 if the staged rows fit in LDS then (and
+// the slices stay at 64 or fewer); 0 when none does.  Narrower slices multiply
+// the planes: the bf16 gate/up pair of 40 tokens in 4-block slices (30
+// planes) took the prompt from 9.9 to 14.7 ms.
+uint32_t stream_kr(const gh_context* ctx, gh_quant_mode mode, bool pair, uint32_t T, uint32_t nb) {
+  const uint32_t narrowest = T <= 32 ? std::min(16u, nb) : std::min(8u, nb);
+  for (uint32_t kr = std::min(16u, nb); kr >= narrowest; kr -= 4)
+    if (stream_lds(mode, pair, T, kr) <= ctx->max_lds && (nb + kr - 1) / kr <= 64) return kr;
+  return 0;
 }
 
 gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void* W0,
@@ -404,12 +417,14 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   const bool pair = W1 != nullptr;
   const uint32_t nmat = pair ? 2u : 1u;
   const uint32_t nb = K / 32, cus = (uint32_t)ctx->num_cus, rgs = (N + 15) / 16;
-  const uint32_t nw = T <= 16 ? 4u : 8u;  // waves per workgroup
+  // waves per workgroup; 16-token groups per wave
+  const uint32_t nw = T <= 16 ? 4u : 8u, tg = T <= 16 ? 1u : T <= 32 ? 2u : 3u;
   auto lds_of = [&](uint32_t kr) { return stream_lds(mode, pair, T, kr); };
-  uint32_t KR = std::min(16u, nb);
+  uint32_t KR = stream_kr(ctx, mode, pair, T, nb);
+  if (KR == 0) return fail(GH_ERR_UNSUPPORTED, "prefill GEMM: stream slice exceeds LDS");
   const std::string kname = std::string(pair ? "gh_pf_sgateup_" : "gh_pf_sgemm_") +
                             (mode == GH_QUANT_Q8 ? "q8" : mode == GH_QUANT_NONE ? "bf16" : "q4") +
-                            (af ? "_f" : "") + (nw == 8 ? "_t2_k" : "_k");
+                            (af ? "_f" : "") + (tg == 3 ? "_t3_k" : tg == 2 ? "_t2_k" : "_k");
   // RGW: the grid sized for the workgroups LDS lets a CU hold, at most two.
   // Sizing it for the 3-4 a CU could hold with a one-matrix set buffer
   // (fewer row groups per wave, so shorter streams) measured slower: gate+up
@@ -443,7 +458,8 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
   void* args[] = {const_cast<void**>(&Ax), const_cast<float**>(&rs), const_cast<void**>(&W0),
                   const_cast<void**>(&W1a), &out, &T, &N, &K, &KR, &RGW};
   const dim3 grid((rgs + nw * RGW - 1) / (nw * RGW), 1, nz);
-  gh_status st = ctx->launch(kname, grid, dim3(64 * nw), lds, args);
+  // dynamic LDS: all of it but the static slice scales' share
+  gh_status st = ctx->launch(kname, grid, dim3(64 * nw), lds - 256u, args);
   if (planes) {
     *planes = nz > 1 ? out : C;
     *nplanes = nz;
@@ -457,13 +473,18 @@ gh_status launch_prefill_stream(gh_context* ctx, gh_quant_mode mode, const void*
 }
 
 // Short batches stream the weights (16-byte pieces of 4-block runs: K a
-// multiple of 128, rows 16-byte aligned): up to 16 tokens, and up to 32 when
-// the 8-wave workgroup's LDS fits (Q4 weights).
+// multiple of 128, rows 16-byte aligned): up to 16 tokens, and up to 48 (bf16
+// rows: 40) when the 8-wave workgroup's LDS fits (GH_PF_STREAM_MAX lowers the
+// limit).  Measured on the 12B shape against the tile GEMMs, prompts of
+// 33 / 40 / 48 tokens: Q4 9.3 / 9.4 / 9.5 -> 7.2 / 7.9 / 8.0 ms, Q8 (33, 48)
+// 10.2 / 10.5 -> 8.4 / 9.4, bf16 9.5 / 9.6 / 9.9 -> 8.8 / 9.0 / 10.0.
 bool stream_ok(const gh_context* ctx, gh_quant_mode mode, uint32_t T, uint32_t K, const void* W0,
                const void* W1) {
-  return T <= 32 && K % 128 == 0 &&
+  uint32_t tmax = mode == GH_QUANT_NONE ? 40u : 48u;
+  if (const char* env = getenv("GH_PF_STREAM_MAX")) tmax = std::min(tmax, (uint32_t)atoi(env));
+  return T <= tmax && K % 128 == 0 &&
          !((reinterpret_cast<uintptr_t>(W0) | reinterpret_cast<uintptr_t>(W1 ? W1 : W0)) & 15) &&
-         stream_lds(mode, W1 != nullptr, T, std::min(16u, K / 32)) <= ctx->max_lds &&
+         stream_kr(ctx, mode, W1 != nullptr, T, K / 32) != 0 &&
          getenv("GH_PF_NO_STREAM") == nullptr;
 }
 }  // namespace

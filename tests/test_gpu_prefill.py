@@ -134,16 +134,16 @@ def test_prefill_gemm_weight_scale_range(gpu):
         assert_close(got[:, n], ref[:, n], what="prefill GEMM weight row %d" % n)
 
 
-# Batches of at most 32 tokens with K a multiple of 128 run the
+# Batches of at most 48 tokens with K a multiple of 128 run the
 # weight-streaming GEMM (16-token groups on the 16x16x32 MFMA; 8-wave
-# workgroups with two groups per wave from 17 tokens, where their LDS fits;
-# K in slices staged in LDS, the slices' planes added in order).  One token;
-# 16; 17 and 32; a ragged N; the 12B K values (3840, 4096, 15360); K of four
-# quant blocks (one slice, a partial weight set).  K = 160 and 33 tokens take
-# the tile GEMM.
+# workgroups with two groups per wave from 17 tokens and three from 33, where
+# their LDS fits; K in slices staged in LDS, the slices' planes added in
+# order).  One token; 16; 17 and 32; 33, 40, 45 and 48 (narrower slices); a
+# ragged N; the 12B K values (3840, 4096, 15360); K of four quant blocks (one
+# slice, a partial weight set).  K = 160 and 49 tokens take the tile GEMM.
 STREAM_SHAPES = [(1, 64, 128), (4, 100, 3840), (16, 256, 4096), (13, 96, 15360), (16, 48, 2048),
                  (9, 512, 128), (17, 96, 3840), (32, 200, 4096), (27, 64, 15360), (6, 40, 160),
-                 (33, 64, 256)]
+                 (33, 64, 256), (40, 96, 3840), (48, 200, 4096), (45, 64, 15360), (49, 64, 256)]
 
 
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
@@ -159,7 +159,8 @@ def test_prefill_stream_gemm(gpu, mode, T, N, K):
 
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 @pytest.mark.parametrize("T,N,K", [(3, 200, 3840), (16, 64, 1024), (11, 16, 15360),
-                                   (24, 300, 3840), (32, 48, 1024)])
+                                   (24, 300, 3840), (32, 48, 1024), (40, 300, 3840),
+                                   (48, 48, 1024)])
 def test_prefill_stream_gate_up(gpu, mode, T, N, K):
     gq, gdeq = quantized(N, K, mode, 370)
     uq, udeq = quantized(N, K, mode, 371)
@@ -171,13 +172,14 @@ def test_prefill_stream_gate_up(gpu, mode, T, N, K):
     assert_close(got, nr.gelu64(a64 @ gdeq.T) * (a64 @ udeq.T), what="streamed prefill GeGLU")
 
 
-@pytest.mark.parametrize("T", [7, 16, 29])
+@pytest.mark.parametrize("T", [7, 16, 29, 41])
 @pytest.mark.parametrize("shape", ["8,1", "16,2", "4,3", "4,8", "24,1", "32,2", "12,2"])
 def test_prefill_stream_slices(gpu, monkeypatch, T, shape):
     # forced slice widths (KR quant blocks: 32 blocks of K in 1, 2, 3, 4 or 8
     # slices; 24 and 12 leave an uneven last slice, and 12 and 4 a partial
     # weight set) and row groups per wave (8: waves whose rows all lie past N);
-    # at 29 tokens the widths whose LDS does not fit fall back to the default
+    # at 29 and 41 tokens the widths whose LDS does not fit fall back to the
+    # default
     T_, N, K = T, 300, 1024
     monkeypatch.setenv("GH_PF_STREAM", shape)
     gq, gdeq = quantized(N, K, gh.QUANT_Q4, 380)
@@ -319,7 +321,7 @@ def test_model_prefill_norm_forms_bit_identical(gpu, monkeypatch):
         m.close()
 
 
-@pytest.mark.parametrize("T", [40, 37])
+@pytest.mark.parametrize("T", [40, 37, 48])
 def test_model_prefill_equals_per_token_path(gpu, T):
     # the batched prefill and T per-token calls leave the same caches (to
     # tolerance) and pick the same final token on a 12B-width layer pair

@@ -1459,9 +1459,12 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
     {
       void* args[] = {&a, &clocks, &slots};
       // head_dim 256: one workgroup per token (angles once per wave), or for
-      // fewer tokens than CUs ceil(jobs / 8) per token; else one wavefront
-      // per (head, token)
-      const bool few = T < (uint32_t)ctx->num_cus;
+      // fewer tokens than twice the CUs ceil(jobs / 8) per token; else one
+      // wavefront per (head, token).  At 256 tokens the split form measured
+      // 20.39 -> 20.15 ms for the prompt, at 512 the same either way
+      // (GH_PF_ROPE4_S=0/1 forces one form).
+      const char* few_env = getenv("GH_PF_ROPE4_S");
+      const bool few = few_env ? atoi(few_env) != 0 : T < 2u * (uint32_t)ctx->num_cus;
       st = !rope4 ? ctx->launch("gh_pf_qkv_rope_k", dim3(a.nq + a.nkv, T), dim3(64), 0, args)
            : few  ? ctx->launch("gh_pf_qkv_rope4_s_k", dim3(T, (a.nq + 2 * a.nkv + 7) / 8),
                                 dim3(256), 0, args)

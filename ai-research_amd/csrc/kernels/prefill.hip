@@ -21,7 +21,9 @@
 //  * accumulation is fp32.
 //
 // Tiling: a workgroup of 256 threads (2 x 2 wavefronts) owns a BM x BN tile
-// of C; each wavefront a (BM/2) x (BN/2) sub-tile of 32 x 32 MFMA blocks.  K
+// of C; each wavefront a (BM/2) x (BN/2) sub-tile of 32 x 32 MFMA blocks (the
+// _w8 forms of the 128-row tiles: 512 threads, 4 x 2 wavefronts of
+// (BM/4) x (BN/2), so a CU's two tiles run four waves per SIMD).  K
 // advances one quant block (32) per step: the A slice (as hi and lo) and the
 // integer W slice with its scales go to LDS in unpadded, XOR-swizzled rows
 // (bank-conflict-free operand reads and stage writes).  Two LDS stages:
@@ -146,20 +148,25 @@ __device__ __forceinline__ uint32_t pf_ax_pos(uint32_t e, bool perm) {
 // [z S / Z, (z + 1) S / Z) and writes its raw sums to C as partial plane
 // (z, matrix) of [Z][NMAT][T][N]; gh_pf_splitk_k adds the planes in z order
 // and applies the epilogue.
-template <class F, int BM, int BN, int NMAT, int KB, bool SPLIT>
+// NW: waves per workgroup, 4 (2 x 2, each (BM/2) x (BN/2)) or 8 (4 x 2, each
+// (BM/4) x (BN/2)).
+template <class F, int BM, int BN, int NMAT, int KB, bool SPLIT, int NW = 4>
 __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
                                           const float* __restrict__ rs,
                                           const uint8_t* __restrict__ W0,
                                           const uint8_t* __restrict__ W1, float* __restrict__ C,
                                           uint32_t T, uint32_t N, uint32_t K) {
   static_assert(KB == 1, "one quant block per K step (the LDS swizzle assumes it)");
-  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave in M and N
+  static_assert(NW == 4 || NW == 8, "2 x 2 or 4 x 2 waves");
+  constexpr int NT = 64 * NW;
+  constexpr int TM = BM / (16 * NW), TN = BN / 64;  // 32x32 blocks per wave in M and N
+  static_assert(TM >= 1, "a wave holds at least one 32-row block");
   constexpr int A_CH = 8 * KB;                               // 16-B chunks per row and step
-  constexpr int A_PER = BM * A_CH / PF_NT;                   // 16-B chunks per thread
+  constexpr int A_PER = BM * A_CH / NT;                      // 16-B chunks per thread
   constexpr int B_ROWS = NMAT * BN;                          // weight rows per step
   constexpr int B_HALVES = 2 * KB * B_ROWS;                  // 16-element half-blocks
-  constexpr int B_PER = (B_HALVES + PF_NT - 1) / PF_NT;
-  static_assert(A_PER >= 1 && (BM * A_CH) % PF_NT == 0, "A chunks divide the workgroup");
+  constexpr int B_PER = (B_HALVES + NT - 1) / NT;
+  static_assert(A_PER >= 1 && (BM * A_CH) % NT == 0, "A chunks divide the workgroup");
   // Two LDS stages: the MFMAs of step s read one while step s+1 is stored
   // into the other, so a K step needs one barrier.  A row of a stage is 128 B
   // (8 chunks of 8 halves: hi 0-3, lo 4-7), a weight row 64 B (4 chunks), with
@@ -187,7 +194,7 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
   if (G % 8 == 0) w = (w % 8) * (G / 8) + w / 8;
   const uint32_t tn = w % gx, tm = (w / gx) % gy;
   const uint32_t m0 = tm * BM, n0 = tn * BN;
-  const uint32_t wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const uint32_t wm = (wave >> 1) * (BM / (NW / 2)), wn = (wave & 1) * (BN / 2);
   const uint32_t nb = K / 32, nsteps = (nb + KB - 1) / KB;
   const size_t row_bytes = (size_t)nb * F::kBlockBytes;
 
@@ -200,7 +207,7 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
     for (int i = 0; i < A_PER; i++) {
       // chunk c: row c / A_CH; q = c % A_CH -> block q / 8 of the step, plane
       // (q / 4) % 2, 8 halves at (q % 4) * 8
-      const uint32_t c = tid + i * PF_NT, q = c % A_CH;
+      const uint32_t c = tid + i * NT, q = c % A_CH;
       uint32_t r = m0 + c / A_CH;
       r = r < T ? r : T - 1;
       uint32_t blk = step * KB + q / 8;
@@ -209,7 +216,7 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
-      const uint32_t hb = tid + i * PF_NT;  // ((row * KB) + block) * 2 + half
+      const uint32_t hb = tid + i * NT;  // ((row * KB) + block) * 2 + half
       if (hb < (uint32_t)B_HALVES) {
         const uint32_t lr = hb / (2 * KB), kq = (hb / 2) % KB, mat = lr / BN;
         uint32_t r = n0 + lr % BN;
@@ -224,12 +231,12 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
   auto store_step = [&](int sb, uint32_t step) {
 #pragma unroll
     for (int i = 0; i < A_PER; i++) {
-      const uint32_t c = tid + i * PF_NT;
+      const uint32_t c = tid + i * NT;
       *reinterpret_cast<u32x4*>(&SA[sb][a_at(c / A_CH, c % A_CH)]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_PER; i++) {
-      const uint32_t hb = tid + i * PF_NT;
+      const uint32_t hb = tid + i * NT;
       if (hb < (uint32_t)B_HALVES) {
         const uint32_t lr = hb / (2 * KB), kq = (hb / 2) % KB;
         uint32_t v[8];
@@ -347,6 +354,19 @@ __device__ __forceinline__ void gemm_tile(const _Float16* __restrict__ Ax,
       uint32_t N, uint32_t K) {                                                            \
     gemm_tile<F, BM, BN, 1, KB, SPLIT>(Ax, rs, W, W, C, T, N, K);                          \
   }
+#define GH_GEMM_W8(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                    \
+  extern "C" __global__ __launch_bounds__(512) GH_PF_OCC_W8 void NAME##_k##KB##SUFFIX(     \
+      const _Float16* Ax, const float* rs, const uint8_t* W, float* C, uint32_t T,         \
+      uint32_t N, uint32_t K) {                                                            \
+    gemm_tile<F, BM, BN, 1, KB, SPLIT, 8>(Ax, rs, W, W, C, T, N, K);                       \
+  }
+#define GH_GEMM_PAIR_W8(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                               \
+  extern "C" __global__ __launch_bounds__(512) GH_PF_OCC_W8 void NAME##_k##KB##SUFFIX(     \
+      const _Float16* Ax, const float* rs, const uint8_t* Wg, const uint8_t* Wu,           \
+      float* Act, uint32_t T, uint32_t N, uint32_t K) {                                    \
+    gemm_tile<F, BM, BN, 2, KB, SPLIT, 8>(Ax, rs, Wg, Wu, Act, T, N, K);                   \
+  }
+#define GH_PF_OCC_W8 __attribute__((amdgpu_waves_per_eu(4, 4)))
 #define GH_GEMM_PAIR(NAME, F, BM, BN, KB, SPLIT, SUFFIX)                                  \
   extern "C" __global__ __launch_bounds__(PF_NT) GH_PF_OCC_##BM void NAME##_k##KB##SUFFIX( \
       const _Float16* Ax, const float* rs, const uint8_t* Wg, const uint8_t* Wu,           \
@@ -396,6 +416,17 @@ GH_GEMM(gh_pf_gemm_q8_m128_n128, Q8W, 128, 128, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q4_m64_n64, Q4W, 64, 64, 1, true, _s)
 GH_GEMM_PAIR(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, 1, true, _s)  // 65-128 tokens
 GH_GEMM_PAIR(gh_pf_gateup_q8_m64_n64, Q8W, 64, 64, 1, true, _s)
+
+// 8-wave forms of the 128-row tiles (names end in _w8)
+#define GH_GEMM_W8_FMT(FMT, F)                                                  \
+  GH_GEMM_W8(gh_pf_gemm_##FMT##_m128_n128, F, 128, 128, 1, false, _w8)          \
+  GH_GEMM_W8(gh_pf_gemm_##FMT##_m128_n64, F, 128, 64, 1, false, _w8)            \
+  GH_GEMM_W8(gh_pf_gemm_##FMT##_m128_n128, F, 128, 128, 1, true, _s_w8)         \
+  GH_GEMM_PAIR_W8(gh_pf_gateup_##FMT##_m128_n64, F, 128, 64, 1, false, _w8)
+GH_GEMM_W8_FMT(q4, Q4W)
+GH_GEMM_W8_FMT(q8, Q8W)
+GH_GEMM_W8_FMT(bf16, Bf16W)
+GH_GEMM_PAIR_W8(gh_pf_gateup_q4_m128_n64, Q4W, 128, 64, 1, true, _s_w8)
 
 // The row scale of the GEMM's A operand for a row whose largest |x| is m:
 // s = 2^(e - 14) with 2^(e-1) <= m < 2^e (1 for m = 0), so every |x| / s

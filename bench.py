@@ -601,9 +601,10 @@ def bench_decode(ctx, n_prompt=512, n_decode=128, cpu=False):
         wrapped[str(T)] = round(sorted(times)[1] * 1e3, 2)
     # short first-turn prompts (clocks from 0, after the run): 1-2 tokens go
     # token by token through the decode graphs, longer ones to the batched
-    # kernels; median of 3 calls each
+    # kernels (the weight-streaming GEMMs up to 48 tokens); median of 3 calls
+    # each
     short = {}
-    for T in (1, 2, 3, 4, 8, 16):
+    for T in (1, 2, 3, 4, 8, 16, 32, 48, 64):
         times = []
         for _ in range(3):
             t0 = time.perf_counter()

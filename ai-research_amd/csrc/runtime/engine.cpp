@@ -522,7 +522,13 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   // the QKV projection's 64x64 tiles came to exactly the CU count or more and
   // ran unsplit (86.6 us at 96 tokens against 32.4 us split at 128), and the
   // prompt took 16.4-16.8 ms against 14.2-14.6 ms this way.
-  const bool big_split = !pair && T > 64 && 4 * tiles_big >= cus &&
+  // With the 8-wave tiles this holds down to a handful of tiles: the o and
+  // down projections of 65-256 tokens (30-60 tiles, split up to 17 ways)
+  // measured 80 / 96 / 128 / 192-token prompts 12.30 / 12.56 / 13.08 / 19.19
+  // -> 11.17 / 11.43 / 11.95 / 17.07 ms against 64x64 tiles
+  // (GH_PF_BIG_SPLIT_MIN=n restores a minimum of n / 4 tiles).
+  const uint32_t bs_min = getenv("GH_PF_BIG_SPLIT_MIN") ? (uint32_t)atoi(getenv("GH_PF_BIG_SPLIT_MIN")) : 1u;
+  const bool big_split = !pair && T > 64 && 4 * tiles_big >= bs_min &&
                          (tiles_big < cus || (planes && tiles_big < 2 * cus)) &&
                          getenv("GH_PF_NO_BIG_SPLIT") == nullptr;
   // A Q4 gate/up pair whose 128x64 tiles give half the CUs or more but not

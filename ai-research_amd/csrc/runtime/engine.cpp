@@ -509,6 +509,21 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
   if (stream_ok(ctx, mode, T, K, W0, W1))
     return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes, false);
+  // A product without planes whose last 128-row tile would hold at most 48
+  // tokens past a multiple of 256 (a 288-token gate+up: 720 tiles, the last
+  // 240 three-quarters padding) runs as two products: the multiple of 256 on
+  // the tiles, the rest on the weight-streaming GEMM.
+  const uint32_t rest = T % 256;
+  if (!planes && T > 256 && rest > 0 && stream_ok(ctx, mode, rest, K, W0, W1) &&
+      getenv("GH_PF_NO_REST_SPLIT") == nullptr) {
+    const uint32_t main = T - rest;
+    gh_status st = launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, main, N, K, nullptr,
+                                             nullptr);
+    if (st != GH_OK) return st;
+    const uint16_t* Ar = static_cast<const uint16_t*>(Ax) + (size_t)main * 2 * K;  // fp16 halves
+    return launch_prefill_gemm_split(ctx, mode, W0, W1, Ar, rs + main, C + (size_t)main * N, rest,
+                                     N, K, nullptr, nullptr);
+  }
   const uint32_t cus = (uint32_t)ctx->num_cus;
   // the large tile when it still gives every CU a workgroup, or (plain
   // products of more than 64 tokens) when splitting K lifts it to that
@@ -573,14 +588,15 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
     grid.z = nz;
   }
   // 128-row tiles in 8-wave workgroups (four waves per SIMD instead of two,
-  // the same two tiles per CU), except a gate/up pair with more than two
+  // the same two tiles per CU), except a gate/up pair with more than three
   // unsplit tiles per CU (the 512-token gate+up: 317 -> 319 us Q4, 332 -> 337
-  // Q8, 304 -> 307 bf16).  Measured at the 12B shapes, bit-identical: 512
+  // Q8, 304 -> 307 bf16; 288-384-token prompts 1.3-1.9% faster with it, 448
+  // 0.3% slower).  Measured at the 12B shapes, bit-identical: 512
   // tokens QKV 116.9 -> 113.3 us, o 64.5 -> 60.5, down 169.2 -> 163.6 (Q4;
   // Q8 and bf16 alike), 96-300-token products 7-17% faster; prompts of 128 /
   // 256 / 512 tokens 13.15 / 19.96 / 31.87 -> 12.99 / 19.89 / 31.68 ms.
   // GH_PF_W8=0/1 forces one form.
-  bool w8 = big && !(pair && nz == 1 && tiles > 2 * cus);
+  bool w8 = big && !(pair && nz == 1 && tiles > 3 * cus);
   if (const char* env = getenv("GH_PF_W8")) w8 = big && atoi(env) != 0;
   if (w8) name += "_w8";
   gh_status st;

@@ -30,7 +30,8 @@ def quantized(rows, cols, mode, seed):
 # (T, N, K): single row, ragged T and N, the 12B K, T past one 128-row tile,
 # and a long prompt's narrow product (128x128 tiles with K split 3 ways)
 # (512, 8192, 256): 256 tiles of 128x128, so the 128x64 tile runs (two per CU);
-# (96, 8192, 1024): one 128-row tile of 96 tokens, 64 tiles split 4 ways
+# (96, 8192, 1024): one 128-row tile of 96 tokens, 64 tiles split 4 ways;
+# (300, 128, 1024): 256 tokens on the tiles, the last 44 streamed
 GEMM_SHAPES = [(1, 64, 128), (7, 96, 256), (64, 384, 3840), (130, 256, 512), (300, 128, 1024),
                (512, 3840, 1024), (512, 8192, 256), (96, 8192, 1024)]
 
@@ -47,10 +48,11 @@ def test_prefill_gemm(gpu, mode, T, N, K):
 
 
 # (100, 8192, 1024): Q4 takes the 128x64 pair tile with K split (64 tiles of one
-# 128-row tile, half the CU count or more)
+# 128-row tile, half the CU count or more); (288, 512, 1024) and (300, 192, 3840):
+# the first 256 tokens on the tiles, the rest on the weight-streaming GEMM
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 @pytest.mark.parametrize("T,N,K", [(1, 64, 128), (45, 192, 512), (256, 512, 3840),
-                                   (100, 8192, 1024)])
+                                   (100, 8192, 1024), (288, 512, 1024), (300, 192, 3840)])
 def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     gq, gdeq = quantized(N, K, mode, 310)
     uq, udeq = quantized(N, K, mode, 311)

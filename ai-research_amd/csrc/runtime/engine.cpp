@@ -509,12 +509,15 @@ gh_status launch_prefill_gemm_split(gh_context* ctx, gh_quant_mode mode, const v
   if (pair && planes) return fail(GH_ERR_INVALID, "prefill GEMM: unsummed planes of a gate/up pair");
   if (stream_ok(ctx, mode, T, K, W0, W1))
     return launch_prefill_stream(ctx, mode, W0, W1, Ax, rs, C, T, N, K, planes, nplanes, false);
-  // A product without planes whose last 128-row tile would hold at most 48
-  // tokens past a multiple of 256 (a 288-token gate+up: 720 tiles, the last
-  // 240 three-quarters padding) runs as two products: the multiple of 256 on
-  // the tiles, the rest on the weight-streaming GEMM.
+  // A product without planes of 256k + 1..127 tokens (a 288-token gate+up:
+  // 720 tiles, the last 240 three-quarters padding) runs as two products: the
+  // multiple of 256 on the tiles, the rest as its own product (the
+  // weight-streaming GEMM up to 48 tokens, tiles above).  Prompts of 272 /
+  // 288 / 300 / 320 / 352 tokens: 26.8 / 26.8 / 26.9 / 27.3 / 27.6 -> 23.3 /
+  // 23.9 / 24.6 / 25.1 / 26.6 ms (GH_PF_REST_MAX=n: at most n tokens).
   const uint32_t rest = T % 256;
-  if (!planes && T > 256 && rest > 0 && stream_ok(ctx, mode, rest, K, W0, W1) &&
+  const uint32_t rest_max = getenv("GH_PF_REST_MAX") ? (uint32_t)atoi(getenv("GH_PF_REST_MAX")) : 127u;
+  if (!planes && T > 256 && rest > 0 && rest <= rest_max &&
       getenv("GH_PF_NO_REST_SPLIT") == nullptr) {
     const uint32_t main = T - rest;
     gh_status st = launch_prefill_gemm_split(ctx, mode, W0, W1, Ax, rs, C, main, N, K, nullptr,

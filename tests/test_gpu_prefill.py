@@ -49,10 +49,12 @@ def test_prefill_gemm(gpu, mode, T, N, K):
 
 # (100, 8192, 1024): Q4 takes the 128x64 pair tile with K split (64 tiles of one
 # 128-row tile, half the CU count or more); (288, 512, 1024) and (300, 192, 3840):
-# the first 256 tokens on the tiles, the rest on the weight-streaming GEMM
+# the first 256 tokens on the tiles, the rest on the weight-streaming GEMM;
+# (352, 192, 1024): the rest of 96 tokens on the tiles
 @pytest.mark.parametrize("mode", [gh.QUANT_Q4, gh.QUANT_Q8, gh.QUANT_NONE])
 @pytest.mark.parametrize("T,N,K", [(1, 64, 128), (45, 192, 512), (256, 512, 3840),
-                                   (100, 8192, 1024), (288, 512, 1024), (300, 192, 3840)])
+                                   (100, 8192, 1024), (288, 512, 1024), (300, 192, 3840),
+                                   (352, 192, 1024)])
 def test_prefill_gate_up_geglu(gpu, mode, T, N, K):
     gq, gdeq = quantized(N, K, mode, 310)
     uq, udeq = quantized(N, K, mode, 311)

@@ -234,10 +234,11 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
   const uint32_t D = a.D, G = a.nq / a.nkv;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t kv_dim = (size_t)a.nkv * D;
-  // decode: one split of one token; prefill: all of token blockIdx.y's list
-  const uint32_t nsplit = PF ? 1u : a.nsplit;
-  const uint32_t kvh = PF ? blockIdx.x : blockIdx.x / nsplit;
-  const uint32_t split = PF ? 0u : blockIdx.x % nsplit;
+  // decode: one split of one token; prefill: one split of token blockIdx.y's
+  // list (nsplit 1: all of it, and the workgroup writes the output rows)
+  const uint32_t nsplit = a.nsplit;
+  const uint32_t kvh = blockIdx.x / nsplit;
+  const uint32_t split = blockIdx.x % nsplit;
   const uint32_t tok = PF ? blockIdx.y : 0u;
   const uint32_t clock = PF ? 0u : a.step[0], cur_slot = PF ? 0u : a.step[1];
   const uint32_t S = PF ? a.n_active[tok] : a.step[2];
@@ -373,7 +374,9 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
   }
   __syncthreads();
   const uint32_t PS = D + 4;  // partial record: o[D], m, l (+2 pad: float4 rows)
-  float* part = PF ? nullptr : a.part + ((size_t)kvh * nsplit + split) * G * PS;
+  // partials: [token][kv head][split][g] records (decode: token 0)
+  float* part = PF && nsplit == 1 ? nullptr
+                                  : a.part + (((size_t)tok * a.nkv + kvh) * nsplit + split) * G * PS;
   for (uint32_t i = tid; i < G * D; i += ATT_NT) {
     const uint32_t g = i / D, d = i % D;
     float M = -INFINITY;
@@ -384,7 +387,7 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a) {
       L += wl[w][g] * c;
       O += wo[w][g][d] * c;
     }
-    if constexpr (PF) {  // the whole list: the final output row of this token
+    if (PF && nsplit == 1) {  // the whole list: the final output row of this token
       a.out_rows[(size_t)tok * a.out_stride + (size_t)(kvh * G + g) * D + d] = L > 0.f ? O / L : 0.f;
     } else {
       part[g * PS + d] = O;
@@ -986,7 +989,9 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_qkv_rope4_s_k(AttnArg
 #define MERGE_U 8
 // GATED: as in attn_decode, the run flag is loaded at entry and tested just
 // before the output row is written.
-template <bool GATED>
+// PF: the batched prefill's split partials, one workgroup per (query head,
+// token blockIdx.y); all a.nsplit splits ran; the output row goes to out_rows.
+template <bool GATED, bool PF = false>
 __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   __shared__ float c[MAX_SPLIT];
   __shared__ float red[ATT_WAVES];
@@ -995,8 +1000,11 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
   const uint32_t lane = tid & 63, wave = tid >> 6;
   const uint32_t go = GATED ? *a.run : 1u;
   const uint32_t kvh = h / G, g = h % G, PS = D + 4;
-  const uint32_t ns = attn_live_splits(a.nsplit, a.step[2]);  // the splits that ran
-  const float* allp = a.part + (size_t)kvh * a.nsplit * G * PS + (size_t)g * PS;
+  const uint32_t tok = PF ? blockIdx.y : 0u;
+  // the splits that ran
+  const uint32_t ns = PF ? a.nsplit : attn_live_splits(a.nsplit, a.step[2]);
+  const float* allp =
+      a.part + ((size_t)tok * a.nkv + kvh) * a.nsplit * G * PS + (size_t)g * PS;
   const size_t stride = (size_t)G * PS;  // one split to the next
   const uint32_t D4 = D / 4;
   auto row = [&](uint32_t sp, uint32_t col) {  // clamped: out-of-range reads get weight 0
@@ -1071,12 +1079,16 @@ __device__ __forceinline__ void attn_merge(const AttnArgs& a) {
     r.y = ((a0.y + a1.y) + (a2.y + a3.y)) * inv;
     r.z = ((a0.z + a1.z) + (a2.z + a3.z)) * inv;
     r.w = ((a0.w + a1.w) + (a2.w + a3.w)) * inv;
-    *reinterpret_cast<float4*>(a.out + (size_t)h * D + col * 4) = r;
+    float* orow = PF ? a.out_rows + (size_t)tok * a.out_stride : a.out;
+    *reinterpret_cast<float4*>(orow + (size_t)h * D + col * 4) = r;
   }
 }
 
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_k(AttnArgs a) { attn_merge<false>(a); }
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_merge_q_k(AttnArgs a) { attn_merge<true>(a); }
+extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_merge_k(AttnArgs a) {
+  attn_merge<false, true>(a);
+}
 
 // ---------------------------------------------------------------------------
 // Matrix-core batched prefill attention, head_dim 256, fp32 throughout.

@@ -128,6 +128,7 @@ struct gh_model {
   uint32_t *pf_union = nullptr, *pf_ucount = nullptr, *pf_scatter = nullptr;
   uint32_t pf_ustride = 0, pf_gtok = 0;
   uint32_t pf_gkind = 0;  // this call: 0 per-token kernel, 1 gh_pf_attn_g_*, 2 gh_pf_attn_m_k
+  uint32_t pf_maxn = 0;   // this call: the longest active list of a token
 
   template <typename T>
   T* at(size_t off) const {
@@ -1055,6 +1056,7 @@ gh_status gh_model_prefill(gh_model* m, const float* x, uint32_t T, const uint64
   uint32_t max_n = 1;
   for (uint32_t t = 0; t < T; t++) max_n = std::max(max_n, n_active[t]);
   if (active_stride < max_n) return fail(GH_ERR_INVALID, "gh_model_prefill: active_stride < n_active");
+  m->pf_maxn = max_n;
   // Slot writers of this batch.  The batched kernels write every token's K/V
   // before any token attends, so they need each token to read only its own
   // and earlier tokens' slots, and no slot written twice.  A batch that
@@ -1490,7 +1492,28 @@ gh_status prefill_forward(gh_model* m, uint32_t T, bool want_logits) {
         const char* name = D <= 64 ? "gh_pf_attn_d1_k"
                            : D <= 128 ? "gh_pf_attn_d2_k"
                            : D <= 256 ? "gh_pf_attn_d4_k" : "gh_pf_attn_d8_k";
-        if ((st = ctx->launch(name, dim3(a.nkv, T), dim3(256), 0, args)) != GH_OK) return st;
+        // Long lists (a prompt after the window has wrapped) split each
+        // token's list over several workgroups, merged per (head, token) by
+        // gh_pf_attn_merge_k, up to about two workgroups per CU: with one
+        // workgroup per (kv head, token) a 16-token batch has 128, each
+        // walking ~540 slots.  Wrapped 16-token prompts: 7.24 ms unsplit,
+        // 6.23 / 6.37 / 6.75 ms at 4 / 8 / 16 splits; 64 tokens (512
+        // workgroups unsplit): 11.49 unsplit, 12.16 at 4 splits.
+        uint32_t ns = 1;
+        const uint32_t wgs = a.nkv * T, fill = (2u * (uint32_t)ctx->num_cus + wgs - 1) / wgs;
+        if (m->pf_maxn > 64) ns = std::min(std::min(16u, fill), (m->pf_maxn + 63) / 64);
+        if (const char* e = getenv("GH_PF_ATTN_SPLITS")) ns = std::max(1, std::min(16, atoi(e)));
+        a.nsplit = ns;
+        if (ns > 1) {
+          const size_t need = (size_t)T * a.nkv * ns * (a.nq / a.nkv) * (D + 4) * sizeof(float);
+          if ((st = ctx->ensure_zeroed(&ctx->attn_scratch, &ctx->attn_scratch_bytes, need)) != GH_OK)
+            return st;
+          a.part = static_cast<float*>(ctx->attn_scratch);
+        }
+        if ((st = ctx->launch(name, dim3(a.nkv * ns, T), dim3(256), 0, args)) != GH_OK) return st;
+        if (ns > 1 && (st = ctx->launch("gh_pf_attn_merge_k", dim3(a.nq, T), dim3(256), 0, args)) != GH_OK)
+          return st;
+        a.nsplit = 1;
       }
     }
     // 4. o = W_o . attn (a K split stays unsummed: the norm below adds the planes)

@@ -411,8 +411,14 @@ def test_model_prefill_windowed_lists(gpu, monkeypatch, shape):
         b.close()
 
 
+@pytest.mark.parametrize("splits", [None, "3", "16"])
 @pytest.mark.parametrize("case", ["slot twice", "reads a later write", "wrapped window"])
-def test_model_prefill_staged_batch_matches_sequential_oracle(gpu, case):
+def test_model_prefill_staged_batch_matches_sequential_oracle(gpu, monkeypatch, case, splits):
+    # splits: each token's list split over that many workgroups of the
+    # per-token attention (as long lists are), merged by gh_pf_attn_merge_k;
+    # 16 leaves some splits empty
+    if splits is not None:
+        monkeypatch.setenv("GH_PF_ATTN_SPLITS", splits)
     # batches whose order the batched kernels cannot keep by writing in place
     # (every token's K/V is written before any token attends): one slot
     # written twice, a token attending to the slot a later token overwrites,
@@ -465,9 +471,12 @@ def test_model_prefill_staged_batch_matches_sequential_oracle(gpu, case):
         p.close()
 
 
-@pytest.mark.parametrize("mfma", [True, False])
+@pytest.mark.parametrize("mfma,splits", [(True, None), (False, None), (False, "4")])
 @pytest.mark.parametrize("T", [20, 30])
-def test_model_ring_prefill_staged_head_dim_256(gpu, monkeypatch, T, mfma):
+def test_model_ring_prefill_staged_head_dim_256(gpu, monkeypatch, T, mfma, splits):
+    # splits "4": the per-token kernel with each list split 4 ways and merged
+    if splits is not None:
+        monkeypatch.setenv("GH_PF_ATTN_SPLITS", splits)
     # Staged batches on the matrix-core grouped attention (head_dim 256, 16
     # query / 8 kv heads: 8 tokens per group, a K/V staging row named in the
     # union lists; forced by GH_PF_ATTN_MFMA=1 at these batch sizes) and on

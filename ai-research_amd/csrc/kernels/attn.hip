@@ -25,7 +25,8 @@
 // (matrix cores, head_dim 256: 16 query columns of consecutive tokens per
 // workgroup over the union of their active lists), gh_pf_attn_g_d*_k (4
 // tokens per workgroup on the vector ALUs), gh_pf_attn_d*_k (one token per
-// workgroup, attn_split over its own list).
+// workgroup, attn_split over its own list, or over one of a.nsplit shares of
+// a long list, combined by gh_pf_attn_merge_k).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -676,8 +677,9 @@ extern "C" __global__ __launch_bounds__(ATT_NT) void gh_attn_d8_k(AttnArgs a) { 
   }
 GH_ATTN_GATED(1, 8) GH_ATTN_GATED(2, 8) GH_ATTN_GATED(4, 8) GH_ATTN_GATED(8, 4)
 
-// Batched prefill: grid (kv heads, tokens); each workgroup runs token
-// blockIdx.y's whole active list (q already normalised and roped by
+// Batched prefill: grid (kv heads x a.nsplit, tokens); each workgroup runs
+// token blockIdx.y's whole active list (a.nsplit 1), or one share of it whose
+// partials gh_pf_attn_merge_k combines (q already normalised and roped by
 // gh_pf_qkv_rope_k, this batch's K/V already in the caches).
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d1_k(AttnArgs a) { attn_split<1, 8, true>(a); }
 extern "C" __global__ __launch_bounds__(ATT_NT) void gh_pf_attn_d2_k(AttnArgs a) { attn_split<2, 8, true>(a); }

@@ -391,7 +391,9 @@ gh_status gh_dispatch_forward_token(gh_model *m, const float *x, int want_logits
  * it).  With layer gating on, a
  * last token with logits runs the gated decode graph after the others (see
  * gh_model_set_quiescence).  Otherwise the first call allocates the model's
- * prefill buffers for T tokens (not inside graph capture). */
+ * prefill buffers for T tokens, and a call that needs more of the context's
+ * scratch (split-K planes, split attention partials) grows it; so a prefill
+ * is not to be recorded inside graph capture. */
 gh_status gh_model_prefill(gh_model *m, const float *x, uint32_t T, const uint64_t *clocks,
                            const uint32_t *slot_idx, const uint32_t *active,
                            uint32_t active_stride, const uint32_t *n_active, int want_logits,
